@@ -1,0 +1,237 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X quantized weight x activation path.
+
+Prints ONE JSON line (the driver contract).  The headline workload is
+BASELINE.json configs[1], the Bonsai-1.7B ternary FFN decode step: gate and up
+matvecs (Q2_0, W 6144 x 2048) and the down matvec (Q2_0, W 2048 x 6144), one
+token.  ``value`` is weight GB/s over that step.  The line also carries the
+whole BASELINE suite under ``suite`` (every decode matvec config, the IQ2_XXS
+MTP-verify matmul at M = 1 and 4, and the Q4_K pp512 GEMM), each with us per
+call, absolute GB/s or TFLOP/s and the roofline fraction.
+
+Timing: inputs are resident in HBM before the timed region.  Every call reads
+a different copy of the weights (copies rotated so that >= 1 GiB is cycled,
+four times the 256 MB MALL), so weights stream from HBM, not from cache.
+Per-kernel durations come from HIP events recorded on the library's own stream
+around each call; the step time is bracketed by device synchronisation.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK = 8.0e12        # MI355X HBM3E, bytes/s
+FP16_PEAK = 2.5e15       # MI355X dense fp16 MFMA, flop/s
+ROTATE_BYTES = 1 << 30   # weights cycled per config
+
+METRIC = "quant matvec HBM GB/s (% of 8 TB/s); pp512 Q4_K GEMM TFLOPS (% MFMA)"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--suite", default="all", help="'all', 'none' or comma list of suite names")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs on one GPU only (the path has no multi-GPU "
+              "mode); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import chatokf_amd as ok
+    from chatokf_amd import synth
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.cuda.init()
+    enc = ok.Enc(0)
+    stream = torch.cuda.ExternalStream(enc.stream)
+
+    def rotated(w_np):
+        """Device copies of one weight tensor, enough to cycle >= 1 GiB."""
+        base = torch.from_numpy(w_np).cuda()
+        n = max(2, -(-ROTATE_BYTES // w_np.nbytes))
+        copies = [base] + [base.clone() for _ in range(n - 1)]
+        torch.cuda.synchronize()
+        return copies
+
+    def time_calls(launch, n_calls, warm):
+        """Average kernel time (s) of n_calls launches, HIP events on enc's stream."""
+        for i in range(warm):
+            launch(i)
+        starts = [torch.cuda.Event(enable_timing=True) for _ in range(n_calls)]
+        ends = [torch.cuda.Event(enable_timing=True) for _ in range(n_calls)]
+        torch.cuda.synchronize()
+        for i in range(n_calls):
+            starts[i].record(stream)
+            launch(warm + i)
+            ends[i].record(stream)
+        torch.cuda.synchronize()
+        ms = np.array([s.elapsed_time(e) for s, e in zip(starts, ends)])
+        return float(ms.mean()) * 1e-3, float(np.median(ms)) * 1e-3
+
+    # ----------------------------------------------------------- headline
+    t0 = time.time()
+    K1, M1 = 2048, 6144
+    log("bench: generating ternary FFN weights")
+    gate_np = synth.q2_0(M1, K1, 1002)
+    up_np = synth.q2_0(M1, K1, 1202)
+    down_np = synth.q2_0(K1, M1, 1102)
+    gates, ups, downs = rotated(gate_np), rotated(up_np), rotated(down_np)
+    x = torch.from_numpy(synth.activations(1, K1, 2002)).cuda()
+    h = torch.empty(M1, device="cuda")
+    h2 = torch.empty(M1, device="cuda")
+    y = torch.empty(K1, device="cuda")
+    hx = torch.from_numpy(synth.activations(1, M1, 2102)).cuda()  # down-proj input
+    nrot = len(gates)
+    step_bytes = gate_np.nbytes + up_np.nbytes + down_np.nbytes
+
+    def ffn_step(i):
+        j = i % nrot
+        enc.gemv(ok.QuantTensor(gates[j], K1, M1, ok.Q2_0), x, h)
+        enc.gemv(ok.QuantTensor(ups[j], K1, M1, ok.Q2_0), x, h2)
+        enc.gemv(ok.QuantTensor(downs[j], M1, K1, ok.Q2_0), hx, y)
+
+    for i in range(args.warmup):
+        ffn_step(i)
+    torch.cuda.synchronize()
+    w0 = time.perf_counter()
+    for i in range(args.steps):
+        ffn_step(args.warmup + i)
+    torch.cuda.synchronize()
+    step_s = (time.perf_counter() - w0) / args.steps
+    value = step_bytes / step_s / 1e9
+
+    # dominant kernel of the step: per-launch HIP-event durations
+    gate_t, _ = time_calls(
+        lambda i: enc.gemv(ok.QuantTensor(gates[i % nrot], K1, M1, ok.Q2_0), x, h), args.steps, 5)
+    down_t, _ = time_calls(
+        lambda i: enc.gemv(ok.QuantTensor(downs[i % nrot], M1, K1, ok.Q2_0), hx, y), args.steps, 5)
+    if gate_t >= down_t:
+        dom = ("q2_0 gate/up matvec 6144x2048", gate_np.nbytes, gate_t)
+    else:
+        dom = ("q2_0 down matvec 2048x6144", down_np.nbytes, down_t)
+    roofline = {"kernel": dom[0], "bound": "hbm", "achieved": round(dom[1] / dom[2] / 1e9, 1),
+                "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(dom[1] / dom[2] / HBM_PEAK, 4),
+                "us_per_launch": round(dom[2] * 1e6, 3), "traffic": None}
+    log(f"bench: ffn step {step_s*1e6:.2f} us, {value:.1f} GB/s; gate {gate_t*1e6:.2f} us, "
+        f"down {down_t*1e6:.2f} us")
+    del gates, ups, downs
+    torch.cuda.empty_cache()
+
+    # ----------------------------------------------------------- suite
+    SUITE = [
+        # name, type, M, K, N, weight seed, x seed
+        ("q8_0_matvec_2048x2048", ok.Q8_0, 2048, 2048, 1, 1001, 2001),
+        ("q2_0_matvec_6144x2048", ok.Q2_0, 6144, 2048, 1, 1002, 2002),
+        ("q2_0_matvec_2048x6144", ok.Q2_0, 2048, 6144, 1, 1102, 2102),
+        ("q4_k_matvec_17408x5120", ok.Q4_K, 17408, 5120, 1, 1003, 2003),
+        ("q4_k_matvec_5120x17408", ok.Q4_K, 5120, 17408, 1, 1103, 2103),
+        ("iq2_xxs_matvec_17408x5120_m1", ok.IQ2_XXS, 17408, 5120, 1, 1004, 2004),
+        ("iq2_xxs_matmul_17408x5120_m4", ok.IQ2_XXS, 17408, 5120, 4, 1004, 2004),
+        ("q4_k_gemm_pp512_17408x5120", ok.Q4_K, 17408, 5120, 512, 1003, 2005),
+    ]
+    want = None if args.suite == "all" else set(args.suite.split(",")) if args.suite != "none" else set()
+    suite = []
+    wcache = {}
+    for name, t, M, K, N, ws, xs in SUITE:
+        if want is not None and name not in want:
+            continue
+        key = (t, M, K, ws)
+        if key not in wcache:
+            wcache.clear()
+            torch.cuda.empty_cache()
+            log(f"bench: generating {name}")
+            w_np = synth.weights(t, M, K, ws)
+            wcache[key] = (w_np.nbytes, rotated(w_np))
+        wbytes, copies = wcache[key]
+        X = torch.from_numpy(synth.activations(N, K, xs)).cuda()
+        Y = torch.empty((N, M), device="cuda")
+        nr = len(copies)
+
+        def call(i, copies=copies, t=t, M=M, K=K, N=N, X=X, Y=Y, nr=nr):
+            enc.gemm(ok.QuantTensor(copies[i % nr], K, M, t), X, Y, N)
+
+        n_calls = args.steps if N < 512 else max(10, args.steps // 10)
+        mean_s, med_s = time_calls(call, n_calls, max(3, args.warmup // 2))
+        flops = 2.0 * M * K * N
+        rec = {"name": name, "us": round(mean_s * 1e6, 3), "us_median": round(med_s * 1e6, 3),
+               "weight_bytes": wbytes, "GBps": round(wbytes / mean_s / 1e9, 1),
+               "TFLOPs": round(flops / mean_s / 1e12, 2)}
+        if N >= 512:
+            rec["bound"], rec["frac"] = "mfma_fp16", round(flops / mean_s / FP16_PEAK, 4)
+        else:
+            rec["bound"], rec["frac"] = "hbm", round(wbytes / mean_s / HBM_PEAK, 4)
+        log("bench:", json.dumps(rec))
+        suite.append(rec)
+        del X, Y
+    wcache.clear()
+
+    # ----------------------------------------------------------- CPU baseline
+    cpu = None
+    if not args.no_cpu:
+        import oracle  # the CPU baseline leg: the oracle restatement of GQ.matvec
+
+        cores = oracle.usable_cores()
+        xn = synth.activations(1, K1, 2002)[0]
+        hn = synth.activations(1, M1, 2102)[0]
+        times = []
+        c0 = time.perf_counter()
+        while time.perf_counter() - c0 < args.cpu_seconds or len(times) < 5:
+            s = time.perf_counter()
+            oracle.matvec(ok.Q2_0, gate_np, K1, M1, xn, threads=cores)
+            oracle.matvec(ok.Q2_0, up_np, K1, M1, xn, threads=cores)
+            oracle.matvec(ok.Q2_0, down_np, M1, K1, hn, threads=cores)
+            times.append(time.perf_counter() - s)
+        cpu_step = float(np.median(times))
+        cpu = {"value": round(step_bytes / cpu_step / 1e9, 2), "unit": "GB/s", "cores": cores,
+               "kind": "port",
+               "sample": f"median of {len(times)} ternary FFN steps (gate+up+down Q2_0 matvec, "
+                         f"same inputs) in {time.perf_counter() - c0:.1f} s: C restatement of "
+                         "Q2_0.matvec (LLM/Base/Quant.swift:28-65), row-parallel over cores",
+               "us_per_step": round(cpu_step * 1e6, 1)}
+        log("bench: cpu", json.dumps(cpu))
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_s * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (reference LCG, BASELINE.json distributions); weights rotated over >= 1 GiB",
+        "config": {"workload": "BASELINE configs[1]: Bonsai-1.7B ternary FFN decode step, one token: "
+                               "gate+up Q2_0 W 6144x2048 and down Q2_0 W 2048x6144 matvecs",
+                   "weight_bytes_per_step": step_bytes, "parallelism": "single GPU"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "suite": suite,
+        "wall_s": round(time.time() - t0, 1),
+    }
+    enc.close()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

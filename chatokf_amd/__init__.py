@@ -1,0 +1,180 @@
+"""chatokf_amd -- MI355X (gfx950) quantized weight x activation path.
+
+The product is the C-ABI library ``libokf_quant.so`` (declared in
+``include/okf_quant.h``, built by ``chatokf_amd.build``).  This module is the
+Python binding of that ABI, shaped like the reference's dispatch surface
+``MetalEnc`` (``LLM/Base/MetalEnc.swift``): ``gemv`` (:84-93), ``gemm``
+(:241-289), ``gemm_tile`` (:326-352) and ``dequant_row`` (:402-459).  Torch
+tensors are only device-memory plumbing; every computation runs in the HIP
+library.  There is no fallback: if the library is missing, importing the
+binding raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+from .formats import Q8_0, Q4_K, IQ2_XXS, Q2_0, NAMES, BY_NAME, block_elems, row_bytes
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libokf_quant.so")
+
+OKF_OK, OKF_E_TYPE, OKF_E_SHAPE, OKF_E_HIP, OKF_E_INJECTED, OKF_E_ARG, OKF_E_NODEV = range(7)
+
+# Every symbol include/okf_quant.h declares.
+EXPORTS = (
+    "okf_ctx_create", "okf_ctx_destroy", "okf_ctx_stream", "okf_row_bytes",
+    "okf_gemv", "okf_gemm", "okf_gemm_tile", "okf_dequant_row", "okf_sync",
+    "okf_set_fault_rate", "okf_last_hip_error", "okf_strerror",
+)
+
+
+class OkfWeight(ctypes.Structure):
+    """``okf_weight`` of include/okf_quant.h."""
+    _fields_ = [
+        ("base", ctypes.c_void_p),
+        ("off", ctypes.c_uint64),
+        ("K", ctypes.c_uint32),
+        ("M", ctypes.c_uint32),
+        ("ggml_type", ctypes.c_int32),
+    ]
+
+
+class OkfError(RuntimeError):
+    def __init__(self, status: int, what: str):
+        self.status = status
+        super().__init__(f"{what}: {_lib().okf_strerror(status).decode()} ({status})")
+
+
+_LIB = None
+
+
+def _lib():
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"{LIB_PATH} is missing: build it with `python -m chatokf_amd.build` "
+                "(there is no non-HIP fallback)")
+        lib = ctypes.CDLL(LIB_PATH)
+        vp, u32, u64, i32 = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int32
+        W = ctypes.POINTER(OkfWeight)
+        sig = {
+            "okf_ctx_create": [ctypes.c_int, ctypes.POINTER(vp)],
+            "okf_ctx_destroy": [vp],
+            "okf_ctx_stream": [vp, ctypes.POINTER(vp)],
+            "okf_row_bytes": [i32, u64, ctypes.POINTER(u64)],
+            "okf_gemv": [vp, W, vp, vp],
+            "okf_gemm": [vp, W, vp, u32, vp],
+            "okf_gemm_tile": [vp, W, vp, u32, vp],
+            "okf_dequant_row": [vp, W, u32, vp],
+            "okf_sync": [vp],
+            "okf_set_fault_rate": [vp, ctypes.c_double, u64],
+            "okf_last_hip_error": [vp],
+        }
+        for name, args in sig.items():
+            f = getattr(lib, name)
+            f.argtypes = args
+            f.restype = ctypes.c_int
+        lib.okf_strerror.argtypes = [ctypes.c_int]
+        lib.okf_strerror.restype = ctypes.c_char_p
+        _LIB = lib
+    return _LIB
+
+
+def lib():
+    """The loaded ctypes library (raises if it was never built)."""
+    return _lib()
+
+
+def _ptr(t) -> int:
+    if t is None:
+        return 0
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+class QuantTensor:
+    """A GGUF-quantized matrix in device memory: M rows of K weights.
+
+    Replaces GGUFTensor + WeightRef (``LLM/Base/GGUF.swift:49-57``,
+    ``LLM/Base/MetalContext.swift:4-11``).  ``data`` is a device byte buffer
+    (a torch uint8 tensor or a raw pointer), ``off`` a byte offset into it.
+    """
+
+    def __init__(self, data, K: int, M: int, ggml_type: int, off: int = 0):
+        self.data, self.K, self.M, self.type, self.off = data, int(K), int(M), int(ggml_type), int(off)
+
+    @property
+    def row_bytes(self) -> int:
+        return row_bytes(self.type, self.K)
+
+    def c(self) -> OkfWeight:
+        return OkfWeight(_ptr(self.data), self.off, self.K, self.M, self.type)
+
+
+class Enc:
+    """The MetalEnc-shaped encoder over one okf context (one device, one stream)."""
+
+    def __init__(self, device: int = 0):
+        self._lib = _lib()
+        h = ctypes.c_void_p()
+        st = self._lib.okf_ctx_create(int(device), ctypes.byref(h))
+        if st != OKF_OK:
+            raise OkfError(st, f"okf_ctx_create({device})")
+        self.h = h
+        self.device = device
+
+    # -- lifetime
+    def close(self):
+        if getattr(self, "h", None):
+            self._lib.okf_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, st: int, what: str):
+        if st != OKF_OK:
+            raise OkfError(st, what)
+
+    # -- calls
+    @property
+    def stream(self) -> int:
+        s = ctypes.c_void_p()
+        self._check(self._lib.okf_ctx_stream(self.h, ctypes.byref(s)), "okf_ctx_stream")
+        return s.value or 0
+
+    def gemv(self, w: QuantTensor, x, out):
+        wc = w.c()
+        self._check(self._lib.okf_gemv(self.h, ctypes.byref(wc), _ptr(x), _ptr(out)), "okf_gemv")
+
+    def gemm(self, w: QuantTensor, X, out, N: int):
+        wc = w.c()
+        self._check(self._lib.okf_gemm(self.h, ctypes.byref(wc), _ptr(X), int(N), _ptr(out)), "okf_gemm")
+
+    def gemm_tile(self, w: QuantTensor, X, out, N: int):
+        wc = w.c()
+        self._check(self._lib.okf_gemm_tile(self.h, ctypes.byref(wc), _ptr(X), int(N), _ptr(out)),
+                    "okf_gemm_tile")
+
+    def dequant_row(self, w: QuantTensor, out, n: int):
+        wc = w.c()
+        self._check(self._lib.okf_dequant_row(self.h, ctypes.byref(wc), int(n), _ptr(out)),
+                    "okf_dequant_row")
+
+    def sync(self):
+        self._check(self._lib.okf_sync(self.h), "okf_sync")
+
+    def set_fault_rate(self, rate: float, seed: int):
+        self._check(self._lib.okf_set_fault_rate(self.h, float(rate), int(seed)), "okf_set_fault_rate")
+
+
+__all__ = [
+    "Q8_0", "Q4_K", "IQ2_XXS", "Q2_0", "NAMES", "BY_NAME", "block_elems", "row_bytes",
+    "QuantTensor", "Enc", "OkfError", "OkfWeight", "lib", "EXPORTS", "LIB_PATH",
+]

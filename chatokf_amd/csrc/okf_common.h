@@ -1,0 +1,54 @@
+// okf_common.h -- shared device helpers for the gfx950 quantized kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace okf {
+
+enum Fmt : int { Q8_0 = 8, Q4_K = 12, IQ2_XXS = 16, Q2_0 = 42 };
+
+// Bytes of one 256-weight span (Q8_0: 8 blocks, Q2_0: 2 blocks), matching the
+// reference's IQArgs.blk (LLM/Base/MetalEnc.swift:162-167).
+__host__ __device__ constexpr uint32_t block_bytes(int f) {
+    return f == Q8_0 ? 34 : f == Q2_0 ? 34 : f == Q4_K ? 144 : 66;
+}
+__host__ __device__ constexpr uint32_t block_elems(int f) {
+    return f == Q8_0 ? 32 : f == Q2_0 ? 128 : 256;
+}
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// Unaligned load: gfx950 runs with unaligned global access enabled, so this
+// compiles to one global_load_dword{,x2,x4} at any byte address.
+template <class T>
+__device__ __forceinline__ T ldu(const uint8_t *p) {
+    T v;
+    __builtin_memcpy(&v, p, sizeof(T));
+    return v;
+}
+
+// Exact binary16 -> binary32 (v_cvt_f32_f16).
+__device__ __forceinline__ float h2f(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+__device__ __forceinline__ uint32_t byte_of(uint32_t v, uint32_t i) {
+    return __builtin_amdgcn_ubfe(v, i * 8, 8);
+}
+
+// Sum over the 64 lanes of a wavefront; every lane gets the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// ksigns (LLM/Quantize/IQ2Grid.swift:73): the 7 stored sign bits plus an
+// eighth that makes the count of set bits even.
+__device__ __forceinline__ uint32_t iq2_signs(uint32_t s7) {
+    return s7 | ((__builtin_popcount(s7) & 1u) << 7);
+}
+
+}  // namespace okf

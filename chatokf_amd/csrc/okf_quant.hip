@@ -1,0 +1,266 @@
+// okf_quant.hip -- the C ABI (include/okf_quant.h) over the gfx950 kernels.
+//
+// Host-side dispatch mirrors the reference's MetalEnc (LLM/Base/MetalEnc.swift):
+// gemv picks the per-format kernel (:84-153), gemm applies the
+// N == 1 / 2..5 / > 5 policy (:241-289), dequantRow unpacks one row (:402-459).
+// Validation failures return a status instead of the reference's
+// fatalError / precondition.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdint>
+#include <cstring>
+#include <new>
+
+#include "../../include/okf_quant.h"
+#include "okf_common.h"
+#include "okf_decode.h"
+#include "okf_gemm.h"
+#include "okf_gemv.h"
+
+#include "iq2xxs_grid.inc"
+
+struct okf_ctx {
+    int device = -1;
+    hipStream_t stream = nullptr;
+    uint2 *grid = nullptr;  // 256 IQ2_XXS grid entries in device memory
+    double fault_rate = 0;
+    uint64_t fault_state = 0;
+    int last_hip = 0;
+};
+
+namespace {
+
+using namespace okf;
+
+bool supported(int32_t t) { return t == Q8_0 || t == Q4_K || t == IQ2_XXS || t == Q2_0; }
+
+int hip_fail(okf_ctx *c, hipError_t e) {
+    c->last_hip = (int)e;
+    return OKF_E_HIP;
+}
+
+// splitmix64 -> uniform [0, 1); deterministic per seed.
+double next_uniform(uint64_t &s) {
+    uint64_t z = (s += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    return (double)(z >> 11) * (1.0 / 9007199254740992.0);
+}
+
+// Shared prologue of every launch call: arguments, fault injection, device.
+int begin(okf_ctx *c) {
+    if (!c) return OKF_E_ARG;
+    if (c->fault_rate > 0 && next_uniform(c->fault_state) < c->fault_rate) return OKF_E_INJECTED;
+    if (c->device < 0) return OKF_E_NODEV;
+    hipError_t e = hipSetDevice(c->device);
+    return e == hipSuccess ? OKF_OK : hip_fail(c, e);
+}
+
+int check_weight(const okf_weight *w, uint64_t *row_bytes) {
+    if (!w || !w->base) return OKF_E_ARG;
+    if (!supported(w->ggml_type)) return OKF_E_TYPE;
+    if (w->K == 0 || w->M == 0 || w->K % block_elems(w->ggml_type)) return OKF_E_SHAPE;
+    *row_bytes = (uint64_t)w->K / block_elems(w->ggml_type) * block_bytes(w->ggml_type);
+    const uintptr_t a = (uintptr_t)w->base + w->off;
+    // Q4_K kernels read 16-byte header/code chunks; others need 2-byte alignment.
+    if (w->ggml_type == Q4_K ? (a & 15) : (a & 1)) return OKF_E_SHAPE;
+    return OKF_OK;
+}
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+int finish(okf_ctx *c) {
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? OKF_OK : hip_fail(c, e);
+}
+
+template <int F, int NC>
+void launch_gemv_nc(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t M,
+                    const float *X, float *Y) {
+    // Two rows per wavefront when there are rows to spare, else one, so small
+    // M still spreads over the 256 CUs.
+    if (M >= 4096) {
+        constexpr int R = 2;
+        dim3 grid((M + 4 * R - 1) / (4 * R));
+        hipLaunchKernelGGL((gemv_kernel<F, NC, R>), grid, dim3(256), 0, c->stream, W, rb, K, M, X, Y,
+                           c->grid);
+    } else {
+        constexpr int R = 1;
+        dim3 grid((M + 4 * R - 1) / (4 * R));
+        hipLaunchKernelGGL((gemv_kernel<F, NC, R>), grid, dim3(256), 0, c->stream, W, rb, K, M, X, Y,
+                           c->grid);
+    }
+}
+
+template <int F>
+void launch_gemv(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t M, const float *X,
+                 uint32_t N, float *Y) {
+    switch (N) {
+    case 1: launch_gemv_nc<F, 1>(c, W, rb, K, M, X, Y); break;
+    case 2: launch_gemv_nc<F, 2>(c, W, rb, K, M, X, Y); break;
+    case 3: launch_gemv_nc<F, 3>(c, W, rb, K, M, X, Y); break;
+    case 4: launch_gemv_nc<F, 4>(c, W, rb, K, M, X, Y); break;
+    default: launch_gemv_nc<F, 5>(c, W, rb, K, M, X, Y); break;
+    }
+}
+
+template <int F>
+void launch_gemm(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t M, const float *X,
+                 uint32_t N, float *Y) {
+    dim3 grid((N + GB_N - 1) / GB_N, (M + GB_M - 1) / GB_M);
+    hipLaunchKernelGGL((gemm_mfma_kernel<F>), grid, dim3(256), 0, c->stream, W, rb, K, M, X, N, Y,
+                       c->grid);
+}
+
+template <int F>
+void launch_dequant(okf_ctx *c, const uint8_t *row, uint32_t n, float *out) {
+    const uint32_t units = n / 32;
+    hipLaunchKernelGGL((dequant_row_kernel<F>), dim3((units + 255) / 256), dim3(256), 0, c->stream,
+                       row, units, out, c->grid);
+}
+
+#define OKF_DISPATCH(type, fn, ...)                         \
+    switch (type) {                                         \
+    case Q8_0: fn<Q8_0>(__VA_ARGS__); break;                \
+    case Q2_0: fn<Q2_0>(__VA_ARGS__); break;                \
+    case Q4_K: fn<Q4_K>(__VA_ARGS__); break;                \
+    default: fn<IQ2_XXS>(__VA_ARGS__); break;               \
+    }
+
+enum class Path { Auto, Tile };
+
+int run_gemm(okf_ctx *c, const okf_weight *w, const float *X, uint32_t N, float *Y, Path path) {
+    uint64_t rb = 0;
+    int st = check_weight(w, &rb);
+    if (st) return st;
+    if (!X || !Y) return OKF_E_ARG;
+    if (N == 0) return OKF_E_SHAPE;
+    if (!aligned16(X)) return OKF_E_SHAPE;
+    if ((st = begin(c))) return st;
+    const uint8_t *W = (const uint8_t *)w->base + w->off;
+    if (path == Path::Auto && N <= 5) {
+        OKF_DISPATCH(w->ggml_type, launch_gemv, c, W, rb, w->K, w->M, X, N, Y);
+    } else {
+        OKF_DISPATCH(w->ggml_type, launch_gemm, c, W, rb, w->K, w->M, X, N, Y);
+    }
+    return finish(c);
+}
+
+}  // namespace
+
+extern "C" {
+
+int okf_ctx_create(int device, okf_ctx **out) {
+    if (!out) return OKF_E_ARG;
+    *out = nullptr;
+    okf_ctx *c = new (std::nothrow) okf_ctx();
+    if (!c) return OKF_E_ARG;
+    c->device = device;
+    if (device >= 0) {
+        hipError_t e = hipSetDevice(device);
+        // A blocking stream: it orders with the legacy default stream, so buffers
+        // filled there (e.g. by a framework) are complete before our kernels run.
+        if (e == hipSuccess) e = hipStreamCreate(&c->stream);
+        if (e == hipSuccess) e = hipMalloc((void **)&c->grid, sizeof(okf_iq2xxs_grid_host));
+        if (e == hipSuccess)
+            e = hipMemcpy(c->grid, okf_iq2xxs_grid_host, sizeof(okf_iq2xxs_grid_host),
+                          hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            if (c->grid) (void)hipFree(c->grid);
+            if (c->stream) (void)hipStreamDestroy(c->stream);
+            delete c;
+            return OKF_E_HIP;
+        }
+    } else if (device != -1) {
+        delete c;
+        return OKF_E_ARG;
+    }
+    *out = c;
+    return OKF_OK;
+}
+
+int okf_ctx_destroy(okf_ctx *c) {
+    if (!c) return OKF_E_ARG;
+    int st = OKF_OK;
+    if (c->device >= 0) {
+        (void)hipSetDevice(c->device);
+        if (hipStreamSynchronize(c->stream) != hipSuccess) st = OKF_E_HIP;
+        (void)hipFree(c->grid);
+        (void)hipStreamDestroy(c->stream);
+    }
+    delete c;
+    return st;
+}
+
+int okf_ctx_stream(okf_ctx *c, void **stream) {
+    if (!c || !stream) return OKF_E_ARG;
+    if (c->device < 0) return OKF_E_NODEV;
+    *stream = (void *)c->stream;
+    return OKF_OK;
+}
+
+int okf_row_bytes(int32_t type, uint64_t n, uint64_t *out) {
+    if (!out) return OKF_E_ARG;
+    if (!supported(type)) return OKF_E_TYPE;
+    if (n % block_elems(type)) return OKF_E_SHAPE;
+    *out = n / block_elems(type) * block_bytes(type);
+    return OKF_OK;
+}
+
+int okf_gemv(okf_ctx *c, const okf_weight *w, const float *x, float *y) {
+    return run_gemm(c, w, x, 1, y, Path::Auto);
+}
+
+int okf_gemm(okf_ctx *c, const okf_weight *w, const float *X, uint32_t N, float *Y) {
+    return run_gemm(c, w, X, N, Y, Path::Auto);
+}
+
+int okf_gemm_tile(okf_ctx *c, const okf_weight *w, const float *X, uint32_t N, float *Y) {
+    return run_gemm(c, w, X, N, Y, Path::Tile);
+}
+
+int okf_dequant_row(okf_ctx *c, const okf_weight *row, uint32_t n, float *out) {
+    if (!row || !row->base || !out) return OKF_E_ARG;
+    if (!supported(row->ggml_type)) return OKF_E_TYPE;
+    if (n == 0 || n % block_elems(row->ggml_type)) return OKF_E_SHAPE;
+    if (!aligned16(out)) return OKF_E_SHAPE;
+    int st = begin(c);
+    if (st) return st;
+    const uint8_t *p = (const uint8_t *)row->base + row->off;
+    OKF_DISPATCH(row->ggml_type, launch_dequant, c, p, n, out);
+    return finish(c);
+}
+
+int okf_sync(okf_ctx *c) {
+    if (!c) return OKF_E_ARG;
+    if (c->device < 0) return OKF_E_NODEV;
+    (void)hipSetDevice(c->device);
+    hipError_t e = hipStreamSynchronize(c->stream);
+    return e == hipSuccess ? OKF_OK : hip_fail(c, e);
+}
+
+int okf_set_fault_rate(okf_ctx *c, double rate, uint64_t seed) {
+    if (!c || !(rate >= 0.0 && rate <= 1.0)) return OKF_E_ARG;
+    c->fault_rate = rate;
+    c->fault_state = seed;
+    return OKF_OK;
+}
+
+int okf_last_hip_error(okf_ctx *c) { return c ? c->last_hip : 0; }
+
+const char *okf_strerror(int s) {
+    switch (s) {
+    case OKF_OK: return "ok";
+    case OKF_E_TYPE: return "unsupported ggml type";
+    case OKF_E_SHAPE: return "bad shape or alignment";
+    case OKF_E_HIP: return "HIP runtime error";
+    case OKF_E_INJECTED: return "injected fault";
+    case OKF_E_ARG: return "bad argument";
+    case OKF_E_NODEV: return "detached context has no device";
+    default: return "unknown status";
+    }
+}
+
+}  // extern "C"

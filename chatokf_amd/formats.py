@@ -1,0 +1,28 @@
+"""GGUF block formats on the path: ggml type ids and sizes.
+
+Type ids follow ``LLM/Base/GGUF.swift:3-14``; bytes per row follow
+``GGUF.rowByteCount`` (``LLM/Base/GGUF.swift:160-188``) and elements per block
+follow ``GQ.blockElems`` (``LLM/Gemma/Gemma4Quant.swift:77-87``).
+"""
+Q8_0 = 8
+Q4_K = 12
+IQ2_XXS = 16
+Q2_0 = 42
+
+NAMES = {Q8_0: "q8_0", Q4_K: "q4_k", IQ2_XXS: "iq2_xxs", Q2_0: "q2_0"}
+BY_NAME = {v: k for k, v in NAMES.items()}
+
+# type -> (weights per block, bytes per block)
+BLOCK = {Q8_0: (32, 34), Q2_0: (128, 34), Q4_K: (256, 144), IQ2_XXS: (256, 66)}
+
+
+def block_elems(t: int) -> int:
+    return BLOCK[t][0]
+
+
+def row_bytes(t: int, n: int) -> int:
+    """Bytes of one row of n weights; n must be a whole number of blocks."""
+    e, b = BLOCK[t]
+    if n % e:
+        raise ValueError(f"{NAMES[t]} rows need a multiple of {e} weights, got {n}")
+    return n // e * b

@@ -1,0 +1,116 @@
+/*
+ * okf_quant.h -- C ABI of the MI355X (gfx950) quantized weight x activation
+ * path: fused dequantize-and-dot for GGUF Q8_0, Q4_K, IQ2_XXS and the Bonsai
+ * ternary Q2_0 blocks.
+ *
+ * This ABI is the drop-in boundary for the reference's GPU dispatch surface
+ * (LLM/Base/MetalEnc.swift) and the weight reference it takes
+ * (LLM/Base/MetalContext.swift:4-11).  A Swift caller imports it through
+ * include/module.modulemap.
+ *
+ * Conventions (same as the reference kernels, LLM/metal/Kernels.metal):
+ *   - W has M rows of K weights; row m's blocks are contiguous at byte
+ *     m * rowBytes(K), starting at base + off (GGUF dims = [K, M]).
+ *   - x / X are fp32, row-major X[N][K]; outputs are fp32 Y[N][M]
+ *     (out[n * M + m], Kernels.metal:112).
+ *   - Every pointer passed to okf_gemv / okf_gemm / okf_dequant_row is device
+ *     memory owned by the caller.  Calls are asynchronous on the context's
+ *     stream (okf_sync waits); a context is used by one thread at a time.
+ *   - Nothing aborts: each entry point returns an okf_status.
+ */
+#ifndef OKF_QUANT_H
+#define OKF_QUANT_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Return codes.  The reference turns these conditions into fatalError /
+ * precondition (MetalEnc.swift:109-113, :144-146, :268-269) or a GPUGate
+ * verdict (LLM/Base/MetalGates.swift:130-142). */
+typedef enum {
+    OKF_OK = 0,
+    OKF_E_TYPE = 1,     /* ggml type has no kernel here */
+    OKF_E_SHAPE = 2,    /* K not a whole number of blocks, zero size, misalignment */
+    OKF_E_HIP = 3,      /* a HIP runtime call failed (see okf_last_hip_error) */
+    OKF_E_INJECTED = 4, /* fault injected by okf_set_fault_rate */
+    OKF_E_ARG = 5,      /* null pointer or bad argument */
+    OKF_E_NODEV = 6     /* detached context (device -1): nothing can run */
+} okf_status;
+
+/* ggml type ids, LLM/Base/GGUF.swift:3-14 */
+enum {
+    OKF_TYPE_Q8_0 = 8,
+    OKF_TYPE_Q4_K = 12,
+    OKF_TYPE_IQ2_XXS = 16,
+    OKF_TYPE_Q2_0 = 42
+};
+
+typedef struct okf_ctx okf_ctx;
+
+/* A quantized tensor in device memory.  Replaces GGUFTensor + WeightRef
+ * {buf, local u64 off} (LLM/Base/GGUF.swift:49-57,
+ * LLM/Base/MetalContext.swift:4-11): the 64-bit off lets one base address a
+ * weight window larger than 4 GB (Kernels.metal:22-24). */
+typedef struct {
+    const void *base;
+    uint64_t off;
+    uint32_t K;        /* weights per row (dims[0]) */
+    uint32_t M;        /* rows (dims[1]) */
+    int32_t ggml_type;
+} okf_weight;
+
+/* Replaces MetalContext.init (MetalContext.swift:58-80): binds a device,
+ * creates the stream and uploads the IQ2_XXS grid.  device = -1 makes a
+ * detached context that validates arguments and injects faults but runs
+ * nothing (OKF_E_NODEV), for host-only tests. */
+int okf_ctx_create(int device, okf_ctx **out);
+int okf_ctx_destroy(okf_ctx *ctx);
+
+/* The hipStream_t the context launches on (for events / interop). */
+int okf_ctx_stream(okf_ctx *ctx, void **stream);
+
+/* GGUF.rowByteCount (LLM/Base/GGUF.swift:160-188) for the four types. */
+int okf_row_bytes(int32_t ggml_type, uint64_t n, uint64_t *out);
+
+/* MetalEnc.gemv (MetalEnc.swift:84-93): y[M] = W x[K].
+ * Q4_K needs base + off 16-byte aligned; x must be 16-byte aligned. */
+int okf_gemv(okf_ctx *ctx, const okf_weight *w, const float *x, float *y);
+
+/* MetalEnc.gemm (MetalEnc.swift:241-289): Y[N][M] = X[N][K] W^T.  Dispatch
+ * policy as the reference: N == 1 -> gemv; 2 <= N <= 5 -> narrow (one weight
+ * pass serving all N columns, gemmNarrow / gemmNarrowIQ :176-239);
+ * N > 5 -> MFMA tile GEMM (gemmTiled / iqGemmTiled, :354-400). */
+int okf_gemm(okf_ctx *ctx, const okf_weight *w, const float *X, uint32_t N, float *Y);
+
+/* MetalEnc.gemmTile (MetalEnc.swift:326-352): the tile GEMM for any N >= 1. */
+int okf_gemm_tile(okf_ctx *ctx, const okf_weight *w, const float *X, uint32_t N, float *Y);
+
+/* MetalEnc.dequantRow (MetalEnc.swift:402-459): unpack n weights of the row
+ * at base + off to fp32, bit-identical to the reference's CPU decoders
+ * (GQ.gather, LLM/Gemma/Gemma4Quant.swift:330-364).  row->K, row->M are
+ * ignored; n must be a whole number of blocks. */
+int okf_dequant_row(okf_ctx *ctx, const okf_weight *row, uint32_t n, float *out);
+
+/* Waits for all work on the context's stream: the analogue of
+ * commit + waitUntilCompleted (LLM/Base/MetalGates.swift:144-149).  Returns
+ * OKF_E_HIP if a kernel failed. */
+int okf_sync(okf_ctx *ctx);
+
+/* GPUGate.simulate(faultRate:seed:) analogue (MetalGates.swift:101-108):
+ * each later launch call fails with OKF_E_INJECTED with probability rate,
+ * from a seeded generator, before anything is enqueued.  rate = 0 disables. */
+int okf_set_fault_rate(okf_ctx *ctx, double rate, uint64_t seed);
+
+/* The last hipError_t seen by the context (0 if none). */
+int okf_last_hip_error(okf_ctx *ctx);
+
+/* Static text for a status code. */
+const char *okf_strerror(int status);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

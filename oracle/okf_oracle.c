@@ -1,0 +1,363 @@
+/*
+ * okf_oracle.c -- CPU restatement of ChatOKF's quantized matvec/matmul and
+ * block decoders.  TEST INFRASTRUCTURE ONLY (checker + CPU baseline); the
+ * product never links it.  See okf_oracle.h for what pins each function.
+ *
+ * Build: oracle/Makefile (-O2 -ffp-contract=off -fno-fast-math).
+ */
+#define _GNU_SOURCE
+#include "okf_oracle.h"
+
+#include <pthread.h>
+#include <sched.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "iq2xxs_grid.inc"
+
+#if defined(__FP_FAST_FMAF) || defined(__FAST_MATH__)
+#error "the oracle must be built without fast-math"
+#endif
+
+/* ------------------------------------------------------------------ */
+/* scalar helpers                                                      */
+
+float okf_ref_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h >> 15) << 31;
+    uint32_t exp = (h >> 10) & 0x1f;
+    uint32_t man = h & 0x3ff;
+    uint32_t bits;
+    if (exp == 0) {
+        if (man == 0) {
+            bits = sign;
+        } else { /* subnormal: renormalise */
+            int e = -1;
+            do {
+                man <<= 1;
+                e++;
+            } while ((man & 0x400) == 0);
+            man &= 0x3ff;
+            bits = sign | ((uint32_t)(127 - 15 - e) << 23) | (man << 13);
+        }
+    } else if (exp == 31) {
+        bits = sign | 0x7f800000u | (man << 13);
+    } else {
+        bits = sign | ((exp + 127 - 15) << 23) | (man << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+static inline uint16_t ld16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+static inline uint32_t ld32(const uint8_t *p) {
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+static inline float ldh(const uint8_t *p) { return okf_ref_f16_to_f32(ld16(p)); }
+
+/* ------------------------------------------------------------------ */
+/* sizes: LLM/Base/GGUF.swift:160-188, GQ.blockElems Gemma4Quant.swift:77-87 */
+
+static int block_geom(int32_t type, uint32_t *elems, uint32_t *bytes) {
+    switch (type) {
+    case OKF_REF_Q8_0: *elems = 32; *bytes = 34; return 0;
+    case OKF_REF_Q2_0: *elems = 128; *bytes = 34; return 0;
+    case OKF_REF_Q4_K: *elems = 256; *bytes = 144; return 0;
+    case OKF_REF_IQ2_XXS: *elems = 256; *bytes = 66; return 0;
+    default: return -1;
+    }
+}
+
+int okf_ref_row_bytes(int32_t type, uint64_t n, uint64_t *out) {
+    uint32_t e, b;
+    if (block_geom(type, &e, &b) || n % e) return -1;
+    *out = n / e * b;
+    return 0;
+}
+
+/* ------------------------------------------------------------------ */
+/* decoders                                                            */
+
+/* Q8_0.dequant, LLM/Gemma/Gemma4Quant.swift:55-68: w = Float(q) * d */
+static void dq_q8_0(const uint8_t *p, uint64_t n, float *out) {
+    for (uint64_t b = 0; b < n / 32; b++, p += 34, out += 32) {
+        float d = ldh(p);
+        for (int j = 0; j < 32; j++) out[j] = (float)(int8_t)p[2 + j] * d;
+    }
+}
+
+/* Q2_0.dequant, LLM/Base/Quant.swift:10-25: w = Float(code - 1) * d,
+ * code j = (qs[j >> 2] >> 2(j & 3)) & 3 */
+static void dq_q2_0(const uint8_t *p, uint64_t n, float *out) {
+    for (uint64_t b = 0; b < n / 128; b++, p += 34, out += 128) {
+        float d = ldh(p);
+        const uint8_t *qs = p + 2;
+        for (int j = 0; j < 128; j++) {
+            int code = (qs[j >> 2] >> ((j & 3) << 1)) & 3;
+            out[j] = (float)(code - 1) * d;
+        }
+    }
+}
+
+/* KQuant.scaleMin, LLM/Quantize/KQuants.swift:86-101 (ggml get_scale_min_k4):
+ * s(i) is byte 4 + i of the block. */
+static void scale_min(const uint8_t *b, int j, float *sc_out, float *mn_out) {
+    const uint8_t *s = b + 4;
+    uint8_t sc, mn;
+    if (j < 4) {
+        sc = s[j] & 63;
+        mn = s[j + 4] & 63;
+    } else {
+        sc = (uint8_t)((s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4));
+        mn = (uint8_t)((s[j + 4] >> 4) | ((s[j] >> 6) << 4));
+    }
+    *sc_out = (float)sc;
+    *mn_out = (float)mn;
+}
+
+/* KQuant.q4K, LLM/Quantize/KQuants.swift:104-125 */
+static void dq_q4_k_block(const uint8_t *b, float *out) {
+    float d = ldh(b), dmin = ldh(b + 2);
+    int y = 0, qoff = 16, isc = 0;
+    for (int it = 0; it < 4; it++) {
+        float s1, m1, s2, m2;
+        scale_min(b, isc, &s1, &m1);
+        scale_min(b, isc + 1, &s2, &m2);
+        float d1 = d * s1, o1 = dmin * m1;
+        float d2 = d * s2, o2 = dmin * m2;
+        for (int l = 0; l < 32; l++) {
+            uint8_t q = b[qoff + l];
+            out[y + l] = d1 * (float)(q & 0xF) - o1;
+            out[y + 32 + l] = d2 * (float)(q >> 4) - o2;
+        }
+        y += 64;
+        qoff += 32;
+        isc += 2;
+    }
+}
+
+/* IQ2XXS.dequant, LLM/Quantize/IQ2XXS.swift:34-54 */
+static void dq_iq2_xxs_block(const uint8_t *b, float *out) {
+    float d = ldh(b);
+    for (int ib = 0; ib < 8; ib++) {
+        uint32_t a0 = ld32(b + 2 + ib * 8);
+        uint32_t a1 = ld32(b + 2 + ib * 8 + 4);
+        float db = d * (0.5f + (float)(a1 >> 28)) * 0.25f;
+        for (int l = 0; l < 4; l++) {
+            uint64_t entry = okf_ref_iq2xxs_grid[(a0 >> (8 * l)) & 0xFF];
+            uint8_t signs = okf_ref_ksigns[(a1 >> (7 * l)) & 127];
+            for (int j = 0; j < 8; j++) {
+                float g = (float)((entry >> (8 * j)) & 0xFF);
+                float s = (signs & okf_ref_kmask[j]) ? -1.0f : 1.0f;
+                out[ib * 32 + l * 8 + j] = db * g * s;
+            }
+        }
+    }
+}
+
+typedef void (*sb_decode_fn)(const uint8_t *, float *);
+
+static sb_decode_fn sb_decoder(int32_t type) {
+    switch (type) {
+    case OKF_REF_Q4_K: return dq_q4_k_block;
+    case OKF_REF_IQ2_XXS: return dq_iq2_xxs_block;
+    default: return NULL;
+    }
+}
+
+int okf_ref_dequant(int32_t type, const uint8_t *p, uint64_t n, float *out) {
+    uint32_t e, bytes;
+    if (block_geom(type, &e, &bytes) || n % e) return -1;
+    switch (type) {
+    case OKF_REF_Q8_0: dq_q8_0(p, n, out); break;
+    case OKF_REF_Q2_0: dq_q2_0(p, n, out); break;
+    default: { /* superBlockGather, Gemma4Quant.swift:351-360 */
+        sb_decode_fn dec = sb_decoder(type);
+        for (uint64_t b = 0; b < n / 256; b++) dec(p + b * bytes, out + b * 256);
+    }
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------ */
+/* per-row kernels                                                      */
+
+typedef struct {
+    int32_t type;
+    const uint8_t *w;
+    uint32_t K, M;
+    uint64_t row_bytes;
+    const float *x; /* matvec: x[K]; blockMatmul: XT[K][N] */
+    float *y;
+    uint32_t N;
+} job_t;
+
+/* GQ.matvec q8_0 arm, Gemma4Quant.swift:115-124, driven by rowParallel
+ * :250-279: acc += (sum_j Float(q_j) * x_j) * d, block by block. */
+static float row_q8_0(const job_t *j, uint32_t m) {
+    const uint8_t *p = j->w + (uint64_t)m * j->row_bytes;
+    float acc = 0;
+    for (uint32_t k = 0; k < j->K; k += 32, p += 34) {
+        float a = 0;
+        float d = ldh(p);
+        for (int t = 0; t < 32; t++) a += (float)(int8_t)p[2 + t] * j->x[k + t];
+        acc += a * d;
+    }
+    return acc;
+}
+
+/* Q2_0.matvec, LLM/Base/Quant.swift:41-61: acc += d * (lo + 2 * hi - sy). */
+static float row_q2_0(const job_t *j, uint32_t m) {
+    const uint8_t *p = j->w + (uint64_t)m * j->row_bytes;
+    float acc = 0;
+    for (uint32_t k = 0; k < j->K; k += 128, p += 34) {
+        float d = ldh(p);
+        const uint8_t *qs = p + 2;
+        float lo = 0, hi = 0, sy = 0;
+        for (int t = 0; t < 128; t++) {
+            uint8_t code = (qs[t >> 2] >> ((t & 3) << 1)) & 3;
+            float xv = j->x[k + t];
+            sy += xv;
+            if (code & 1) lo += xv;
+            if (code & 2) hi += xv;
+        }
+        acc += d * (lo + 2 * hi - sy);
+    }
+    return acc;
+}
+
+/* GQ.matvec superblock arm, Gemma4Quant.swift:125-136: decode 256 weights,
+ * then acc_b = sum_i w_i * x_i; acc += acc_b. */
+static float row_superblock(const job_t *j, uint32_t m) {
+    const uint8_t *p = j->w + (uint64_t)m * j->row_bytes;
+    sb_decode_fn dec = sb_decoder(j->type);
+    uint32_t bytes = j->type == OKF_REF_Q4_K ? 144 : 66;
+    float w[256];
+    float acc = 0;
+    for (uint32_t k = 0; k < j->K; k += 256, p += bytes) {
+        dec(p, w);
+        float a = 0;
+        for (int i = 0; i < 256; i++) a += w[i] * j->x[k + i];
+        acc += a;
+    }
+    return acc;
+}
+
+/* GQ.blockMatmul, Gemma4Quant.swift:172-223 (Q8_0): per row, every block is
+ * dequantized once and acc[n] += w_j * XT[k + j][n]. */
+static void row_block_matmul_q8_0(const job_t *j, uint32_t m, float *acc) {
+    const uint8_t *p = j->w + (uint64_t)m * j->row_bytes;
+    uint32_t N = j->N;
+    float blk[32];
+    for (uint32_t n = 0; n < N; n++) acc[n] = 0;
+    for (uint32_t k = 0; k < j->K; k += 32, p += 34) {
+        dq_q8_0(p, 32, blk);
+        for (int t = 0; t < 32; t++) {
+            float wj = blk[t];
+            const float *col = j->x + (uint64_t)(k + t) * N;
+            for (uint32_t n = 0; n < N; n++) acc[n] += wj * col[n];
+        }
+    }
+    for (uint32_t n = 0; n < N; n++) j->y[(uint64_t)n * j->M + m] = acc[n];
+}
+
+/* ------------------------------------------------------------------ */
+/* row-parallel driver (DispatchQueue.concurrentPerform over M rows)    */
+
+typedef struct {
+    const job_t *job;
+    uint32_t m0, m1;
+    int matmul;
+} slice_t;
+
+static void *run_slice(void *arg) {
+    const slice_t *s = (const slice_t *)arg;
+    const job_t *j = s->job;
+    if (s->matmul) {
+        float *acc = (float *)malloc(sizeof(float) * j->N);
+        for (uint32_t m = s->m0; m < s->m1; m++) row_block_matmul_q8_0(j, m, acc);
+        free(acc);
+        return NULL;
+    }
+    for (uint32_t m = s->m0; m < s->m1; m++) {
+        float v;
+        switch (j->type) {
+        case OKF_REF_Q8_0: v = row_q8_0(j, m); break;
+        case OKF_REF_Q2_0: v = row_q2_0(j, m); break;
+        default: v = row_superblock(j, m); break;
+        }
+        j->y[m] = v;
+    }
+    return NULL;
+}
+
+int okf_ref_usable_cores(void) {
+    cpu_set_t set;
+    if (sched_getaffinity(0, sizeof(set), &set) == 0) {
+        int c = CPU_COUNT(&set);
+        if (c > 0) return c;
+    }
+    return 1;
+}
+
+static void run_rows(const job_t *job, int threads, int matmul) {
+    if (threads <= 0) threads = okf_ref_usable_cores();
+    if ((uint32_t)threads > job->M) threads = (int)job->M;
+    if (threads < 1) threads = 1;
+    pthread_t *tid = (pthread_t *)malloc(sizeof(pthread_t) * threads);
+    int *live = (int *)calloc(threads, sizeof(int));
+    slice_t *sl = (slice_t *)malloc(sizeof(slice_t) * threads);
+    uint32_t per = (job->M + threads - 1) / threads;
+    for (int t = 0; t < threads; t++) {
+        uint32_t m0 = t * per > job->M ? job->M : t * per;
+        uint32_t m1 = m0 + per > job->M ? job->M : m0 + per;
+        sl[t] = (slice_t){job, m0, m1, matmul};
+    }
+    /* slices 1.. on worker threads, slice 0 inline; a failed spawn runs inline */
+    for (int t = 1; t < threads; t++)
+        live[t] = pthread_create(&tid[t], NULL, run_slice, &sl[t]) == 0;
+    run_slice(&sl[0]);
+    for (int t = 1; t < threads; t++) {
+        if (live[t]) pthread_join(tid[t], NULL);
+        else run_slice(&sl[t]);
+    }
+    free(tid);
+    free(live);
+    free(sl);
+}
+
+static int check(int32_t type, uint32_t K, uint64_t *rb) {
+    if (K == 0) return -1;
+    return okf_ref_row_bytes(type, K, rb);
+}
+
+int okf_ref_matvec(int32_t type, const uint8_t *w, uint32_t K, uint32_t M,
+                   const float *x, float *y, int threads) {
+    job_t j = {type, w, K, M, 0, x, y, 1};
+    if (check(type, K, &j.row_bytes)) return -1;
+    run_rows(&j, threads, 0);
+    return 0;
+}
+
+int okf_ref_matmul(int32_t type, const uint8_t *w, uint32_t K, uint32_t M,
+                   const float *X, uint32_t N, float *Y, int threads) {
+    uint64_t rb;
+    if (check(type, K, &rb)) return -1;
+    if (type == OKF_REF_Q8_0) {
+        /* X transposed to [K][N] (Gemma4Quant.swift:181-188) */
+        float *XT = (float *)malloc(sizeof(float) * (uint64_t)N * K);
+        if (!XT) return -1;
+        for (uint32_t n = 0; n < N; n++)
+            for (uint32_t k = 0; k < K; k++) XT[(uint64_t)k * N + n] = X[(uint64_t)n * K + k];
+        job_t j = {type, w, K, M, rb, XT, Y, N};
+        run_rows(&j, threads, 1);
+        free(XT);
+        return 0;
+    }
+    /* one column at a time (Gemma4Quant.swift:159-169) */
+    for (uint32_t n = 0; n < N; n++) {
+        job_t j = {type, w, K, M, rb, X + (uint64_t)n * K, Y + (uint64_t)n * M, 1};
+        run_rows(&j, threads, 0);
+    }
+    return 0;
+}

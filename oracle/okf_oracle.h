@@ -1,0 +1,68 @@
+/*
+ * okf_oracle.h -- CPU restatement of ChatOKF's quantized weight x activation
+ * path.  TEST INFRASTRUCTURE ONLY: the checker for the HIP library and the
+ * timed CPU baseline.  Nothing in the product (chatokf_amd/, include/) links,
+ * loads or calls it.
+ *
+ * Every function follows one reference function (file:line relative to the
+ * reference checkout).  Arithmetic keeps the reference's fp32 evaluation
+ * order; the file is compiled with -O2 -ffp-contract=off -fno-fast-math so
+ * that no multiply-add is fused and no sum is reassociated.
+ *
+ * Pinning (the evidence that this restatement is right):
+ *   - okf_ref_dequant: hand-built known-answer blocks per format, the IQ2_XXS
+ *     tables against the reference's two copies (Swift grid and the Metal
+ *     header), and an independent numpy decoder (tests/test_oracle.py).
+ *   - okf_ref_matvec / okf_ref_matmul: float64 brute-force dot over the
+ *     dequantized weights (agreement ~1e-6 relative), the closed form of the
+ *     Q2_0 lo/hi/sum identity, linearity in x, and matmul == N x matvec.
+ *   - Unpinned assumption (no Swift toolchain exists to run the original):
+ *     that Swift emitted no FMA contraction or reassociation in GQ.matvec;
+ *     the fp32 evaluation order below is the one the Swift source spells out.
+ */
+#ifndef OKF_ORACLE_H
+#define OKF_ORACLE_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml type ids, LLM/Base/GGUF.swift:3-14 */
+enum {
+    OKF_REF_Q8_0 = 8,
+    OKF_REF_Q4_K = 12,
+    OKF_REF_IQ2_XXS = 16,
+    OKF_REF_Q2_0 = 42,
+};
+
+/* GGUF.rowByteCount, LLM/Base/GGUF.swift:160-188.  0 on success, -1 for an
+ * unsupported type or an n that is not a whole number of blocks. */
+int okf_ref_row_bytes(int32_t type, uint64_t n, uint64_t *out);
+
+/* IEEE binary16 bits -> float, exact (Float(Float16) in Swift). */
+float okf_ref_f16_to_f32(uint16_t h);
+
+/* GQ.gather(row:from:0,count:n), LLM/Gemma/Gemma4Quant.swift:330-364:
+ * unpack n weights starting at p (a row start) into out. */
+int okf_ref_dequant(int32_t type, const uint8_t *p, uint64_t n, float *out);
+
+/* GQ.matvec, LLM/Gemma/Gemma4Quant.swift:89-148 (Q2_0 arm:
+ * LLM/Base/Quant.swift:28-65).  W is M rows of rowBytes(K), x[K] -> y[M].
+ * threads <= 0 uses every usable core. */
+int okf_ref_matvec(int32_t type, const uint8_t *w, uint32_t K, uint32_t M,
+                   const float *x, float *y, int threads);
+
+/* GQ.matmul, LLM/Gemma/Gemma4Quant.swift:150-170: X[N][K] -> Y[N][M].
+ * Q8_0 uses the block-reuse matmul (:172-223); Q2_0, Q4_K and IQ2_XXS run N
+ * sequential matvecs (:159-169). */
+int okf_ref_matmul(int32_t type, const uint8_t *w, uint32_t K, uint32_t M,
+                   const float *X, uint32_t N, float *Y, int threads);
+
+/* Cores this process may run on (sched_getaffinity). */
+int okf_ref_usable_cores(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,237 @@
+"""GPU parity: the HIP library (through its C ABI) against the CPU oracle.
+
+Bars (written in each test): dequantized weights bit-identical; matvec,
+narrow matmul and tile GEMM outputs within max|gpu - ref| / max|ref| <= 1e-3
+(the reference's relative metric, LLM/Qwen/QwenMetalSelfTest.swift:441-445,
+at the north-star tolerance); narrow-N vs N x gemv within 1e-5
+(QwenMetalSelfTest.swift:478-483).
+"""
+import functools
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from chatokf_amd import synth
+from chatokf_amd.formats import Q8_0, Q2_0, Q4_K, IQ2_XXS, NAMES, row_bytes
+
+torch = pytest.importorskip("torch")
+import chatokf_amd as ok  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+def say(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def rel(got, ref):
+    return float(np.abs(got.astype(np.float64) - ref).max() / np.abs(ref).max())
+
+
+@functools.lru_cache(maxsize=None)
+def weights(t, M, K, seed):
+    return synth.weights(t, M, K, seed)
+
+
+@functools.lru_cache(maxsize=None)
+def acts(N, K, seed):
+    return synth.activations(N, K, seed)
+
+
+def run_gemm(enc, t, M, K, w, X, tile=False):
+    N = X.shape[0]
+    wd, Xd = dev(w), dev(X)
+    Y = torch.full((N, M), float("nan"), device="cuda")
+    qt = ok.QuantTensor(wd, K, M, t)
+    if tile:
+        enc.gemm_tile(qt, Xd, Y, N)
+    elif N == 1:
+        enc.gemv(qt, Xd, Y)
+    else:
+        enc.gemm(qt, Xd, Y, N)
+    enc.sync()
+    return host(Y)
+
+
+# ------------------------------------------------------------------ dequant
+DQ_CASES = [(Q8_0, 6, 2048), (Q2_0, 6, 6144), (Q4_K, 4, 5120), (IQ2_XXS, 4, 5120)]
+
+
+@pytest.mark.parametrize("t,M,K", DQ_CASES, ids=[NAMES[c[0]] for c in DQ_CASES])
+def test_dequant_row_bit_exact(enc, t, M, K):
+    say("dequant", NAMES[t], M, K)
+    w = weights(t, M, K, 101)
+    wd = dev(w)
+    rb = row_bytes(t, K)
+    for m in range(M):
+        out = torch.full((K,), float("nan"), device="cuda")
+        enc.dequant_row(ok.QuantTensor(wd, K, 1, t, off=m * rb), out, K)
+        got = host(out)
+        ref = oracle.dequant(t, w[m * rb:(m + 1) * rb], K)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (NAMES[t], m)
+
+
+def test_dequant_row_q2_0_code3(enc):
+    w = synth.q2_0(2, 512, 55, codes=4)
+    out = torch.empty(512, device="cuda")
+    enc.dequant_row(ok.QuantTensor(dev(w), 512, 1, Q2_0, off=row_bytes(Q2_0, 512)), out, 512)
+    ref = oracle.dequant(Q2_0, w[row_bytes(Q2_0, 512):], 512)
+    assert np.array_equal(host(out), ref)
+
+
+# ------------------------------------------------------------------ matvec
+# The BASELINE.json decode configs at their full shapes: (name, type, M, K, seed)
+FULL_GEMV = [
+    ("q8_0 2048x2048", Q8_0, 2048, 2048, 1001),
+    ("q2_0 gate 6144x2048", Q2_0, 6144, 2048, 1002),
+    ("q2_0 down 2048x6144", Q2_0, 2048, 6144, 1102),
+    ("q4_k 17408x5120", Q4_K, 17408, 5120, 1003),
+    ("q4_k 5120x17408", Q4_K, 5120, 17408, 1103),
+    ("iq2_xxs 17408x5120", IQ2_XXS, 17408, 5120, 1004),
+]
+
+
+@pytest.mark.parametrize("name,t,M,K,seed", FULL_GEMV, ids=[c[0] for c in FULL_GEMV])
+def test_gemv_full_config(enc, name, t, M, K, seed):
+    say("gemv", name)
+    w = weights(t, M, K, seed)
+    x = acts(1, K, seed + 1000)
+    ref = oracle.matvec(t, w, K, M, x[0]).astype(np.float64)
+    got = run_gemm(enc, t, M, K, w, x)[0]
+    r = rel(got, ref)
+    say("  rel", r)
+    assert r <= TOL
+
+
+# Shapes that exercise tails: M not a multiple of the rows per workgroup, a
+# single block per row, K not a multiple of 64 units.
+EDGE = [(Q8_0, 1, 32), (Q8_0, 3, 96), (Q8_0, 4099, 2080), (Q2_0, 5, 128), (Q2_0, 4097, 384),
+        (Q4_K, 1, 256), (Q4_K, 7, 768), (Q4_K, 4101, 2304), (IQ2_XXS, 2, 256), (IQ2_XXS, 4103, 1280)]
+
+
+@pytest.mark.parametrize("t,M,K", EDGE)
+def test_gemv_edges(enc, t, M, K):
+    say("gemv edge", NAMES[t], M, K)
+    w = weights(t, M, K, 7)
+    x = acts(1, K, 8)
+    ref = oracle.matvec(t, w, K, M, x[0]).astype(np.float64)
+    assert rel(run_gemm(enc, t, M, K, w, x)[0], ref) <= TOL
+
+
+def test_gemv_weight_offset(enc):
+    # the weight window + 64-bit offset of WeightRef (MetalContext.swift:4-11)
+    t, M, K = Q4_K, 64, 1024
+    w = weights(t, M, K, 9)
+    pad = 4096
+    buf = np.zeros(pad + w.size, np.uint8)
+    buf[pad:] = w
+    x = acts(1, K, 10)
+    y = torch.empty(M, device="cuda")
+    enc.gemv(ok.QuantTensor(dev(buf), K, M, t, off=pad), dev(x), y)
+    ref = oracle.matvec(t, w, K, M, x[0]).astype(np.float64)
+    assert rel(host(y), ref) <= TOL
+
+
+# ------------------------------------------------------------------ narrow N = 2..5
+@pytest.mark.parametrize("t", [Q8_0, Q2_0, Q4_K, IQ2_XXS], ids=lambda t: NAMES[t])
+@pytest.mark.parametrize("N", [2, 3, 4, 5])
+def test_narrow_matches_oracle_and_gemv(enc, t, N):
+    M, K = 1030, 2048
+    say("narrow", NAMES[t], N)
+    w = weights(t, M, K, 13)
+    X = acts(N, K, 14)
+    ref = oracle.matmul(t, w, K, M, X).astype(np.float64)
+    got = run_gemm(enc, t, M, K, w, X)
+    assert rel(got, ref) <= TOL
+    for n in range(N):
+        g1 = run_gemm(enc, t, M, K, w, X[n:n + 1])[0]
+        assert rel(got[n], g1.astype(np.float64)) <= 1e-5
+
+
+def test_iq2_xxs_mtp_verify_full_config(enc):
+    # BASELINE config 4 at M = 4: W 17408 x 5120, X 4 x 5120
+    t, M, K = IQ2_XXS, 17408, 5120
+    w = weights(t, M, K, 1004)
+    X = acts(4, K, 2004)
+    ref = oracle.matmul(t, w, K, M, X).astype(np.float64)
+    r = rel(run_gemm(enc, t, M, K, w, X), ref)
+    say("iq2_xxs M=4 rel", r)
+    assert r <= TOL
+
+
+# ------------------------------------------------------------------ tile GEMM
+# (The metric is relative to max|ref| over the output, so every case keeps
+# enough outputs for that maximum to be representative; a single dot product
+# can cancel to near zero, where fp16 staging error is not bounded by 1e-3.)
+TILE = [(Q8_0, 300, 2048, 37), (Q2_0, 130, 1024, 129), (Q4_K, 260, 2304, 77), (IQ2_XXS, 129, 1536, 6),
+        (Q4_K, 1, 256, 64), (Q8_0, 5, 96, 200)]
+
+
+@pytest.mark.parametrize("t,M,K,N", TILE)
+def test_tile_gemm_matches_oracle(enc, t, M, K, N):
+    say("tile", NAMES[t], M, K, N)
+    w = weights(t, M, K, 17)
+    X = acts(N, K, 18)
+    ref = oracle.matmul(t, w, K, M, X).astype(np.float64)
+    got = run_gemm(enc, t, M, K, w, X, tile=True)
+    assert rel(got, ref) <= TOL
+    if N > 5:  # the auto path takes the tile for N > 5
+        assert np.array_equal(run_gemm(enc, t, M, K, w, X), got)
+
+
+def test_q4_k_pp512_full_config(enc):
+    # X 512 x 5120 . W(17408 x 5120, Q4_K) -> Y 512 x 17408.
+    t, M, K, N = Q4_K, 17408, 5120, 512
+    w = weights(t, M, K, 1003)
+    X = acts(N, K, 2005)
+    got = run_gemm(enc, t, M, K, w, X)
+    assert np.isfinite(got).all()
+    # the full oracle GEMM (512 sequential matvecs, GQ.matmul :159-169)
+    ref = oracle.matmul(t, w, K, M, X).astype(np.float64)
+    r = rel(got, ref)
+    say("pp512 rel", r)
+    assert r <= TOL
+    # every token against the independent gemv kernel
+    wd = dev(w)
+    Xd = dev(X)
+    y = torch.empty((N, M), device="cuda")
+    qt = ok.QuantTensor(wd, K, M, t)
+    for n in range(N):
+        enc.gemv(qt, Xd[n], y[n])
+    enc.sync()
+    r2 = rel(got, host(y).astype(np.float64))
+    say("pp512 vs gemv rel", r2)
+    assert r2 <= TOL
+
+
+# ------------------------------------------------------------------ failure handling
+def test_injected_fault_launches_nothing(enc):
+    t, M, K = Q8_0, 64, 256
+    w = dev(weights(t, M, K, 3))
+    x = dev(acts(1, K, 4))
+    y = torch.full((M,), 7.0, device="cuda")
+    enc.set_fault_rate(1.0, 5)
+    try:
+        with pytest.raises(ok.OkfError) as e:
+            enc.gemv(ok.QuantTensor(w, K, M, t), x, y)
+        assert e.value.status == ok.OKF_E_INJECTED
+    finally:
+        enc.set_fault_rate(0.0, 0)
+    enc.sync()
+    assert (host(y) == 7.0).all()
+    enc.gemv(ok.QuantTensor(w, K, M, t), x, y)
+    enc.sync()
+    assert not (host(y) == 7.0).all()

@@ -1,0 +1,267 @@
+"""Pins the CPU oracle (oracle/okf_oracle.c) before anything is checked against it.
+
+Every check here is independent of the oracle's own code: the reference's
+table data (tests/golden/iq2xxs_tables.json, extracted from two copies in the
+reference), hand-built blocks with closed-form answers, an independent
+vectorised numpy decoder, float64 brute force, and invariants.
+"""
+import json
+import os
+import re
+
+import numpy as np
+import pytest
+
+import oracle
+from chatokf_amd import synth
+from chatokf_amd.formats import Q8_0, Q2_0, Q4_K, IQ2_XXS
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+GOLD = json.load(open(os.path.join(ROOT, "tests", "golden", "iq2xxs_tables.json")))
+GRID = np.array([int(v, 16) for v in GOLD["iq2xxs_grid"]], dtype=np.uint64)
+KSIGNS = np.array(GOLD["ksigns"], dtype=np.uint8)
+
+
+def _f16(v):
+    return np.frombuffer(np.float16(v).tobytes(), np.uint8)
+
+
+# ------------------------------------------------------------------ tables
+def _inc_grid(path, name):
+    text = open(path).read()
+    body = text[text.index(name):]
+    body = body[body.index("{") + 1: body.index("}")]
+    return [int(t.rstrip("ull"), 16) for t in re.findall(r"0x[0-9a-fA-F]+ull", body)]
+
+
+@pytest.mark.parametrize("path,name", [
+    ("oracle/iq2xxs_grid.inc", "okf_ref_iq2xxs_grid"),
+    ("chatokf_amd/csrc/iq2xxs_grid.inc", "okf_iq2xxs_grid_host"),
+])
+def test_grid_tables_match_reference(path, name):
+    assert _inc_grid(os.path.join(ROOT, path), name) == [int(v) for v in GRID]
+
+
+def test_oracle_ksigns_match_reference():
+    text = open(os.path.join(ROOT, "oracle/iq2xxs_grid.inc")).read()
+    body = text[text.index("okf_ref_ksigns"):]
+    body = body[body.index("{") + 1: body.index("}")]
+    assert [int(t) for t in re.findall(r"\d+", body)] == GOLD["ksigns"]
+    assert GOLD["kmask"] == [1 << j for j in range(8)]
+
+
+def test_ksigns_is_even_parity_completion():
+    # The eighth sign bit makes the number of negated weights even; the HIP
+    # kernels compute it this way instead of loading the table.
+    for i in range(128):
+        par = bin(i).count("1") & 1
+        assert KSIGNS[i] == i | (par << 7)
+
+
+def test_grid_magnitudes():
+    mags = {(int(e) >> (8 * j)) & 0xFF for e in GRID for j in range(8)}
+    assert mags == {0x08, 0x19, 0x2B}
+    assert len(set(int(e) for e in GRID)) == 256
+
+
+@pytest.mark.skipif(not os.path.isdir("/root/reference/LLM"), reason="reference checkout absent")
+def test_golden_fixture_is_current(tmp_path):
+    import subprocess
+    import sys
+    env = dict(os.environ)
+    out = tmp_path / "t.json"
+    script = os.path.join(ROOT, "tests/golden/make_iq2_tables.py")
+    # regenerate into a temp copy of the script dir
+    src = open(script).read().replace('HERE = os.path.dirname(os.path.abspath(__file__))',
+                                      f'HERE = {str(tmp_path)!r}')
+    p = tmp_path / "mk.py"
+    p.write_text(src)
+    subprocess.run([sys.executable, str(p)], check=True, env=env, capture_output=True)
+    assert json.load(open(tmp_path / "iq2xxs_tables.json")) == GOLD
+
+
+# ------------------------------------------------------------------ sizes
+def test_row_bytes_match_rowByteCount():
+    # GGUF.rowByteCount, LLM/Base/GGUF.swift:160-188, at the BASELINE shapes
+    cases = [(Q8_0, 2048, 2176), (Q2_0, 2048, 544), (Q2_0, 6144, 1632),
+             (Q4_K, 5120, 2880), (Q4_K, 17408, 9792), (IQ2_XXS, 5120, 1320)]
+    for t, n, want in cases:
+        assert oracle.row_bytes(t, n) == want
+    with pytest.raises(ValueError):
+        oracle.row_bytes(Q4_K, 100)
+
+
+def test_f16_conversion_exact():
+    bits = np.arange(65536, dtype=np.uint16)
+    ref = bits.view(np.float16).astype(np.float32)
+    got = np.array([oracle.f16_to_f32(int(b)) for b in bits[::7]], np.float32)
+    r = ref[::7]
+    nan = np.isnan(r)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), r[~nan].view(np.uint32))
+
+
+# ------------------------------------------------------------------ known answers
+def test_q8_0_known_answer():
+    qs = np.array(list(range(-127, 128, 8)), np.int8)  # 32 values
+    assert qs.size == 32
+    blk = np.concatenate([_f16(1.0), qs.view(np.uint8)])
+    assert np.array_equal(oracle.dequant(Q8_0, blk, 32), qs.astype(np.float32))
+    blk = np.concatenate([_f16(0.5), qs.view(np.uint8)])
+    assert np.array_equal(oracle.dequant(Q8_0, blk, 32), qs.astype(np.float32) * 0.5)
+
+
+def test_q2_0_known_answer():
+    # byte 0b11100100 holds codes 0, 1, 2, 3 (LSB first) -> -d, 0, d, 2d
+    qs = np.full(32, 0b11100100, np.uint8)
+    blk = np.concatenate([_f16(0.25), qs])
+    want = np.tile(np.array([-0.25, 0.0, 0.25, 0.5], np.float32), 32)
+    assert np.array_equal(oracle.dequant(Q2_0, blk, 128), want)
+
+
+def test_q4_k_known_answer_scale_paths():
+    # d = 1, dmin = 2.  Scale bytes s[0..11]:
+    #   s[0..3] = 0x45 -> j<4: sc = 0x45 & 63 = 5; top bits 01 feed j>=4 sc
+    #   s[4..7] = 0x83 -> j<4: mn = 3;            top bits 10 feed j>=4 mn
+    #   s[8..11] = 0x7A -> j>=4: sc = 0xA | (1 << 4) = 26, mn = 7 | (2 << 4) = 39
+    hdr = np.concatenate([_f16(1.0), _f16(2.0), np.array([0x45] * 4 + [0x83] * 4 + [0x7A] * 4, np.uint8)])
+    qs = (np.arange(128) % 16 | ((15 - np.arange(128) % 16) << 4)).astype(np.uint8)
+    w = oracle.dequant(Q4_K, np.concatenate([hdr, qs]), 256)
+    for sb in range(8):
+        sc, mn = (5, 3) if sb < 4 else (26, 39)
+        g, hi = sb // 2, sb % 2
+        for l in range(32):
+            q = int(qs[g * 32 + l])
+            nib = (q >> 4) if hi else (q & 15)
+            assert w[sb * 32 + l] == np.float32(sc * nib - 2.0 * mn)
+
+
+def test_iq2_xxs_known_answer():
+    d = _f16(1.0)
+    sub = []
+    # sub-block 0: grid 0 (all 8s), signs 0 (+), scale 0 -> db = 1/8 -> all 1.0
+    sub.append((0, 0, 0))
+    # sub-block 1: grid 1 (byte 0 = 0x2b), signs idx 127 (all -), scale 15 -> db = 3.875
+    sub.append((0x01010101, 0x7F | (0x7F << 7) | (0x7F << 14) | (0x7F << 21), 15))
+    while len(sub) < 8:
+        sub.append((0, 0, 0))
+    qs = []
+    for a0, s, sc in sub:
+        a1 = s | (sc << 28)
+        qs += list(np.array([a0, a1], np.uint32).view(np.uint8))
+    w = oracle.dequant(IQ2_XXS, np.concatenate([d, np.array(qs, np.uint8)]), 256)
+    assert np.array_equal(w[:32], np.ones(32, np.float32))
+    row = np.array([-43.0] + [-8.0] * 7, np.float32) * np.float32(3.875)
+    assert np.array_equal(w[32:64], np.tile(row, 4))
+
+
+# ------------------------------------------------------------------ numpy decoders
+def np_dequant(t, w, M, K):
+    """Independent vectorised decoders (array arithmetic in float32)."""
+    if t == Q8_0:
+        b = w.reshape(M, K // 32, 34)
+        d = b[:, :, :2].copy().view(np.float16).astype(np.float32)
+        q = b[:, :, 2:].view(np.int8).astype(np.float32)
+        return (q * d).reshape(M, K)
+    if t == Q2_0:
+        b = w.reshape(M, K // 128, 34)
+        d = b[:, :, :2].copy().view(np.float16).astype(np.float32)
+        qs = b[:, :, 2:]
+        codes = np.stack([(qs >> s) & 3 for s in (0, 2, 4, 6)], -1).reshape(M, K // 128, 128)
+        return ((codes.astype(np.float32) - 1) * d).reshape(M, K)
+    if t == Q4_K:
+        b = w.reshape(M, K // 256, 144)
+        d = b[:, :, 0:2].copy().view(np.float16).astype(np.float32)[..., 0]
+        dm = b[:, :, 2:4].copy().view(np.float16).astype(np.float32)[..., 0]
+        s = b[:, :, 4:16].astype(np.uint32)
+        sc = np.zeros((M, K // 256, 8), np.uint32)
+        mn = np.zeros_like(sc)
+        sc[..., :4] = s[..., 0:4] & 63
+        mn[..., :4] = s[..., 4:8] & 63
+        sc[..., 4:] = (s[..., 8:12] & 15) | ((s[..., 0:4] >> 6) << 4)
+        mn[..., 4:] = (s[..., 8:12] >> 4) | ((s[..., 4:8] >> 6) << 4)
+        qs = b[:, :, 16:].reshape(M, K // 256, 4, 32)
+        nib = np.stack([qs & 15, qs >> 4], 3).reshape(M, K // 256, 8, 32).astype(np.float32)
+        d1 = d[..., None] * sc.astype(np.float32)
+        o1 = dm[..., None] * mn.astype(np.float32)
+        return (d1[..., None] * nib - o1[..., None]).reshape(M, K)
+    if t == IQ2_XXS:
+        b = w.reshape(M, K // 256, 66)
+        d = b[:, :, 0:2].copy().view(np.float16).astype(np.float32)[..., 0]
+        a = b[:, :, 2:].copy().view(np.uint32).reshape(M, K // 256, 8, 2)
+        a0, a1 = a[..., 0], a[..., 1]
+        db = d[..., None] * (np.float32(0.5) + (a1 >> 28).astype(np.float32)) * np.float32(0.25)
+        out = np.empty((M, K // 256, 8, 4, 8), np.float32)
+        for l in range(4):
+            e = GRID[(a0 >> (8 * l)) & 255]
+            sg = KSIGNS[(a1 >> (7 * l)) & 127]
+            for j in range(8):
+                g = ((e >> np.uint64(8 * j)) & np.uint64(255)).astype(np.float32)
+                s = np.where(sg & (1 << j), np.float32(-1), np.float32(1))
+                out[..., l, j] = db * g * s
+        return out.reshape(M, K)
+    raise ValueError(t)
+
+
+SMALL = [(Q8_0, 64, 256), (Q2_0, 64, 512), (Q4_K, 32, 512), (IQ2_XXS, 32, 512)]
+
+
+@pytest.mark.parametrize("t,M,K", SMALL)
+def test_oracle_dequant_matches_numpy(t, M, K):
+    w = synth.weights(t, M, K, 77)
+    ref = np_dequant(t, w, M, K)
+    rb = oracle.row_bytes(t, K)
+    for m in range(M):
+        got = oracle.dequant(t, w[m * rb:(m + 1) * rb], K)
+        assert np.array_equal(got.view(np.uint32), ref[m].view(np.uint32)), m
+
+
+def test_q2_0_code3_decodes_to_2d():
+    w = synth.q2_0(4, 256, 5, codes=4)
+    ref = np_dequant(Q2_0, w, 4, 256)
+    got = np.concatenate([oracle.dequant(Q2_0, w[m * 68:(m + 1) * 68], 256) for m in range(4)])
+    assert np.array_equal(got, ref.reshape(-1))
+    d = w.reshape(-1, 34)[:, :2].copy().view(np.float16).astype(np.float32)
+    assert np.any(ref.reshape(-1, 128) == 2 * d)  # some code 3 was drawn
+
+
+# ------------------------------------------------------------------ matvec/matmul
+@pytest.mark.parametrize("t,M,K", SMALL + [(Q2_0, 48, 6144 // 4), (Q4_K, 16, 4096)])
+def test_matvec_matches_float64(t, M, K):
+    w = synth.weights(t, M, K, 11)
+    x = synth.activations(1, K, 12)[0]
+    W = np_dequant(t, w, M, K).astype(np.float64)
+    ref = W @ x.astype(np.float64)
+    y = oracle.matvec(t, w, K, M, x)
+    assert np.abs(y - ref).max() / np.abs(ref).max() < 2e-6
+
+
+@pytest.mark.parametrize("t,M,K", SMALL)
+def test_matmul_is_column_matvecs(t, M, K):
+    w = synth.weights(t, M, K, 21)
+    X = synth.activations(3, K, 22)
+    Y = oracle.matmul(t, w, K, M, X)
+    for n in range(3):
+        y = oracle.matvec(t, w, K, M, X[n])
+        if t == Q8_0:  # block-reuse matmul sums in another order
+            assert np.abs(Y[n] - y).max() <= 1e-5 * np.abs(y).max()
+        else:  # GQ.matmul runs the matvec itself
+            assert np.array_equal(Y[n], y)
+
+
+def test_matvec_thread_count_does_not_change_bits():
+    w = synth.weights(Q4_K, 37, 1024, 31)
+    x = synth.activations(1, 1024, 32)[0]
+    a = oracle.matvec(Q4_K, w, 1024, 37, x, threads=1)
+    b = oracle.matvec(Q4_K, w, 1024, 37, x, threads=7)
+    assert np.array_equal(a, b)
+
+
+def test_matvec_linear_in_x():
+    w = synth.weights(IQ2_XXS, 16, 512, 41)
+    x = synth.activations(1, 512, 42)[0]
+    a = oracle.matvec(IQ2_XXS, w, 512, 16, x)
+    b = oracle.matvec(IQ2_XXS, w, 512, 16, 2 * x)  # exact: scaling by 2
+    assert np.array_equal(2 * a, b)
+    c = oracle.matvec(IQ2_XXS, w, 512, 16, -x)
+    assert np.array_equal(-a, c)
