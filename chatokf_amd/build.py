@@ -22,6 +22,9 @@ FLAGS = [
     "-shared",
     # no packed fp32 instructions anywhere in device code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # keep private arrays in registers: LDS promotion of a prefetch buffer
+    # serialises its loads
+    "-mllvm", "-disable-promote-alloca-to-lds",
     "-Wall",
     "-Wno-unused-function",
     "-I", os.path.join(ROOT, "include"),

@@ -3,293 +3,496 @@
 // One weight pass serves all NC activation columns (the reference's
 // gemv / gemm_nb kernels, LLM/metal/Kernels.metal:1572-1753, :2486-2585).
 //
-// Work split: a 256-thread workgroup is 4 wavefronts; each wavefront owns R
-// consecutive output rows.  Lane l walks the row's 32-weight units
-// u = l, l + 64, ... so that, per load instruction, consecutive lanes read
-// consecutive bytes of every row (coalesced 16-byte loads for Q4_K, 8/16-byte
-// loads for the 2-byte-aligned formats).  The lane's activation slice is
-// loaded once per unit and reused for all R rows, then the row sums are
-// reduced across the wavefront.  Scales are factored out of the inner sums:
-// Q4_K uses (d*sc)*sum(q*x) - (dmin*m)*sum(x) per 32 weights, Q2_0 uses
-// d*(sum(code*x) - sum(x)), Q8_0 and IQ2_XXS use d * sum(q*x) per unit.
+// Layout of the work.  A wavefront is four row slots of 16 lanes; each slot
+// owns R consecutive rows.  A row is cut into units (Q4_K: one 32-byte code
+// group = sub-blocks 2g and 2g+1; IQ2_XXS: two sub-blocks; Q8_0: one block;
+// Q2_0: half a block); lane i of a slot walks units
+// i, i + 16, ... so the 16 lanes of a slot read contiguous bytes of the row
+// with 16-byte loads, and the next step's weights are loaded before the
+// current step is computed.
+//
+// Arithmetic.  The activations are staged once per workgroup into LDS as fp16,
+// permuted so that each packed pair of weights meets its pair of activations,
+// and every multiply-add is a v_dot2_f32_f16 (two fp16 products, fp32
+// accumulate).  Quantized integers become exact fp16 numbers with the
+// magic-exponent trick: 0x6400 | q is the fp16 value 1024 + q, and the
+// 1024 * sum(x) bias is removed per unit from an fp32 sum of the same fp16
+// activations.  Block scales are applied in fp32 per sub-block, in the
+// reference's factored form ((d*sc)*sum(q*x) - (dmin*m)*sum(x) for Q4_K,
+// d*sum((code-1)*x) for Q2_0, d*sum(q*x) for Q8_0, db*sum(g*s*x) for
+// IQ2_XXS).  The fp16 rounding of x is the only approximation beyond fp32
+// summation order (relative error ~2e-4 of the output scale).
 #pragma once
 #include "okf_common.h"
 #include "okf_decode.h"
 
 namespace okf {
 
-template <int NC>
-struct XSlice {
-    float v[NC][16];
+constexpr int GV_SLOTS_PER_WAVE = 4;  // row slots of 16 lanes
+constexpr int GV_LANES = 16;          // lanes per row slot
+
+// Weights per unit: 64, except Q8_0 whose unit is one 32-weight block (so
+// any K that is a whole number of blocks works).
+template <int F>
+__host__ __device__ constexpr uint32_t unit_weights() { return F == Q8_0 ? 32 : 64; }
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, a), __builtin_bit_cast(half2v, b), c,
+                                  false);
+}
+
+// v_perm_b32: byte k of the result is byte sel_k of the 8-byte value {hi, lo}.
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+    return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+// v_bfi_b32: (mask & a) | (~mask & b).  With b = MAGIC2 this drops a's masked
+// bits into the mantissa of two fp16 1024.0: bits 0..3 give 1024 + q, bits
+// 4..7 give 1024 + 16 q (the factor 16 is folded into the scale).
+// (The compiler splits the constant-operand form into v_and + v_or, so the
+// single instruction is written out; the mask lives in an SGPR, b in a VGPR.)
+__device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t a, uint32_t b) {
+    uint32_t r;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(a), "v"(b));
+    return r;
+}
+
+constexpr uint32_t MAGIC2 = 0x64006400u;  // two fp16 1024.0
+constexpr uint32_t ONES2 = 0x3C003C00u;   // two fp16 1.0
+
+// ---------------------------------------------------------------- units --
+// Raw bytes of one unit for R rows (native vector types keep them in VGPRs).
+template <int F, int R>
+struct Unit;
+template <int R>
+struct Unit<Q4_K, R> {  // 16-byte header + 32 code bytes of group g
+    u32x4 hdr[R], q0[R], q1[R];
+};
+template <int R>
+struct Unit<IQ2_XXS, R> {  // d + two sub-blocks (a0, a1, a0', a1')
+    uint32_t d[R];
+    u32x4 a[R];
+};
+template <int R>
+struct Unit<Q8_0, R> {  // one block: d + 32 code bytes (2-byte aligned)
+    uint32_t d[R];
+    u32x4 q0[R], q1[R];
+};
+template <int R>
+struct Unit<Q2_0, R> {  // d + 16 code bytes (64 codes)
+    uint32_t d[R];
+    u32x4 q[R];
 };
 
-// 16 consecutive activations of each column, starting at k.
-template <int NC>
-__device__ __forceinline__ void load_x16(const float *X, uint32_t K, uint32_t k, XSlice<NC> &xs) {
+template <int F, int R>
+__device__ __forceinline__ void load_unit(const uint8_t *const rows[R], uint32_t u, Unit<F, R> &w) {
 #pragma unroll
-    for (int n = 0; n < NC; n++) {
-        const float4 *p = (const float4 *)(X + (uint64_t)n * K + k);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            float4 t = p[i];
-            xs.v[n][4 * i + 0] = t.x;
-            xs.v[n][4 * i + 1] = t.y;
-            xs.v[n][4 * i + 2] = t.z;
-            xs.v[n][4 * i + 3] = t.w;
+    for (int r = 0; r < R; r++) {
+        if constexpr (F == Q4_K) {
+            const uint8_t *b = rows[r] + (uint64_t)(u >> 2) * 144;
+            const uint32_t g = u & 3;
+            w.hdr[r] = *(const u32x4 *)b;
+            w.q0[r] = *(const u32x4 *)(b + 16 + g * 32);
+            w.q1[r] = *(const u32x4 *)(b + 32 + g * 32);
+        } else if constexpr (F == IQ2_XXS) {
+            const uint8_t *b = rows[r] + (uint64_t)(u >> 2) * 66;
+            w.d[r] = ldu<uint16_t>(b);
+            w.a[r] = ldu<u32x4>(b + 2 + (u & 3) * 16);
+        } else if constexpr (F == Q8_0) {
+            const uint8_t *b = rows[r] + (uint64_t)u * 34;
+            w.d[r] = ldu<uint16_t>(b);
+            w.q0[r] = ldu<u32x4>(b + 2);
+            w.q1[r] = ldu<u32x4>(b + 18);
+        } else {
+            const uint8_t *b = rows[r] + (uint64_t)(u >> 1) * 34;
+            w.d[r] = ldu<uint16_t>(b);
+            w.q[r] = ldu<u32x4>(b + 2 + (u & 1) * 16);
         }
     }
 }
 
-template <int NC>
-__device__ __forceinline__ void sum_x16(const XSlice<NC> &xs, float *s) {
-#pragma unroll
-    for (int n = 0; n < NC; n++) {
-        float a = 0;
-#pragma unroll
-        for (int i = 0; i < 16; i++) a += xs.v[n][i];
-        s[n] = a;
+// Staging order.  Slot s of a unit holds 4 packed pairs (8 fp16 values) read
+// by one 16-byte LDS load; h[0..7] below are those values in memory order,
+// built from two float4s A and B of the activations.
+//  Q4_K: code dword i (bytes 4i..4i+3) gives low-nibble pairs (4i, 4i+2),
+//        (4i+1, 4i+3); so slot s (weights 8s..8s+7 of the unit, the first
+//        four slots low nibbles, the last four high nibbles) is
+//        A = x[8s..], B = x[8s+4..] as A0 A2 A1 A3 B0 B2 B1 B3.
+//  Q2_0: code dword j (16 codes, weights 16j..) gives pairs (c, c + 8); slot
+//        s = 2j + h is A = x[16j + 4h..], B = x[16j + 8 + 4h..] as
+//        A0 B0 A1 B1 A2 B2 A3 B3.
+//  Q8_0, IQ2_XXS: natural order, A = x[8s..], B = x[8s+4..].
+template <int F>
+__device__ __forceinline__ uint32_t slot_first(uint32_t s, uint32_t &second) {
+    if constexpr (F == Q2_0) {
+        const uint32_t base = 16 * (s >> 1) + 4 * (s & 1);
+        second = base + 8;
+        return base;
+    } else {
+        second = 8 * s + 4;
+        return 8 * s;
     }
 }
 
-// sum_i byte_i(q) * x_i over the 16 bytes of q (unsigned bytes).
-template <int NC>
-__device__ __forceinline__ void dot_u8x16(const uint32_t q[4], const XSlice<NC> &xs, float *s) {
-#pragma unroll
-    for (int n = 0; n < NC; n++) s[n] = 0;
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        float w = (float)byte_of(q[i >> 2], i & 3);
-#pragma unroll
-        for (int n = 0; n < NC; n++) s[n] += w * xs.v[n][i];
-    }
+__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
+    const half2v h = {(_Float16)a, (_Float16)b};
+    return __builtin_bit_cast(uint32_t, h);
 }
 
-// ---------------------------------------------------------------- Q8_0 --
+template <int F>
+__device__ __forceinline__ u32x4 slot_pack(floatx4 A, floatx4 B) {
+    if constexpr (F == Q4_K)
+        return u32x4{pack_h2(A[0], A[2]), pack_h2(A[1], A[3]), pack_h2(B[0], B[2]),
+                     pack_h2(B[1], B[3])};
+    else if constexpr (F == Q2_0)
+        return u32x4{pack_h2(A[0], B[0]), pack_h2(A[1], B[1]), pack_h2(A[2], B[2]),
+                     pack_h2(A[3], B[3])};
+    else
+        return u32x4{pack_h2(A[0], A[1]), pack_h2(A[2], A[3]), pack_h2(B[0], B[1]),
+                     pack_h2(B[2], B[3])};
+}
+
+// fp32 sum of the 8 fp16 values of a packed slot
+__device__ __forceinline__ float slot_total(u32x4 v) {
+    float t = 0;
+#pragma unroll
+    for (int e = 0; e < 4; e++) t = dot2(v[e], ONES2, t);
+    return t;
+}
+
+// LDS layout of the staged activations of one column: units in groups of 16
+// (one per lane of a slot); within a group, the unit's pairs as slots of 4
+// pairs, each slot [16 lanes][4 pairs] so a slot's 16 lanes read 256
+// contiguous bytes.  Index in uint32 (one pair).
+template <int F>
+__device__ __forceinline__ uint32_t xs_index(uint32_t u, uint32_t p) {
+    constexpr uint32_t SL = unit_weights<F>() / 8;  // slots per unit
+    const uint32_t t = u >> 4, i = u & 15;
+    return ((t * SL + (p >> 2)) * 16 + i) * 4 + (p & 3);
+}
+
+// ------------------------------------------------------------- compute --
+// acc[r][n] += unit contribution; xp = this lane's pairs of column 0 in
+// LDS (slot s at xp[s * 64]), cs = uint32 stride between columns.
+template <int F, int NC, int R>
+struct Compute;
+
 template <int NC, int R>
-__device__ __forceinline__ void unit_q8_0(const uint8_t *const rows[R], uint32_t u, const float *X,
-                                          uint32_t K, float (&acc)[R][NC]) {
-    uint32_t q[R][8];
-    float d[R];
+struct Compute<Q4_K, NC, R> {
+    // xsum: this unit's two 32-weight sums of the staged fp16 x per column
+    // (low-nibble half, high-nibble half), columns xcs floats apart.
+    __device__ __forceinline__ static void run(const Unit<Q4_K, R> &w, const uint32_t *xp, uint32_t cs,
+                                               const float *xsum, uint32_t xcs, uint32_t u,
+                                               float (&acc)[R][NC], const u32x4 *) {
+        const uint32_t g = u & 3;
+        float slo[R][NC], shi[R][NC];
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-        const uint8_t *b = rows[r] + (uint64_t)u * 34;
-        d[r] = h2f(ldu<uint16_t>(b));
-        *(uint4 *)&q[r][0] = ldu<uint4>(b + 2);
-        *(uint4 *)&q[r][4] = ldu<uint4>(b + 18);
-    }
-    float s[R][NC];
+        for (int r = 0; r < R; r++)
 #pragma unroll
-    for (int r = 0; r < R; r++)
+            for (int n = 0; n < NC; n++) slo[r][n] = shi[r][n] = 0;
 #pragma unroll
-        for (int n = 0; n < NC; n++) s[r][n] = 0;
+        for (int s = 0; s < 4; s++) {  // code dwords 2s, 2s + 1
+            u32x4 xl[NC], xh[NC];
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
-        XSlice<NC> xs;
-        load_x16<NC>(X, K, u * 32 + h * 16, xs);
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                float w = (float)(int)(int8_t)byte_of(q[r][h * 4 + (i >> 2)], i & 3);
-#pragma unroll
-                for (int n = 0; n < NC; n++) s[r][n] += w * xs.v[n][i];
+            for (int n = 0; n < NC; n++) {
+                xl[n] = *(const u32x4 *)(xp + n * cs + s * 64);
+                xh[n] = *(const u32x4 *)(xp + n * cs + (4 + s) * 64);
             }
-        }
-    }
 #pragma unroll
-    for (int r = 0; r < R; r++)
+            for (int r = 0; r < R; r++) {
 #pragma unroll
-        for (int n = 0; n < NC; n++) acc[r][n] += d[r] * s[r][n];
-}
-
-// ---------------------------------------------------------------- Q2_0 --
-template <int NC, int R>
-__device__ __forceinline__ void unit_q2_0(const uint8_t *const rows[R], uint32_t u, const float *X,
-                                          uint32_t K, float (&acc)[R][NC]) {
-    uint2 q[R];
-    float d[R];
+                for (int h = 0; h < 2; h++) {
+                    const uint32_t v = (2 * s + h < 4) ? w.q0[r][2 * s + h] : w.q1[r][2 * s + h - 4];
+                    const uint32_t v8 = v >> 8;
+                    // low nibbles of bytes (0, 2) and (1, 3): 1024 + q
+                    const uint32_t l02 = bfi(0x000F000Fu, v, MAGIC2);
+                    const uint32_t l13 = bfi(0x000F000Fu, v8, MAGIC2);
+                    // high nibbles: 1024 + 16 q
+                    const uint32_t h02 = bfi(0x00F000F0u, v, MAGIC2);
+                    const uint32_t h13 = bfi(0x00F000F0u, v8, MAGIC2);
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-        const uint8_t *b = rows[r] + (uint64_t)(u >> 2) * 34;
-        d[r] = h2f(ldu<uint16_t>(b));
-        q[r] = ldu<uint2>(b + 2 + (u & 3) * 8);
-    }
-    float s[R][NC], sx[NC];
-#pragma unroll
-    for (int n = 0; n < NC; n++) sx[n] = 0;
-#pragma unroll
-    for (int r = 0; r < R; r++)
-#pragma unroll
-        for (int n = 0; n < NC; n++) s[r][n] = 0;
-#pragma unroll
-    for (int h = 0; h < 2; h++) {
-        XSlice<NC> xs;
-        load_x16<NC>(X, K, u * 32 + h * 16, xs);
-        float t[NC];
-        sum_x16<NC>(xs, t);
-#pragma unroll
-        for (int n = 0; n < NC; n++) sx[n] += t[n];
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            uint32_t dw = h ? q[r].y : q[r].x;
-            // codes 2i of the 4 bytes land at byte positions: expand by masks
-            uint32_t c0 = dw & 0x03030303u, c1 = (dw >> 2) & 0x03030303u;
-            uint32_t c2 = (dw >> 4) & 0x03030303u, c3 = (dw >> 6) & 0x03030303u;
-            uint32_t cs[4] = {c0, c1, c2, c3};
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                // weight i: byte i>>2, code position i&3
-                float w = (float)byte_of(cs[i & 3], i >> 2);
-#pragma unroll
-                for (int n = 0; n < NC; n++) s[r][n] += w * xs.v[n][i];
-            }
-        }
-    }
-#pragma unroll
-    for (int r = 0; r < R; r++)
-#pragma unroll
-        for (int n = 0; n < NC; n++) acc[r][n] += d[r] * (s[r][n] - sx[n]);
-}
-
-// ---------------------------------------------------------------- Q4_K --
-// Unit u = 16-byte code chunk c = u & 7 of superblock u >> 3: its low nibbles
-// are weights 64g + 16h + i of sub-block 2g, its high nibbles weights
-// 64g + 32 + 16h + i of sub-block 2g + 1 (g = c >> 1, h = c & 1).
-template <int NC, int R>
-__device__ __forceinline__ void unit_q4_k(const uint8_t *const rows[R], uint32_t u, const float *X,
-                                          uint32_t K, float (&acc)[R][NC]) {
-    uint32_t sb = u >> 3, c = u & 7, g = c >> 1, h = c & 1;
-    uint4 hdr[R], qv[R];
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        const uint8_t *b = rows[r] + (uint64_t)sb * 144;
-        hdr[r] = *(const uint4 *)b;
-        qv[r] = *(const uint4 *)(b + 16 + c * 16);
-    }
-    uint32_t k0 = sb * 256 + g * 64 + h * 16;
-    float slo[R][NC], shi[R][NC], xlo[NC], xhi[NC];
-    {
-        XSlice<NC> xs;
-        load_x16<NC>(X, K, k0, xs);
-        sum_x16<NC>(xs, xlo);
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            uint32_t q[4] = {qv[r].x & 0x0F0F0F0Fu, qv[r].y & 0x0F0F0F0Fu, qv[r].z & 0x0F0F0F0Fu,
-                             qv[r].w & 0x0F0F0F0Fu};
-            dot_u8x16<NC>(q, xs, slo[r]);
-        }
-    }
-    {
-        XSlice<NC> xs;
-        load_x16<NC>(X, K, k0 + 32, xs);
-        sum_x16<NC>(xs, xhi);
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            uint32_t q[4] = {(qv[r].x >> 4) & 0x0F0F0F0Fu, (qv[r].y >> 4) & 0x0F0F0F0Fu,
-                             (qv[r].z >> 4) & 0x0F0F0F0Fu, (qv[r].w >> 4) & 0x0F0F0F0Fu};
-            dot_u8x16<NC>(q, xs, shi[r]);
-        }
-    }
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        uint32_t sc0, mn0, sc1, mn1;
-        q4k_scale_min_pair(hdr[r], g, sc0, mn0, sc1, mn1);
-        float d = h2f(hdr[r].x & 0xFFFF), dmin = h2f(hdr[r].x >> 16);
-        float a0 = d * (float)sc0, a1 = d * (float)sc1;
-        float b0 = dmin * (float)mn0, b1 = dmin * (float)mn1;
-#pragma unroll
-        for (int n = 0; n < NC; n++)
-            acc[r][n] += (a0 * slo[r][n] + a1 * shi[r][n]) - (b0 * xlo[n] + b1 * xhi[n]);
-    }
-}
-
-// ------------------------------------------------------------- IQ2_XXS --
-template <int NC, int R>
-__device__ __forceinline__ void unit_iq2_xxs(const uint8_t *const rows[R], uint32_t u,
-                                             const float *X, uint32_t K, float (&acc)[R][NC],
-                                             const uint2 *grid) {
-    uint2 a[R];
-    float d[R];
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        const uint8_t *b = rows[r] + (uint64_t)(u >> 3) * 66;
-        d[r] = h2f(ldu<uint16_t>(b));
-        a[r] = ldu<uint2>(b + 2 + (u & 7) * 8);
-    }
-    float s[R][NC];
-#pragma unroll
-    for (int r = 0; r < R; r++)
-#pragma unroll
-        for (int n = 0; n < NC; n++) s[r][n] = 0;
-#pragma unroll
-    for (int h = 0; h < 2; h++) {
-        XSlice<NC> xs;
-        load_x16<NC>(X, K, u * 32 + h * 16, xs);
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-#pragma unroll
-            for (int ll = 0; ll < 2; ll++) {
-                int l = 2 * h + ll;
-                uint2 e = grid[byte_of(a[r].x, l)];
-                uint32_t sg = iq2_signs((a[r].y >> (7 * l)) & 127);
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    float gv = (float)byte_of(j < 4 ? e.x : e.y, j & 3);
-                    // the sign goes into the weight's sign bit
-                    gv = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, gv) ^ (((sg >> j) & 1u) << 31));
-#pragma unroll
-                    for (int n = 0; n < NC; n++) s[r][n] += gv * xs.v[n][ll * 8 + j];
+                    for (int n = 0; n < NC; n++) {
+                        slo[r][n] = dot2(l02, xl[n][2 * h], slo[r][n]);
+                        slo[r][n] = dot2(l13, xl[n][2 * h + 1], slo[r][n]);
+                        shi[r][n] = dot2(h02, xh[n][2 * h], shi[r][n]);
+                        shi[r][n] = dot2(h13, xh[n][2 * h + 1], shi[r][n]);
+                    }
                 }
             }
         }
-    }
+        float xlo[NC], xhi[NC];
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-        float db = d[r] * (0.5f + (float)(a[r].y >> 28)) * 0.25f;
+        for (int n = 0; n < NC; n++) {
+            const float2 t = *(const float2 *)(xsum + n * xcs);
+            xlo[n] = t.x;
+            xhi[n] = t.y;
+        }
 #pragma unroll
-        for (int n = 0; n < NC; n++) acc[r][n] += db * s[r][n];
+        for (int r = 0; r < R; r++) {
+            uint32_t sc0, mn0, sc1, mn1;
+            const uint4 hv = make_uint4(w.hdr[r][0], w.hdr[r][1], w.hdr[r][2], w.hdr[r][3]);
+            q4k_scale_min_pair(hv, g, sc0, mn0, sc1, mn1);
+            const float d = h2f(w.hdr[r][0] & 0xFFFF), dmin = h2f(w.hdr[r][0] >> 16);
+            const float a0 = d * (float)sc0, a1 = d * (float)sc1;
+            // bias: sum((1024 + q) x) = sum(q x) + 1024 sum(x); the high
+            // nibbles carry an extra factor 16
+            const float b0 = 1024.0f * a0 + dmin * (float)mn0;
+            const float b1 = 64.0f * a1 + dmin * (float)mn1;
+            const float a1s = 0.0625f * a1;
+#pragma unroll
+            for (int n = 0; n < NC; n++)
+                acc[r][n] += (a0 * slo[r][n] + a1s * shi[r][n]) - (b0 * xlo[n] + b1 * xhi[n]);
+        }
     }
+};
+
+template <int NC, int R>
+struct Compute<IQ2_XXS, NC, R> {
+    // tab: [0, 256) fp16 grid entries (8 halves), [256, 384) sign masks
+    // (fp16 sign bits of the 8 weights, the eighth from the parity rule).
+    __device__ __forceinline__ static void run(const Unit<IQ2_XXS, R> &w, const uint32_t *xp,
+                                               uint32_t cs, const float *, uint32_t, uint32_t,
+                                               float (&acc)[R][NC], const u32x4 *tab) {
+#pragma unroll
+        for (int sb = 0; sb < 2; sb++) {  // the unit's two sub-blocks
+            float s[R][NC];
+#pragma unroll
+            for (int r = 0; r < R; r++)
+#pragma unroll
+                for (int n = 0; n < NC; n++) s[r][n] = 0;
+#pragma unroll
+            for (int l = 0; l < 4; l++) {  // 8-weight groups
+                u32x4 xv[NC];
+#pragma unroll
+                for (int n = 0; n < NC; n++) {
+                    // pairs 16 sb + 4 l .. +4 = slot 4 sb + l
+                    xv[n] = *(const u32x4 *)(xp + n * cs + (4 * sb + l) * 64);
+                }
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const uint32_t a0 = w.a[r][2 * sb], a1 = w.a[r][2 * sb + 1];
+                    const u32x4 gv = tab[(a0 >> (8 * l)) & 0xFF];
+                    const u32x4 sg = tab[256 + ((a1 >> (7 * l)) & 127)];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const uint32_t wv = gv[e] ^ sg[e];
+#pragma unroll
+                        for (int n = 0; n < NC; n++) s[r][n] = dot2(wv, xv[n][e], s[r][n]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const uint32_t a1 = w.a[r][2 * sb + 1];
+                const float db = h2f(w.d[r]) * (0.5f + (float)(a1 >> 28)) * 0.25f;
+#pragma unroll
+                for (int n = 0; n < NC; n++) acc[r][n] += db * s[r][n];
+            }
+        }
+    }
+};
+
+template <int NC, int R>
+struct Compute<Q8_0, NC, R> {
+    // Code byte j is byte j & 3 of code dword j >> 2; XOR 0x80 turns int8 q
+    // into q + 128, so the fp16 0x64 | (q + 128) is 1152 + q.
+    __device__ __forceinline__ static void run(const Unit<Q8_0, R> &w, const uint32_t *xp, uint32_t cs,
+                                               const float *xsp, uint32_t xcs, uint32_t,
+                                               float (&acc)[R][NC], const u32x4 *) {
+        float xsum[NC], s[R][NC];
+#pragma unroll
+        for (int n = 0; n < NC; n++) xsum[n] = xsp[n * xcs];
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int n = 0; n < NC; n++) s[r][n] = 0;
+#pragma unroll
+        for (int sl = 0; sl < 4; sl++) {  // pairs 4 sl .. 4 sl + 3 = code dwords 2 sl, 2 sl + 1
+            u32x4 xv[NC];
+#pragma unroll
+            for (int n = 0; n < NC; n++) {
+                xv[n] = *(const u32x4 *)(xp + n * cs + sl * 64);
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int dwi = 2 * sl + (e >> 1);
+                    const uint32_t dw = (dwi < 4 ? w.q0[r][dwi] : w.q1[r][dwi - 4]) ^ 0x80808080u;
+                    // selector bytes 0..3 address dw, 4 addresses 0x64
+                    const uint32_t hv = perm(0x64646464u, dw, (e & 1) ? 0x04030402u : 0x04010400u);
+#pragma unroll
+                    for (int n = 0; n < NC; n++) s[r][n] = dot2(hv, xv[n][e], s[r][n]);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const float d = h2f(w.d[r]);
+#pragma unroll
+            for (int n = 0; n < NC; n++) acc[r][n] += d * (s[r][n] - 1152.0f * xsum[n]);
+        }
+    }
+};
+
+template <int NC, int R>
+struct Compute<Q2_0, NC, R> {
+    __device__ __forceinline__ static void run(const Unit<Q2_0, R> &w, const uint32_t *xp, uint32_t cs,
+                                               const float *xsp, uint32_t xcs, uint32_t,
+                                               float (&acc)[R][NC], const u32x4 *) {
+        float xsum[NC], s[R][NC];
+#pragma unroll
+        for (int n = 0; n < NC; n++) {
+            const float2 t = *(const float2 *)(xsp + n * xcs);
+            xsum[n] = t.x + t.y;
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int n = 0; n < NC; n++) s[r][n] = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {  // code dword j: pairs 8j .. 8j + 7 = slots 2j, 2j + 1
+            u32x4 xa[NC], xb[NC];
+#pragma unroll
+            for (int n = 0; n < NC; n++) {
+                xa[n] = *(const u32x4 *)(xp + n * cs + (2 * j) * 64);
+                xb[n] = *(const u32x4 *)(xp + n * cs + (2 * j + 1) * 64);
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const uint32_t v = w.q[r][j];
+#pragma unroll
+                for (int c = 0; c < 8; c++) {
+                    // codes c and c + 8 of the dword -> fp16 (1024 + code)
+                    const uint32_t hv = ((v >> (2 * c)) & 0x00030003u) | MAGIC2;
+#pragma unroll
+                    for (int n = 0; n < NC; n++)
+                        s[r][n] = dot2(hv, c < 4 ? xa[n][c] : xb[n][c - 4], s[r][n]);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const float d = h2f(w.d[r]);
+            // sum((code - 1) x) = sum((1024 + code) x) - 1025 sum(x)
+#pragma unroll
+            for (int n = 0; n < NC; n++) acc[r][n] += d * (s[r][n] - 1025.0f * xsum[n]);
+        }
+    }
+};
+
+// Sum over the 16 lanes of a row slot (every lane of the slot gets it).
+__device__ __forceinline__ float slot_sum(float v) {
+    v += __shfl_xor(v, 1, 64);
+    v += __shfl_xor(v, 2, 64);
+    v += __shfl_xor(v, 4, 64);
+    v += __shfl_xor(v, 8, 64);
+    return v;
 }
 
 // ------------------------------------------------------------- kernel --
-template <int F, int NC, int R>
+// Dynamic LDS: [IQ2 tables (384 x 16 B)], then NC columns of staged pairs for
+// `cunits` units (a multiple of 16), column stride cs = cunits * UW / 2
+// uint32, then NC columns of 32-weight sums of the staged x (cunits * UW / 32
+// floats each).
+template <int F, int NC, int R, int D>
 __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t *__restrict__ W, uint64_t row_bytes,
                                                    uint32_t K, uint32_t M,
                                                    const float *__restrict__ X,
                                                    float *__restrict__ Y,
-                                                   const uint2 *__restrict__ grid_g) {
-    __shared__ uint2 grid[F == IQ2_XXS ? 256 : 1];
-    if constexpr (F == IQ2_XXS) {
-        grid[threadIdx.x] = grid_g[threadIdx.x];
-        __syncthreads();
-    }
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t m0 = (blockIdx.x * 4 + wave) * R;
-    if (m0 >= M) return;
+                                                   const u32x4 *__restrict__ tab_g,
+                                                   uint32_t cunits) {
+    extern __shared__ u32x4 lds[];
+    constexpr uint32_t TAB = F == IQ2_XXS ? 384 : 0;
+    u32x4 *tab = lds;
+    uint32_t *xs = (uint32_t *)(lds + TAB);
+    const uint32_t tid = threadIdx.x, nthr = blockDim.x;
+    const uint32_t lane = tid & 63, i = lane & 15, slot = lane >> 4;
+    const uint32_t wave = tid >> 6, waves = nthr >> 6;
+    if constexpr (F == IQ2_XXS)
+        for (uint32_t e = tid; e < TAB; e += nthr) tab[e] = tab_g[e];
+
+    const uint32_t m0 = ((blockIdx.x * waves + wave) * GV_SLOTS_PER_WAVE + slot) * R;
     const uint8_t *rows[R];
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-        uint32_t m = m0 + r < M ? m0 + r : M - 1;  // clamp: result discarded
-        rows[r] = W + (uint64_t)m * row_bytes;
-    }
+    for (int r = 0; r < R; r++) rows[r] = W + (uint64_t)min(m0 + r, M - 1) * row_bytes;
+    const bool live = m0 < M;  // dead slots still stage activations
+    constexpr uint32_t UW = unit_weights<F>();
+    const uint32_t units = K / UW, cs = cunits * (UW / 2), xcs = cunits * (UW / 32);
+    float *xsum = (float *)(xs + NC * cs);
+
     float acc[R][NC];
 #pragma unroll
     for (int r = 0; r < R; r++)
 #pragma unroll
         for (int n = 0; n < NC; n++) acc[r][n] = 0;
-    const uint32_t units = K / 32;
-    for (uint32_t u = lane; u < units; u += 64) {
-        if constexpr (F == Q8_0) unit_q8_0<NC, R>(rows, u, X, K, acc);
-        else if constexpr (F == Q2_0) unit_q2_0<NC, R>(rows, u, X, K, acc);
-        else if constexpr (F == Q4_K) unit_q4_k<NC, R>(rows, u, X, K, acc);
-        else unit_iq2_xxs<NC, R>(rows, u, X, K, acc, grid);
+
+    for (uint32_t c0 = 0; c0 < units; c0 += cunits) {
+        const uint32_t cn = min(cunits, units - c0);
+        const uint32_t steps = (cn + GV_LANES - 1) / GV_LANES, last = cn - 1;
+        // The first D steps' weights are requested before the activations are
+        // staged, so their latency overlaps the staging.  Every load is
+        // unconditional (past the end it re-reads the chunk's last unit, an
+        // L2 hit) so that no branch hides a load from the compiler's count of
+        // outstanding loads, and the wait before a compute covers only the
+        // loads of that buffer.
+        Unit<F, R> buf[D];
+#pragma unroll
+        for (int j = 0; j < D; j++) load_unit<F, R>(rows, c0 + min(i + GV_LANES * j, last), buf[j]);
+
+        // stage units [c0, c0 + cn) of every column as fp16 pairs
+        __syncthreads();
+        // one thread per 8-value slot; 4 consecutive slots (one 32-weight
+        // group) sit in 4 consecutive lanes of a wavefront (nthr % 64 == 0)
+        constexpr uint32_t SL = UW / 8;
+        const uint32_t nslots = cn * SL;
+        for (uint32_t q0 = 0; q0 < nslots; q0 += nthr) {
+            const uint32_t q = q0 + tid, u = q / SL, sidx = q % SL;
+            const bool in = q < nslots;
+            uint32_t kb;
+            const uint32_t ka = slot_first<F>(sidx, kb);
+#pragma unroll
+            for (int n = 0; n < NC; n++) {
+                const float *xb = X + (uint64_t)n * K + (uint64_t)(c0 + u) * UW;
+                floatx4 A = {0, 0, 0, 0}, B = {0, 0, 0, 0};
+                if (in) {
+                    A = *(const floatx4 *)(xb + ka);
+                    B = *(const floatx4 *)(xb + kb);
+                }
+                const u32x4 v = slot_pack<F>(A, B);
+                float part = slot_total(v);
+                part += __shfl_xor(part, 1, 64);
+                part += __shfl_xor(part, 2, 64);
+                if (in) {
+                    *(u32x4 *)(xs + n * cs + xs_index<F>(u, 4 * sidx)) = v;
+                    if ((q & 3) == 0) xsum[n * xcs + q / 4] = part;
+                }
+            }
+        }
+        __syncthreads();
+        if (!live) continue;
+        // stream the chunk's units u = c0 + i + 16 t through a ring of D
+        // register buffers
+        for (uint32_t t = 0; t < steps; t += D) {
+#pragma unroll
+            for (int j = 0; j < D; j++) {
+                const uint32_t u = i + GV_LANES * (t + j);
+                if (u < cn)
+                    Compute<F, NC, R>::run(buf[j], xs + xs_index<F>(u, 0), cs, xsum + u * (UW / 32),
+                                           xcs, c0 + u, acc, tab);
+                load_unit<F, R>(rows, c0 + min(u + GV_LANES * D, last), buf[j]);
+            }
+        }
     }
+    if (!live) return;
 #pragma unroll
     for (int r = 0; r < R; r++)
 #pragma unroll
         for (int n = 0; n < NC; n++) {
-            float v = wave_sum(acc[r][n]);
-            if (lane == 0 && m0 + r < M) Y[(uint64_t)n * M + m0 + r] = v;
+            const float v = slot_sum(acc[r][n]);
+            if (i == 0 && m0 + r < M) Y[(uint64_t)n * M + m0 + r] = v;
         }
 }
 

@@ -9,6 +9,7 @@
 
 #include <atomic>
 #include <cstdint>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 
@@ -24,6 +25,12 @@ struct okf_ctx {
     int device = -1;
     hipStream_t stream = nullptr;
     uint2 *grid = nullptr;  // 256 IQ2_XXS grid entries in device memory
+    okf::u32x4 *tab = nullptr;   // IQ2_XXS fp16 grid (256 x 8 halves) + sign masks (128)
+    size_t max_lds = 65536;  // dynamic LDS a workgroup may use
+    // matvec tuning (defaults chosen per shape; OKF_GEMV_* environment
+    // variables override them for measurements)
+    int gemv_r = 0;      // rows per row slot (0 = auto)
+    int gemv_waves = 0;  // wavefronts per workgroup (0 = auto)
     double fault_rate = 0;
     uint64_t fault_state = 0;
     int last_hip = 0;
@@ -76,22 +83,59 @@ int finish(okf_ctx *c) {
     return e == hipSuccess ? OKF_OK : hip_fail(c, e);
 }
 
+// IQ2_XXS tables the matvec keeps in LDS: the grid as fp16 (entry e = 8
+// halves, two per dword) and, per 7-bit sign index, the fp16 sign bits of the
+// eight weights (the eighth from the even-parity rule of ksigns,
+// LLM/Quantize/IQ2Grid.swift:73).
+void build_iq2_tables(uint32_t *t) {
+    for (int e = 0; e < 256; e++) {
+        const uint64_t g = okf_iq2xxs_grid_host[e];
+        for (int j = 0; j < 4; j++) {
+            const _Float16 a = (_Float16)(float)((g >> (16 * j)) & 0xFF);
+            const _Float16 b = (_Float16)(float)((g >> (16 * j + 8)) & 0xFF);
+            t[e * 4 + j] = (uint32_t)__builtin_bit_cast(uint16_t, a) |
+                           ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+        }
+    }
+    for (int s7 = 0; s7 < 128; s7++) {
+        const uint32_t s = s7 | ((__builtin_popcount(s7) & 1u) << 7);
+        for (int j = 0; j < 4; j++)
+            t[(256 + s7) * 4 + j] = (((s >> (2 * j)) & 1u) << 15) | (((s >> (2 * j + 1)) & 1u) << 31);
+    }
+}
+
+template <int F, int NC, int R>
+void launch_gemv_r(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t M, const float *X,
+                   float *Y, uint32_t waves, uint32_t cunits, size_t lds) {
+    constexpr int D = 4;       // register buffers in flight per lane
+    static bool attr = false;  // one attribute call per instantiation
+    if (!attr) {
+        (void)hipFuncSetAttribute((const void *)gemv_kernel<F, NC, R, D>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)c->max_lds);
+        attr = true;
+    }
+    const uint32_t rows_per_wg = waves * GV_SLOTS_PER_WAVE * R;
+    dim3 grid((M + rows_per_wg - 1) / rows_per_wg);
+    hipLaunchKernelGGL((gemv_kernel<F, NC, R, D>), grid, dim3(64 * waves), lds, c->stream, W, rb, K,
+                       M, X, Y, c->tab, cunits);
+}
+
 template <int F, int NC>
 void launch_gemv_nc(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t M,
                     const float *X, float *Y) {
-    // Two rows per wavefront when there are rows to spare, else one, so small
-    // M still spreads over the 256 CUs.
-    if (M >= 4096) {
-        constexpr int R = 2;
-        dim3 grid((M + 4 * R - 1) / (4 * R));
-        hipLaunchKernelGGL((gemv_kernel<F, NC, R>), grid, dim3(256), 0, c->stream, W, rb, K, M, X, Y,
-                           c->grid);
-    } else {
-        constexpr int R = 1;
-        dim3 grid((M + 4 * R - 1) / (4 * R));
-        hipLaunchKernelGGL((gemv_kernel<F, NC, R>), grid, dim3(256), 0, c->stream, W, rb, K, M, X, Y,
-                           c->grid);
-    }
+    constexpr uint32_t UW = unit_weights<F>();
+    const size_t tab = F == IQ2_XXS ? 384 * 16 : 0;
+    const uint32_t units = K / UW;
+    // stage all of x when it fits, else in chunks of 16-unit groups
+    const size_t per_unit = (size_t)NC * (UW * 2 + UW / 32 * 4);
+    uint32_t cunits = (units + 15) / 16 * 16;
+    const size_t budget = c->max_lds - tab;
+    if (cunits * per_unit > budget) cunits = (uint32_t)(budget / per_unit) / 16 * 16;
+    const size_t lds = tab + cunits * per_unit;
+    int R = c->gemv_r ? c->gemv_r : (NC == 1 && M >= 8192 ? 2 : 1);
+    uint32_t waves = c->gemv_waves ? (uint32_t)c->gemv_waves : 4;
+    if (R >= 2) launch_gemv_r<F, NC, 2>(c, W, rb, K, M, X, Y, waves, cunits, lds);
+    else launch_gemv_r<F, NC, 1>(c, W, rb, K, M, X, Y, waves, cunits, lds);
 }
 
 template <int F>
@@ -167,12 +211,23 @@ int okf_ctx_create(int device, okf_ctx **out) {
         if (e == hipSuccess)
             e = hipMemcpy(c->grid, okf_iq2xxs_grid_host, sizeof(okf_iq2xxs_grid_host),
                           hipMemcpyHostToDevice);
+        uint32_t tabh[384 * 4];
+        build_iq2_tables(tabh);
+        if (e == hipSuccess) e = hipMalloc((void **)&c->tab, sizeof(tabh));
+        if (e == hipSuccess) e = hipMemcpy(c->tab, tabh, sizeof(tabh), hipMemcpyHostToDevice);
         if (e != hipSuccess) {
             if (c->grid) (void)hipFree(c->grid);
+            if (c->tab) (void)hipFree(c->tab);
             if (c->stream) (void)hipStreamDestroy(c->stream);
             delete c;
             return OKF_E_HIP;
         }
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, device) ==
+                hipSuccess && v > 0)
+            c->max_lds = (size_t)v;
+        if (const char *e = getenv("OKF_GEMV_R")) c->gemv_r = atoi(e);
+        if (const char *e = getenv("OKF_GEMV_WAVES")) c->gemv_waves = atoi(e);
     } else if (device != -1) {
         delete c;
         return OKF_E_ARG;
@@ -188,6 +243,7 @@ int okf_ctx_destroy(okf_ctx *c) {
         (void)hipSetDevice(c->device);
         if (hipStreamSynchronize(c->stream) != hipSuccess) st = OKF_E_HIP;
         (void)hipFree(c->grid);
+        (void)hipFree(c->tab);
         (void)hipStreamDestroy(c->stream);
     }
     delete c;
