@@ -3,13 +3,13 @@
 // One weight pass serves all NC activation columns (the reference's
 // gemv / gemm_nb kernels, LLM/metal/Kernels.metal:1572-1753, :2486-2585).
 //
-// Layout of the work.  A wavefront is four row slots of 16 lanes; each slot
-// owns R consecutive rows.  A row is cut into units (Q4_K: one 32-byte code
+// Layout of the work.  A wavefront is 64 / L row slots of L lanes (L = 16 or
+// 64); each slot owns R consecutive rows.  A row is cut into units (Q4_K: one 32-byte code
 // group = sub-blocks 2g and 2g+1; IQ2_XXS: two sub-blocks; Q8_0: one block;
 // Q2_0: half a block); lane i of a slot walks units
-// i, i + 16, ... so the 16 lanes of a slot read contiguous bytes of the row
-// with 16-byte loads, and the next step's weights are loaded before the
-// current step is computed.
+// i, i + L, ... so the lanes of a slot read contiguous bytes of the row with
+// 16-byte loads, and the weights of the next D steps are in flight while a
+// step is computed.
 //
 // Arithmetic.  The activations are staged once per workgroup into LDS as fp16,
 // permuted so that each packed pair of weights meets its pair of activations,
@@ -28,8 +28,6 @@
 
 namespace okf {
 
-constexpr int GV_SLOTS_PER_WAVE = 4;  // row slots of 16 lanes
-constexpr int GV_LANES = 16;          // lanes per row slot
 
 // Weights per unit: 64, except Q8_0 whose unit is one 32-weight block (so
 // any K that is a whole number of blocks works).
@@ -162,15 +160,15 @@ __device__ __forceinline__ float slot_total(u32x4 v) {
     return t;
 }
 
-// LDS layout of the staged activations of one column: units in groups of 16
-// (one per lane of a slot); within a group, the unit's pairs as slots of 4
-// pairs, each slot [16 lanes][4 pairs] so a slot's 16 lanes read 256
-// contiguous bytes.  Index in uint32 (one pair).
-template <int F>
+// LDS layout of the staged activations of one column: units in groups of L
+// (one per lane of a row slot); within a group, the unit's pairs as slots of
+// 4 pairs, each slot [L lanes][4 pairs] so a row slot's lanes read contiguous
+// bytes.  Index in uint32 (one pair).
+template <int F, int L>
 __device__ __forceinline__ uint32_t xs_index(uint32_t u, uint32_t p) {
     constexpr uint32_t SL = unit_weights<F>() / 8;  // slots per unit
-    const uint32_t t = u >> 4, i = u & 15;
-    return ((t * SL + (p >> 2)) * 16 + i) * 4 + (p & 3);
+    const uint32_t t = u / L, i = u % L;
+    return ((t * SL + (p >> 2)) * L + i) * 4 + (p & 3);
 }
 
 // ------------------------------------------------------------- compute --
@@ -183,7 +181,7 @@ template <int NC, int R>
 struct Compute<Q4_K, NC, R> {
     // xsum: this unit's two 32-weight sums of the staged fp16 x per column
     // (low-nibble half, high-nibble half), columns xcs floats apart.
-    __device__ __forceinline__ static void run(const Unit<Q4_K, R> &w, const uint32_t *xp, uint32_t cs,
+    __device__ __forceinline__ static void run(const Unit<Q4_K, R> &w, const uint32_t *xp, uint32_t ss, uint32_t cs,
                                                const float *xsum, uint32_t xcs, uint32_t u,
                                                float (&acc)[R][NC], const u32x4 *) {
         const uint32_t g = u & 3;
@@ -197,8 +195,8 @@ struct Compute<Q4_K, NC, R> {
             u32x4 xl[NC], xh[NC];
 #pragma unroll
             for (int n = 0; n < NC; n++) {
-                xl[n] = *(const u32x4 *)(xp + n * cs + s * 64);
-                xh[n] = *(const u32x4 *)(xp + n * cs + (4 + s) * 64);
+                xl[n] = *(const u32x4 *)(xp + n * cs + s * ss);
+                xh[n] = *(const u32x4 *)(xp + n * cs + (4 + s) * ss);
             }
 #pragma unroll
             for (int r = 0; r < R; r++) {
@@ -252,7 +250,7 @@ template <int NC, int R>
 struct Compute<IQ2_XXS, NC, R> {
     // tab: [0, 256) fp16 grid entries (8 halves), [256, 384) sign masks
     // (fp16 sign bits of the 8 weights, the eighth from the parity rule).
-    __device__ __forceinline__ static void run(const Unit<IQ2_XXS, R> &w, const uint32_t *xp,
+    __device__ __forceinline__ static void run(const Unit<IQ2_XXS, R> &w, const uint32_t *xp, uint32_t ss,
                                                uint32_t cs, const float *, uint32_t, uint32_t,
                                                float (&acc)[R][NC], const u32x4 *tab) {
 #pragma unroll
@@ -268,7 +266,7 @@ struct Compute<IQ2_XXS, NC, R> {
 #pragma unroll
                 for (int n = 0; n < NC; n++) {
                     // pairs 16 sb + 4 l .. +4 = slot 4 sb + l
-                    xv[n] = *(const u32x4 *)(xp + n * cs + (4 * sb + l) * 64);
+                    xv[n] = *(const u32x4 *)(xp + n * cs + (4 * sb + l) * ss);
                 }
 #pragma unroll
                 for (int r = 0; r < R; r++) {
@@ -298,7 +296,7 @@ template <int NC, int R>
 struct Compute<Q8_0, NC, R> {
     // Code byte j is byte j & 3 of code dword j >> 2; XOR 0x80 turns int8 q
     // into q + 128, so the fp16 0x64 | (q + 128) is 1152 + q.
-    __device__ __forceinline__ static void run(const Unit<Q8_0, R> &w, const uint32_t *xp, uint32_t cs,
+    __device__ __forceinline__ static void run(const Unit<Q8_0, R> &w, const uint32_t *xp, uint32_t ss, uint32_t cs,
                                                const float *xsp, uint32_t xcs, uint32_t,
                                                float (&acc)[R][NC], const u32x4 *) {
         float xsum[NC], s[R][NC];
@@ -313,7 +311,7 @@ struct Compute<Q8_0, NC, R> {
             u32x4 xv[NC];
 #pragma unroll
             for (int n = 0; n < NC; n++) {
-                xv[n] = *(const u32x4 *)(xp + n * cs + sl * 64);
+                xv[n] = *(const u32x4 *)(xp + n * cs + sl * ss);
             }
 #pragma unroll
             for (int r = 0; r < R; r++) {
@@ -339,7 +337,7 @@ struct Compute<Q8_0, NC, R> {
 
 template <int NC, int R>
 struct Compute<Q2_0, NC, R> {
-    __device__ __forceinline__ static void run(const Unit<Q2_0, R> &w, const uint32_t *xp, uint32_t cs,
+    __device__ __forceinline__ static void run(const Unit<Q2_0, R> &w, const uint32_t *xp, uint32_t ss, uint32_t cs,
                                                const float *xsp, uint32_t xcs, uint32_t,
                                                float (&acc)[R][NC], const u32x4 *) {
         float xsum[NC], s[R][NC];
@@ -357,8 +355,8 @@ struct Compute<Q2_0, NC, R> {
             u32x4 xa[NC], xb[NC];
 #pragma unroll
             for (int n = 0; n < NC; n++) {
-                xa[n] = *(const u32x4 *)(xp + n * cs + (2 * j) * 64);
-                xb[n] = *(const u32x4 *)(xp + n * cs + (2 * j + 1) * 64);
+                xa[n] = *(const u32x4 *)(xp + n * cs + (2 * j) * ss);
+                xb[n] = *(const u32x4 *)(xp + n * cs + (2 * j + 1) * ss);
             }
 #pragma unroll
             for (int r = 0; r < R; r++) {
@@ -383,45 +381,52 @@ struct Compute<Q2_0, NC, R> {
     }
 };
 
-// Sum over the 16 lanes of a row slot (every lane of the slot gets it).
+// Sum over the L lanes of a row slot (every lane of the slot gets it).
+template <int L>
 __device__ __forceinline__ float slot_sum(float v) {
-    v += __shfl_xor(v, 1, 64);
-    v += __shfl_xor(v, 2, 64);
-    v += __shfl_xor(v, 4, 64);
-    v += __shfl_xor(v, 8, 64);
+#pragma unroll
+    for (int o = 1; o < L; o <<= 1) v += __shfl_xor(v, o, 64);
     return v;
 }
 
 // ------------------------------------------------------------- kernel --
+// A wavefront is four row slots of L = 16 lanes; each slot owns R consecutive
+// rows.  The S parts of a workgroup's wavefronts (S = 1, 2 or 4) share the
+// same rows and take every S-th step of K, so that short or few rows still
+// give many short wavefronts; their partial sums meet in LDS.  D register
+// buffers per lane hold the weights of the wavefront's next D steps.
+//
 // Dynamic LDS: [IQ2 tables (384 x 16 B)], then NC columns of staged pairs for
-// `cunits` units (a multiple of 16), column stride cs = cunits * UW / 2
+// `cunits` units (a multiple of 64), column stride cs = cunits * UW / 2
 // uint32, then NC columns of 32-weight sums of the staged x (cunits * UW / 32
-// floats each).
-template <int F, int NC, int R, int D>
-__global__ __launch_bounds__(256) void gemv_kernel(const uint8_t *__restrict__ W, uint64_t row_bytes,
-                                                   uint32_t K, uint32_t M,
-                                                   const float *__restrict__ X,
-                                                   float *__restrict__ Y,
-                                                   const u32x4 *__restrict__ tab_g,
-                                                   uint32_t cunits) {
+// floats each), then the S-way partial sums.
+constexpr int GV_L = 16;  // lanes per row slot
+constexpr int GV_SLOTS = 4;
+
+template <int F, int NC, int R, int D, int S>
+__device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ W, uint64_t row_bytes, uint32_t K,
+                                          uint32_t M, const float *__restrict__ X, float *__restrict__ Y,
+                                          const u32x4 *__restrict__ tab_g, uint32_t cunits) {
+    constexpr int L = GV_L;
     extern __shared__ u32x4 lds[];
     constexpr uint32_t TAB = F == IQ2_XXS ? 384 : 0;
     u32x4 *tab = lds;
     uint32_t *xs = (uint32_t *)(lds + TAB);
     const uint32_t tid = threadIdx.x, nthr = blockDim.x;
-    const uint32_t lane = tid & 63, i = lane & 15, slot = lane >> 4;
+    const uint32_t lane = tid & 63, i = lane % L, slot = lane / L;
     const uint32_t wave = tid >> 6, waves = nthr >> 6;
+    const uint32_t part = wave % S, group = wave / S, groups = waves / S;
     if constexpr (F == IQ2_XXS)
         for (uint32_t e = tid; e < TAB; e += nthr) tab[e] = tab_g[e];
 
-    const uint32_t m0 = ((blockIdx.x * waves + wave) * GV_SLOTS_PER_WAVE + slot) * R;
+    const uint32_t m0 = ((blockIdx.x * groups + group) * GV_SLOTS + slot) * R;
     const uint8_t *rows[R];
 #pragma unroll
     for (int r = 0; r < R; r++) rows[r] = W + (uint64_t)min(m0 + r, M - 1) * row_bytes;
-    const bool live = m0 < M;  // dead slots still stage activations
     constexpr uint32_t UW = unit_weights<F>();
     const uint32_t units = K / UW, cs = cunits * (UW / 2), xcs = cunits * (UW / 32);
     float *xsum = (float *)(xs + NC * cs);
+    float *red = xsum + NC * xcs;  // [groups][slots][R][NC][S]
 
     float acc[R][NC];
 #pragma unroll
@@ -431,16 +436,18 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t *__restrict__ W
 
     for (uint32_t c0 = 0; c0 < units; c0 += cunits) {
         const uint32_t cn = min(cunits, units - c0);
-        const uint32_t steps = (cn + GV_LANES - 1) / GV_LANES, last = cn - 1;
+        // this wavefront's steps: t = part, part + S, ... of the chunk
+        const uint32_t steps = ((cn + L - 1) / L + S - 1 - part) / S, last = cn - 1;
         // The first D steps' weights are requested before the activations are
-        // staged, so their latency overlaps the staging.  Every load is
-        // unconditional (past the end it re-reads the chunk's last unit, an
-        // L2 hit) so that no branch hides a load from the compiler's count of
-        // outstanding loads, and the wait before a compute covers only the
+        // staged, so their latency overlaps the staging.  Loads are
+        // unconditional (past the end they re-read the chunk's last unit, a
+        // cache hit) so that no branch hides a load from the compiler's count
+        // of outstanding loads, and the wait before a compute covers only the
         // loads of that buffer.
         Unit<F, R> buf[D];
 #pragma unroll
-        for (int j = 0; j < D; j++) load_unit<F, R>(rows, c0 + min(i + GV_LANES * j, last), buf[j]);
+        for (int j = 0; j < D; j++)
+            load_unit<F, R>(rows, c0 + min(i + L * (part + S * j), last), buf[j]);
 
         // stage units [c0, c0 + cn) of every column as fp16 pairs
         __syncthreads();
@@ -462,38 +469,77 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t *__restrict__ W
                     B = *(const floatx4 *)(xb + kb);
                 }
                 const u32x4 v = slot_pack<F>(A, B);
-                float part = slot_total(v);
-                part += __shfl_xor(part, 1, 64);
-                part += __shfl_xor(part, 2, 64);
+                float pt = slot_total(v);
+                pt += __shfl_xor(pt, 1, 64);
+                pt += __shfl_xor(pt, 2, 64);
                 if (in) {
-                    *(u32x4 *)(xs + n * cs + xs_index<F>(u, 4 * sidx)) = v;
-                    if ((q & 3) == 0) xsum[n * xcs + q / 4] = part;
+                    *(u32x4 *)(xs + n * cs + xs_index<F, L>(u, 4 * sidx)) = v;
+                    if ((q & 3) == 0) xsum[n * xcs + q / 4] = pt;
                 }
             }
         }
         __syncthreads();
-        if (!live) continue;
-        // stream the chunk's units u = c0 + i + 16 t through a ring of D
-        // register buffers
-        for (uint32_t t = 0; t < steps; t += D) {
+        // stream the wavefront's units u = c0 + i + L (part + S t) through
+        // the ring
+        uint32_t t = 0;
+        for (; t + D < steps; t += D) {
 #pragma unroll
             for (int j = 0; j < D; j++) {
-                const uint32_t u = i + GV_LANES * (t + j);
+                const uint32_t u = i + L * (part + S * (t + j));
                 if (u < cn)
-                    Compute<F, NC, R>::run(buf[j], xs + xs_index<F>(u, 0), cs, xsum + u * (UW / 32),
-                                           xcs, c0 + u, acc, tab);
-                load_unit<F, R>(rows, c0 + min(u + GV_LANES * D, last), buf[j]);
+                    Compute<F, NC, R>::run(buf[j], xs + xs_index<F, L>(u, 0), 4 * L, cs,
+                                           xsum + u * (UW / 32), xcs, c0 + u, acc, tab);
+                load_unit<F, R>(rows, c0 + min(u + L * S * D, last), buf[j]);
             }
         }
+#pragma unroll
+        for (int j = 0; j < D; j++) {
+            const uint32_t u = i + L * (part + S * (t + j));
+            if (u < cn)
+                Compute<F, NC, R>::run(buf[j], xs + xs_index<F, L>(u, 0), 4 * L, cs,
+                                       xsum + u * (UW / 32), xcs, c0 + u, acc, tab);
+        }
     }
-    if (!live) return;
+    // reduce: over the slot's lanes, then (S > 1) over the parts in LDS
 #pragma unroll
     for (int r = 0; r < R; r++)
 #pragma unroll
-        for (int n = 0; n < NC; n++) {
-            const float v = slot_sum(acc[r][n]);
-            if (i == 0 && m0 + r < M) Y[(uint64_t)n * M + m0 + r] = v;
-        }
+        for (int n = 0; n < NC; n++) acc[r][n] = slot_sum<L>(acc[r][n]);
+    if constexpr (S > 1) {
+        const uint32_t base = ((group * GV_SLOTS + slot) * R) * NC * S;
+        if (i == 0)
+#pragma unroll
+            for (int r = 0; r < R; r++)
+#pragma unroll
+                for (int n = 0; n < NC; n++) red[base + (r * NC + n) * S + part] = acc[r][n];
+        __syncthreads();
+        if (part != 0) return;
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int n = 0; n < NC; n++) {
+                float v = red[base + (r * NC + n) * S];
+#pragma unroll
+                for (int p = 1; p < S; p++) v += red[base + (r * NC + n) * S + p];
+                acc[r][n] = v;
+            }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int n = 0; n < NC; n++)
+            if (i == 0 && m0 + r < M) Y[(uint64_t)n * M + m0 + r] = acc[r][n];
+}
+
+
+template <int F, int NC, int R, int D, int S>
+__global__ __launch_bounds__(256) void gemv_kernel(const uint8_t *__restrict__ W, uint64_t row_bytes,
+                                                   uint32_t K, uint32_t M,
+                                                   const float *__restrict__ X,
+                                                   float *__restrict__ Y,
+                                                   const u32x4 *__restrict__ tab_g,
+                                                   uint32_t cunits) {
+    gemv_body<F, NC, R, D, S>(W, row_bytes, K, M, X, Y, tab_g, cunits);
 }
 
 }  // namespace okf

@@ -29,8 +29,7 @@ struct okf_ctx {
     size_t max_lds = 65536;  // dynamic LDS a workgroup may use
     // matvec tuning (defaults chosen per shape; OKF_GEMV_* environment
     // variables override them for measurements)
-    int gemv_r = 0;      // rows per row slot (0 = auto)
-    int gemv_waves = 0;  // wavefronts per workgroup (0 = auto)
+    int gemv_s = 0;      // K split across a workgroup's wavefronts (0 = auto)
     double fault_rate = 0;
     uint64_t fault_state = 0;
     int last_hip = 0;
@@ -104,38 +103,45 @@ void build_iq2_tables(uint32_t *t) {
     }
 }
 
-template <int F, int NC, int R>
-void launch_gemv_r(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t M, const float *X,
-                   float *Y, uint32_t waves, uint32_t cunits, size_t lds) {
-    constexpr int D = 4;       // register buffers in flight per lane
+template <int F, int NC, int S>
+void launch_gemv_s(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t M, const float *X,
+                   float *Y, uint32_t cunits, size_t lds) {
+    constexpr int R = 1, D = 2, WAVES = 4;
+    const void *fn = (const void *)gemv_kernel<F, NC, R, D, S>;
     static bool attr = false;  // one attribute call per instantiation
     if (!attr) {
-        (void)hipFuncSetAttribute((const void *)gemv_kernel<F, NC, R, D>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)c->max_lds);
+        (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)c->max_lds);
         attr = true;
     }
-    const uint32_t rows_per_wg = waves * GV_SLOTS_PER_WAVE * R;
+    const uint32_t rows_per_wg = (WAVES / S) * GV_SLOTS * R;
     dim3 grid((M + rows_per_wg - 1) / rows_per_wg);
-    hipLaunchKernelGGL((gemv_kernel<F, NC, R, D>), grid, dim3(64 * waves), lds, c->stream, W, rb, K,
+    hipLaunchKernelGGL((gemv_kernel<F, NC, R, D, S>), grid, dim3(64 * WAVES), lds, c->stream, W, rb, K,
                        M, X, Y, c->tab, cunits);
 }
 
+// Launch geometry: 256-thread workgroups of four wavefronts, each four row
+// slots of 16 lanes.  For one column with fewer than ~3072 wavefronts' worth
+// of rows, K is split two ways across the wavefronts of a workgroup (more,
+// shorter wavefronts); measured on MI355X, a four-way split loses to the
+// extra activation staging it needs.
 template <int F, int NC>
 void launch_gemv_nc(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t M,
                     const float *X, float *Y) {
     constexpr uint32_t UW = unit_weights<F>();
     const size_t tab = F == IQ2_XXS ? 384 * 16 : 0;
     const uint32_t units = K / UW;
-    // stage all of x when it fits, else in chunks of 16-unit groups
+    // stage all of x when it fits, else in chunks of 64-unit groups
     const size_t per_unit = (size_t)NC * (UW * 2 + UW / 32 * 4);
-    uint32_t cunits = (units + 15) / 16 * 16;
-    const size_t budget = c->max_lds - tab;
-    if (cunits * per_unit > budget) cunits = (uint32_t)(budget / per_unit) / 16 * 16;
-    const size_t lds = tab + cunits * per_unit;
-    int R = c->gemv_r ? c->gemv_r : (NC == 1 && M >= 8192 ? 2 : 1);
-    uint32_t waves = c->gemv_waves ? (uint32_t)c->gemv_waves : 4;
-    if (R >= 2) launch_gemv_r<F, NC, 2>(c, W, rb, K, M, X, Y, waves, cunits, lds);
-    else launch_gemv_r<F, NC, 1>(c, W, rb, K, M, X, Y, waves, cunits, lds);
+    const size_t red = 4 * GV_SLOTS * NC * 4 * sizeof(float);
+    uint32_t cunits = (units + 63) / 64 * 64;
+    const size_t budget = c->max_lds - tab - red;
+    if (cunits * per_unit > budget) cunits = (uint32_t)(budget / per_unit) / 64 * 64;
+    const size_t lds = tab + cunits * per_unit + red;
+    const uint32_t waves1 = (M + GV_SLOTS - 1) / GV_SLOTS;  // wavefronts without a split
+    uint32_t S = c->gemv_s ? (uint32_t)c->gemv_s : (NC == 1 && waves1 < 3072 ? 2 : 1);
+    if (S >= 4) launch_gemv_s<F, NC, 4>(c, W, rb, K, M, X, Y, cunits, lds);
+    else if (S == 2) launch_gemv_s<F, NC, 2>(c, W, rb, K, M, X, Y, cunits, lds);
+    else launch_gemv_s<F, NC, 1>(c, W, rb, K, M, X, Y, cunits, lds);
 }
 
 template <int F>
@@ -226,8 +232,7 @@ int okf_ctx_create(int device, okf_ctx **out) {
         if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, device) ==
                 hipSuccess && v > 0)
             c->max_lds = (size_t)v;
-        if (const char *e = getenv("OKF_GEMV_R")) c->gemv_r = atoi(e);
-        if (const char *e = getenv("OKF_GEMV_WAVES")) c->gemv_waves = atoi(e);
+        if (const char *e = getenv("OKF_GEMV_S")) c->gemv_s = atoi(e);
     } else if (device != -1) {
         delete c;
         return OKF_E_ARG;
