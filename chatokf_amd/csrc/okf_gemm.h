@@ -141,3 +141,188 @@ __global__ __launch_bounds__(256) void dequant_row_kernel(const uint8_t *__restr
 }
 
 }  // namespace okf
+
+namespace okf {
+
+// ------------------------------------------------------------------------
+// Q4_K x fp16 tile GEMM (the pp512 prefill path).
+//
+// Y[n][m] = sum_k W[m][k] X[n][k] with X already in fp16 (Xh[N][K]).
+// Workgroup tile 128 (rows m) x 128 (tokens n), K step 64 (one 32-byte code
+// group of a superblock); four wavefronts in 2 x 2, each 64 x 64 with
+// v_mfma_f32_32x32x16_f16.  The Q4_K bytes and fp16 activations of a step
+// arrive in registers two steps ahead; they are dequantized with packed fp16
+// arithmetic and stored to the single LDS stage between two barriers.  Tiles are laid out
+// so that each XCD (workgroup id mod 8) owns a contiguous range of tiles.
+constexpr int QG_BM = 128, QG_BN = 128, QG_BK = 64, QG_LD = QG_BK + 8;
+
+// v_bfi_b32 with 0x64006400: drops the masked bits of a into the mantissas of
+// two fp16 1024.0 (written out: the compiler splits the constant form).
+__device__ __forceinline__ uint32_t gbfi(uint32_t mask, uint32_t a) {
+    uint32_t r;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(a), "v"(0x64006400u));
+    return r;
+}
+
+__global__ __launch_bounds__(256) void x_to_f16_kernel(const float *__restrict__ X,
+                                                       _Float16 *__restrict__ Xh, uint64_t n4) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) return;
+    const floatx4 v = ((const floatx4 *)X)[i];
+    typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+    ((half4 *)Xh)[i] = half4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+}
+
+__global__ __launch_bounds__(256, 2) void gemm_q4k_kernel(const uint8_t *__restrict__ W, uint64_t row_bytes,
+                                                       uint32_t K, uint32_t M,
+                                                       const _Float16 *__restrict__ Xh, uint32_t N,
+                                                       float *__restrict__ Y, uint32_t tiles_m,
+                                                       uint32_t tiles, uint32_t per_xcd) {
+    __shared__ __attribute__((aligned(16))) _Float16 As[1][QG_BM * QG_LD];
+    __shared__ __attribute__((aligned(16))) _Float16 Bs[1][QG_BN * QG_LD];
+    // XCD-contiguous tile index: workgroup b runs on XCD b % 8
+    const uint32_t tile = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (tile >= tiles) return;
+    const uint32_t mt = tile % tiles_m, nt = tile / tiles_m;
+    const uint32_t m0 = mt * QG_BM, n0 = nt * QG_BN;
+
+    const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const uint32_t wm = wave >> 1, wn = wave & 1;
+    // loader roles: weight row t/2, code half t%2; activation row t/2, half t%2
+    const uint32_t lr = t >> 1, lh = t & 1;
+    const uint8_t *wrow = W + (uint64_t)min(m0 + lr, M - 1) * row_bytes;
+    const _Float16 *xrow = Xh + (uint64_t)min(n0 + lr, N - 1) * K;
+    const uint32_t steps = K / QG_BK;
+
+    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+    struct Regs {
+        u32x4v hdr, qv, xv[4];
+    };
+    // global -> registers for step s (clamped: the loads after the last step
+    // repeat it, so that every fetch is unconditional and the compiler's
+    // count of outstanding loads stays exact)
+    auto fetch = [&](uint32_t s, Regs &r) {
+        s = min(s, steps - 1);
+        const uint8_t *b = wrow + (uint64_t)(s >> 2) * 144;  // superblock s / 4, group s % 4
+        r.hdr = *(const u32x4v *)b;
+        r.qv = *(const u32x4v *)(b + 16 + (s & 3) * 32 + lh * 16);
+        const u32x4v *xp = (const u32x4v *)(xrow + (uint64_t)s * QG_BK + lh * 32);
+#pragma unroll
+        for (int i = 0; i < 4; i++) r.xv[i] = xp[i];
+    };
+    auto stash = [&](uint32_t s, const Regs &r, int buf) {
+        const u32x4v hdr = r.hdr, qv = r.qv;
+        // dequantize 32 weights of row lr: low nibbles -> k = 16 lh + i
+        // (sub-block 2g), high nibbles -> k = 32 + 16 lh + i (sub-block 2g+1).
+        // Packed fp16: a nibble pair becomes fp16 (1024 + q) by v_bfi, minus
+        // 1024 (exact), then one fused q * (d*sc) - dmin*m with the two scale
+        // products rounded to fp16 (the result is rounded once).
+        const uint32_t g = s & 3;
+        uint32_t sc0, mn0, sc1, mn1;
+        q4k_scale_min_pair(make_uint4(hdr[0], hdr[1], hdr[2], hdr[3]), g, sc0, mn0, sc1, mn1);
+        const float d = h2f(hdr[0] & 0xFFFF), dmin = h2f(hdr[0] >> 16);
+        const half2v a0 = (half2v)(_Float16)(d * (float)sc0), o0 = (half2v)(_Float16)(-dmin * (float)mn0);
+        const half2v a1 = (half2v)(_Float16)(d * (float)sc1), o1 = (half2v)(_Float16)(-dmin * (float)mn1);
+        const half2v m1024 = (half2v)(_Float16)-1024.0f;
+        uint32_t lo[8], hi[8];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t v = qv[i];
+            const uint32_t p01 = __builtin_amdgcn_perm(v, v, 0x0C010C00u);  // b0, b1 -> 16-bit lanes
+            const uint32_t p23 = __builtin_amdgcn_perm(v, v, 0x0C030C02u);
+            const uint32_t l01 = gbfi(0x000F000Fu, p01), l23 = gbfi(0x000F000Fu, p23);
+            const uint32_t h01 = gbfi(0x000F000Fu, p01 >> 4), h23 = gbfi(0x000F000Fu, p23 >> 4);
+            auto dq = [&](uint32_t x, half2v a, half2v o) {
+                const half2v q = __builtin_bit_cast(half2v, x) + m1024;
+                return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, a, o));
+            };
+            lo[2 * i] = dq(l01, a0, o0);
+            lo[2 * i + 1] = dq(l23, a0, o0);
+            hi[2 * i] = dq(h01, a1, o1);
+            hi[2 * i + 1] = dq(h23, a1, o1);
+        }
+        _Float16 *ad = As[buf] + lr * QG_LD + lh * 16;
+        *(u32x4v *)(ad) = u32x4v{lo[0], lo[1], lo[2], lo[3]};
+        *(u32x4v *)(ad + 8) = u32x4v{lo[4], lo[5], lo[6], lo[7]};
+        *(u32x4v *)(ad + 32) = u32x4v{hi[0], hi[1], hi[2], hi[3]};
+        *(u32x4v *)(ad + 40) = u32x4v{hi[4], hi[5], hi[6], hi[7]};
+        _Float16 *bd = Bs[buf] + lr * QG_LD + lh * 32;
+#pragma unroll
+        for (int i = 0; i < 4; i++) *(u32x4v *)(bd + i * 8) = r.xv[i];
+    };
+    typedef float floatx16 __attribute__((ext_vector_type(16)));
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = floatx16{};
+
+    // v_mfma_f32_32x32x16_f16 (about twice the throughput of 16x16x32 on
+    // gfx950): lane l supplies row l % 32, k = 8 (l / 32) .. +8 of A (weights)
+    // and column l % 32, same k, of B (tokens).
+    auto mfma_step = [&](int buf) {
+        const _Float16 *A = As[buf], *B = Bs[buf];
+#pragma unroll
+        for (int kk = 0; kk < QG_BK / 16; kk++) {
+            const uint32_t kc = kk * 16 + (lane >> 5) * 8;
+            half8 a[2], b[2];
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+                a[i] = *(const half8 *)(A + (wm * 64 + i * 32 + (lane & 31)) * QG_LD + kc);
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+                b[j] = *(const half8 *)(B + (wn * 64 + j * 32 + (lane & 31)) * QG_LD + kc);
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    // One LDS stage (so three workgroups fit per CU and the whole grid is
+    // resident) and two register sets: step s + 1 is stored to LDS from
+    // registers loaded a full step earlier, while the loads of step s + 2 are
+    // in flight.
+    Regs ra, rb;
+    fetch(0, ra);
+    fetch(1, rb);
+    // steps = K / 64 is a multiple of 4 (K is whole 256-weight superblocks)
+    for (uint32_t s = 0; s < steps; s += 2) {
+        __syncthreads();
+        stash(s, ra, 0);
+        __syncthreads();
+        fetch(s + 2, ra);
+        mfma_step(0);
+        __syncthreads();
+        stash(s + 1, rb, 0);
+        __syncthreads();
+        fetch(s + 3, rb);
+        mfma_step(0);
+    }
+
+    // C fragment of a 32 x 32 tile: register e of lane l holds row
+    // 8 (e / 4) + 4 (l / 32) + e % 4 (weight rows m) of column l % 32 (token n)
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const uint32_t n = n0 + wn * 64 + j * 32 + (lane & 31);
+            if (n >= N) continue;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const uint32_t m = m0 + wm * 64 + i * 32 + 8 * q + 4 * (lane >> 5);
+                float *dst = Y + (uint64_t)n * M + m;
+                const floatx16 &c = acc[i][j];
+                if (m + 3 < M && (M & 3) == 0) {
+                    *(float4 *)dst = make_float4(c[4 * q], c[4 * q + 1], c[4 * q + 2], c[4 * q + 3]);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        if (m + e < M) dst[e] = c[4 * q + e];
+                }
+            }
+        }
+}
+
+}  // namespace okf

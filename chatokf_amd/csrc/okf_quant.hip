@@ -33,6 +33,8 @@ struct okf_ctx {
     double fault_rate = 0;
     uint64_t fault_state = 0;
     int last_hip = 0;
+    _Float16 *xh = nullptr;  // fp16 copy of the GEMM activations (grown on demand)
+    size_t xh_bytes = 0;
 };
 
 namespace {
@@ -157,11 +159,36 @@ void launch_gemv(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t
 }
 
 template <int F>
-void launch_gemm(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t M, const float *X,
-                 uint32_t N, float *Y) {
+int launch_gemm(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t M, const float *X,
+                uint32_t N, float *Y) {
+    if constexpr (F == Q4_K) {
+        // fp16 activations, converted once per call into the context's buffer
+        const size_t need = (size_t)N * K * sizeof(_Float16);
+        if (need > c->xh_bytes) {
+            if (c->xh) {
+                hipError_t e = hipStreamSynchronize(c->stream);
+                if (e != hipSuccess) return hip_fail(c, e);
+                (void)hipFree(c->xh);
+                c->xh = nullptr;
+                c->xh_bytes = 0;
+            }
+            hipError_t e = hipMalloc((void **)&c->xh, need);
+            if (e != hipSuccess) return hip_fail(c, e);
+            c->xh_bytes = need;
+        }
+        const uint64_t n4 = (uint64_t)N * K / 4;
+        hipLaunchKernelGGL(x_to_f16_kernel, dim3((uint32_t)((n4 + 255) / 256)), dim3(256), 0, c->stream,
+                           X, c->xh, n4);
+        const uint32_t tm = (M + QG_BM - 1) / QG_BM, tn = (N + QG_BN - 1) / QG_BN;
+        const uint32_t tiles = tm * tn, per_xcd = (tiles + 7) / 8;
+        hipLaunchKernelGGL(gemm_q4k_kernel, dim3(per_xcd * 8), dim3(256), 0, c->stream, W, rb, K, M,
+                           (const _Float16 *)c->xh, N, Y, tm, tiles, per_xcd);
+        return OKF_OK;
+    }
     dim3 grid((N + GB_N - 1) / GB_N, (M + GB_M - 1) / GB_M);
     hipLaunchKernelGGL((gemm_mfma_kernel<F>), grid, dim3(256), 0, c->stream, W, rb, K, M, X, N, Y,
                        c->grid);
+    return OKF_OK;
 }
 
 template <int F>
@@ -193,7 +220,13 @@ int run_gemm(okf_ctx *c, const okf_weight *w, const float *X, uint32_t N, float 
     if (path == Path::Auto && N <= 5) {
         OKF_DISPATCH(w->ggml_type, launch_gemv, c, W, rb, w->K, w->M, X, N, Y);
     } else {
-        OKF_DISPATCH(w->ggml_type, launch_gemm, c, W, rb, w->K, w->M, X, N, Y);
+        switch (w->ggml_type) {
+        case Q8_0: st = launch_gemm<Q8_0>(c, W, rb, w->K, w->M, X, N, Y); break;
+        case Q2_0: st = launch_gemm<Q2_0>(c, W, rb, w->K, w->M, X, N, Y); break;
+        case Q4_K: st = launch_gemm<Q4_K>(c, W, rb, w->K, w->M, X, N, Y); break;
+        default: st = launch_gemm<IQ2_XXS>(c, W, rb, w->K, w->M, X, N, Y); break;
+        }
+        if (st) return st;
     }
     return finish(c);
 }
@@ -249,6 +282,7 @@ int okf_ctx_destroy(okf_ctx *c) {
         if (hipStreamSynchronize(c->stream) != hipSuccess) st = OKF_E_HIP;
         (void)hipFree(c->grid);
         (void)hipFree(c->tab);
+        if (c->xh) (void)hipFree(c->xh);
         (void)hipStreamDestroy(c->stream);
     }
     delete c;
