@@ -12,8 +12,15 @@ call, absolute GB/s or TFLOP/s and the roofline fraction.
 Timing: inputs are resident in HBM before the timed region.  Every call reads
 a different copy of the weights (copies rotated so that >= 1 GiB is cycled,
 four times the 256 MB MALL), so weights stream from HBM, not from cache.
-Per-kernel durations come from HIP events recorded on the library's own stream
-around each call; the step time is bracketed by device synchronisation.
+Per-call durations come from two HIP events recorded on the library's own
+stream around a batch of back-to-back calls (the batch time divided by the
+calls, so launch gaps are included and per-event overhead is not); the step
+time is bracketed by device synchronisation.
+
+``roofline.traffic`` is read from ``profiles/traffic.json`` when that file holds
+a rocprofv3 FETCH_SIZE / WRITE_SIZE measurement of the dominant kernel (made by
+running this script under ``rocprofv3 --pmc`` with ``--calibrate``, which adds
+plain device copies of known size to scale the counters); otherwise null.
 """
 from __future__ import annotations
 
@@ -47,6 +54,9 @@ def main():
     ap.add_argument("--suite", default="all", help="'all', 'none' or comma list of suite names")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-headline", action="store_true", help="skip the FFN step (profiling runs)")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="run 64 MiB device copies first (scale for rocprofv3 byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (the path has no multi-GPU "
@@ -71,69 +81,104 @@ def main():
         torch.cuda.synchronize()
         return copies
 
-    def time_calls(launch, n_calls, warm):
-        """Average kernel time (s) of n_calls launches, HIP events on enc's stream."""
+    def time_calls(launch, n_calls, warm, reps=5):
+        """Seconds per call: HIP events on enc's stream around `reps` batches of
+        n_calls back-to-back launches; returns (mean, best) over the batches."""
         for i in range(warm):
             launch(i)
-        starts = [torch.cuda.Event(enable_timing=True) for _ in range(n_calls)]
-        ends = [torch.cuda.Event(enable_timing=True) for _ in range(n_calls)]
+        per = []
+        k = warm
+        for _ in range(reps):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            # hold the stream for a few ms so the whole batch is queued before
+            # the first timed kernel starts: the events then see GPU time only
+            with torch.cuda.stream(stream):
+                torch.cuda._sleep(20_000_000)
+            e0.record(stream)
+            for _ in range(n_calls):
+                launch(k)
+                k += 1
+            e1.record(stream)
+            torch.cuda.synchronize()
+            per.append(e0.elapsed_time(e1) * 1e-3 / n_calls)
+        return float(np.mean(per)), float(np.min(per))
+
+    def load_traffic(name):
+        path = os.path.join(ROOT, "profiles", "traffic.json")
+        if not os.path.exists(path):
+            return None
+        with open(path) as f:
+            t = json.load(f).get(name)
+        return None if t is None else int(t["fetch_bytes"] + t["write_bytes"])
+
+    if args.calibrate:
+        src = torch.empty(64 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
         torch.cuda.synchronize()
-        for i in range(n_calls):
-            starts[i].record(stream)
-            launch(warm + i)
-            ends[i].record(stream)
-        torch.cuda.synchronize()
-        ms = np.array([s.elapsed_time(e) for s, e in zip(starts, ends)])
-        return float(ms.mean()) * 1e-3, float(np.median(ms)) * 1e-3
+        del src, dst
 
     # ----------------------------------------------------------- headline
     t0 = time.time()
+    value, step_s, roofline = None, None, None
     K1, M1 = 2048, 6144
-    log("bench: generating ternary FFN weights")
-    gate_np = synth.q2_0(M1, K1, 1002)
-    up_np = synth.q2_0(M1, K1, 1202)
-    down_np = synth.q2_0(K1, M1, 1102)
-    gates, ups, downs = rotated(gate_np), rotated(up_np), rotated(down_np)
-    x = torch.from_numpy(synth.activations(1, K1, 2002)).cuda()
-    h = torch.empty(M1, device="cuda")
-    h2 = torch.empty(M1, device="cuda")
-    y = torch.empty(K1, device="cuda")
-    hx = torch.from_numpy(synth.activations(1, M1, 2102)).cuda()  # down-proj input
-    nrot = len(gates)
-    step_bytes = gate_np.nbytes + up_np.nbytes + down_np.nbytes
+    step_bytes = 0
+    if not args.no_headline:
+        log("bench: generating ternary FFN weights")
+        gate_np = synth.q2_0(M1, K1, 1002)
+        up_np = synth.q2_0(M1, K1, 1202)
+        down_np = synth.q2_0(K1, M1, 1102)
+        gates, ups, downs = rotated(gate_np), rotated(up_np), rotated(down_np)
+        x = torch.from_numpy(synth.activations(1, K1, 2002)).cuda()
+        h = torch.empty(M1, device="cuda")
+        h2 = torch.empty(M1, device="cuda")
+        y = torch.empty(K1, device="cuda")
+        hx = torch.from_numpy(synth.activations(1, M1, 2102)).cuda()  # down-proj input
+        nrot = len(gates)
+        step_bytes = gate_np.nbytes + up_np.nbytes + down_np.nbytes
 
-    def ffn_step(i):
-        j = i % nrot
-        enc.gemv(ok.QuantTensor(gates[j], K1, M1, ok.Q2_0), x, h)
-        enc.gemv(ok.QuantTensor(ups[j], K1, M1, ok.Q2_0), x, h2)
-        enc.gemv(ok.QuantTensor(downs[j], M1, K1, ok.Q2_0), hx, y)
+        # the C-ABI calls a host engine makes: weight descriptors built once
+        gemv_c = enc.raw_gemv
+        gw = [ok.QuantTensor(g, K1, M1, ok.Q2_0).c() for g in gates]
+        uw = [ok.QuantTensor(u, K1, M1, ok.Q2_0).c() for u in ups]
+        dw = [ok.QuantTensor(d, M1, K1, ok.Q2_0).c() for d in downs]
+        xp, hp, h2p, yp, hxp = (t.data_ptr() for t in (x, h, h2, y, hx))
 
-    for i in range(args.warmup):
-        ffn_step(i)
-    torch.cuda.synchronize()
-    w0 = time.perf_counter()
-    for i in range(args.steps):
-        ffn_step(args.warmup + i)
-    torch.cuda.synchronize()
-    step_s = (time.perf_counter() - w0) / args.steps
-    value = step_bytes / step_s / 1e9
+        def ffn_step(i):
+            j = i % nrot
+            gemv_c(gw[j], xp, hp)
+            gemv_c(uw[j], xp, h2p)
+            gemv_c(dw[j], hxp, yp)
 
-    # dominant kernel of the step: per-launch HIP-event durations
-    gate_t, _ = time_calls(
-        lambda i: enc.gemv(ok.QuantTensor(gates[i % nrot], K1, M1, ok.Q2_0), x, h), args.steps, 5)
-    down_t, _ = time_calls(
-        lambda i: enc.gemv(ok.QuantTensor(downs[i % nrot], M1, K1, ok.Q2_0), hx, y), args.steps, 5)
-    if gate_t >= down_t:
-        dom = ("q2_0 gate/up matvec 6144x2048", gate_np.nbytes, gate_t)
-    else:
-        dom = ("q2_0 down matvec 2048x6144", down_np.nbytes, down_t)
-    roofline = {"kernel": dom[0], "bound": "hbm", "achieved": round(dom[1] / dom[2] / 1e9, 1),
-                "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(dom[1] / dom[2] / HBM_PEAK, 4),
-                "us_per_launch": round(dom[2] * 1e6, 3), "traffic": None}
-    log(f"bench: ffn step {step_s*1e6:.2f} us, {value:.1f} GB/s; gate {gate_t*1e6:.2f} us, "
-        f"down {down_t*1e6:.2f} us")
-    del gates, ups, downs
-    torch.cuda.empty_cache()
+        for i in range(args.warmup):
+            ffn_step(i)
+        torch.cuda.synchronize()
+        w0 = time.perf_counter()
+        for i in range(args.steps):
+            ffn_step(args.warmup + i)
+        torch.cuda.synchronize()
+        step_s = (time.perf_counter() - w0) / args.steps
+        value = step_bytes / step_s / 1e9
+
+        # dominant kernel of the step: HIP events around batches of its launches
+        gate_t, _ = time_calls(lambda i: gemv_c(gw[i % nrot], xp, hp), args.steps, 5)
+        down_t, _ = time_calls(lambda i: gemv_c(dw[i % nrot], hxp, yp), args.steps, 5)
+        if gate_t >= down_t:
+            dom = ("q2_0_matvec_6144x2048", gate_np.nbytes, gate_t)
+        else:
+            dom = ("q2_0_matvec_2048x6144", down_np.nbytes, down_t)
+        roofline = {"kernel": f"okf::gemv_kernel<Q2_0> ({dom[0]})", "bound": "hbm",
+                    "achieved": round(dom[1] / dom[2] / 1e9, 1), "peak": HBM_PEAK / 1e9,
+                    "unit": "GB/s", "frac": round(dom[1] / dom[2] / HBM_PEAK, 4),
+                    "traffic": load_traffic(dom[0]), "us_per_launch": round(dom[2] * 1e6, 3),
+                    "algorithmic_bytes_per_launch": dom[1]}
+        log(f"bench: ffn step {step_s*1e6:.2f} us, {value:.1f} GB/s; gate {gate_t*1e6:.2f} us, "
+            f"down {down_t*1e6:.2f} us")
+        del gates, ups, downs
+        torch.cuda.empty_cache()
 
     # ----------------------------------------------------------- suite
     SUITE = [
@@ -165,13 +210,16 @@ def main():
         Y = torch.empty((N, M), device="cuda")
         nr = len(copies)
 
-        def call(i, copies=copies, t=t, M=M, K=K, N=N, X=X, Y=Y, nr=nr):
-            enc.gemm(ok.QuantTensor(copies[i % nr], K, M, t), X, Y, N)
+        wcs = [ok.QuantTensor(c, K, M, t).c() for c in copies]
+        xp_, yp_ = X.data_ptr(), Y.data_ptr()
+
+        def call(i, wcs=wcs, N=N, xp_=xp_, yp_=yp_, nr=nr):
+            enc.raw_gemm(wcs[i % nr], xp_, N, yp_)
 
         n_calls = args.steps if N < 512 else max(10, args.steps // 10)
-        mean_s, med_s = time_calls(call, n_calls, max(3, args.warmup // 2))
+        mean_s, med_s = time_calls(call, n_calls, max(3, args.warmup // 2))  # (mean, best batch)
         flops = 2.0 * M * K * N
-        rec = {"name": name, "us": round(mean_s * 1e6, 3), "us_median": round(med_s * 1e6, 3),
+        rec = {"name": name, "us": round(mean_s * 1e6, 3), "us_best": round(med_s * 1e6, 3),
                "weight_bytes": wbytes, "GBps": round(wbytes / mean_s / 1e9, 1),
                "TFLOPs": round(flops / mean_s / 1e12, 2)}
         if N >= 512:
@@ -185,7 +233,7 @@ def main():
 
     # ----------------------------------------------------------- CPU baseline
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and not args.no_headline:
         import oracle  # the CPU baseline leg: the oracle restatement of GQ.matvec
 
         cores = oracle.usable_cores()
@@ -210,16 +258,16 @@ def main():
 
     out = {
         "metric": METRIC,
-        "value": round(value, 2),
+        "value": None if value is None else round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(step_s * 1e3, 5),
+        "ms_per_step": None if step_s is None else round(step_s * 1e3, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32",
+        "dtype": "f16 x f16 products, f32 accumulate (weights dequantized exactly to f16)",
         "data": "synthetic (reference LCG, BASELINE.json distributions); weights rotated over >= 1 GiB",
         "config": {"workload": "BASELINE configs[1]: Bonsai-1.7B ternary FFN decode step, one token: "
                                "gate+up Q2_0 W 6144x2048 and down Q2_0 W 2048x6144 matvecs",

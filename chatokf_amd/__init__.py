@@ -17,7 +17,7 @@ import os
 from .formats import Q8_0, Q4_K, IQ2_XXS, Q2_0, NAMES, BY_NAME, block_elems, row_bytes
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libokf_quant.so")
+LIB_PATH = os.environ.get("OKF_LIB") or os.path.join(HERE, "libokf_quant.so")
 
 OKF_OK, OKF_E_TYPE, OKF_E_SHAPE, OKF_E_HIP, OKF_E_INJECTED, OKF_E_ARG, OKF_E_NODEV = range(7)
 
@@ -156,6 +156,19 @@ class Enc:
     def gemm(self, w: QuantTensor, X, out, N: int):
         wc = w.c()
         self._check(self._lib.okf_gemm(self.h, ctypes.byref(wc), _ptr(X), int(N), _ptr(out)), "okf_gemm")
+
+    def raw_gemv(self, wc: OkfWeight, x: int, out: int):
+        """okf_gemv on a prebuilt descriptor and raw device pointers (no
+        per-call Python object construction; for launch-rate-bound callers)."""
+        rc = self._lib.okf_gemv(self.h, ctypes.byref(wc), x, out)
+        if rc:
+            self._check(rc, "okf_gemv")
+
+    def raw_gemm(self, wc: OkfWeight, X: int, N: int, out: int):
+        """okf_gemm on a prebuilt descriptor and raw device pointers."""
+        rc = self._lib.okf_gemm(self.h, ctypes.byref(wc), X, N, out)
+        if rc:
+            self._check(rc, "okf_gemm")
 
     def gemm_tile(self, w: QuantTensor, X, out, N: int):
         wc = w.c()

@@ -176,14 +176,16 @@ __global__ __launch_bounds__(256) void x_to_f16_kernel(const float *__restrict__
 __global__ __launch_bounds__(256, 2) void gemm_q4k_kernel(const uint8_t *__restrict__ W, uint64_t row_bytes,
                                                        uint32_t K, uint32_t M,
                                                        const _Float16 *__restrict__ Xh, uint32_t N,
-                                                       float *__restrict__ Y, uint32_t tiles_m,
+                                                       float *__restrict__ Y, uint32_t tiles_n,
                                                        uint32_t tiles, uint32_t per_xcd) {
     __shared__ __attribute__((aligned(16))) _Float16 As[1][QG_BM * QG_LD];
     __shared__ __attribute__((aligned(16))) _Float16 Bs[1][QG_BN * QG_LD];
-    // XCD-contiguous tile index: workgroup b runs on XCD b % 8
+    // XCD-contiguous tile index: workgroup b runs on XCD b % 8.  The N tiles
+    // of one row block are adjacent, so they run together on one XCD and
+    // read that block's Q4_K bytes from HBM once (the rest hit its L2).
     const uint32_t tile = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
     if (tile >= tiles) return;
-    const uint32_t mt = tile % tiles_m, nt = tile / tiles_m;
+    const uint32_t nt = tile % tiles_n, mt = tile / tiles_n;
     const uint32_t m0 = mt * QG_BM, n0 = nt * QG_BN;
 
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;

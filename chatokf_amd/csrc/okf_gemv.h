@@ -455,26 +455,37 @@ __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ W, uint64_
         // group) sit in 4 consecutive lanes of a wavefront (nthr % 64 == 0)
         constexpr uint32_t SL = UW / 8;
         const uint32_t nslots = cn * SL;
-        for (uint32_t q0 = 0; q0 < nslots; q0 += nthr) {
-            const uint32_t q = q0 + tid, u = q / SL, sidx = q % SL;
-            const bool in = q < nslots;
-            uint32_t kb;
-            const uint32_t ka = slot_first<F>(sidx, kb);
+        // SP passes per round: every pass's global loads are issued before
+        // the first is packed, so staging costs one load latency, not SP
+        constexpr uint32_t SP = NC == 1 ? 4 : NC == 2 ? 2 : 1;
+        for (uint32_t q0 = 0; q0 < nslots; q0 += SP * nthr) {
+            floatx4 A[SP][NC], B[SP][NC];
 #pragma unroll
-            for (int n = 0; n < NC; n++) {
-                const float *xb = X + (uint64_t)n * K + (uint64_t)(c0 + u) * UW;
-                floatx4 A = {0, 0, 0, 0}, B = {0, 0, 0, 0};
-                if (in) {
-                    A = *(const floatx4 *)(xb + ka);
-                    B = *(const floatx4 *)(xb + kb);
+            for (uint32_t p = 0; p < SP; p++) {
+                const uint32_t q = min(q0 + p * nthr + tid, nslots - 1), u = q / SL;
+                uint32_t kb;
+                const uint32_t ka = slot_first<F>(q % SL, kb);
+#pragma unroll
+                for (int n = 0; n < NC; n++) {
+                    const float *xb = X + (uint64_t)n * K + (uint64_t)(c0 + u) * UW;
+                    A[p][n] = *(const floatx4 *)(xb + ka);
+                    B[p][n] = *(const floatx4 *)(xb + kb);
                 }
-                const u32x4 v = slot_pack<F>(A, B);
-                float pt = slot_total(v);
-                pt += __shfl_xor(pt, 1, 64);
-                pt += __shfl_xor(pt, 2, 64);
-                if (in) {
-                    *(u32x4 *)(xs + n * cs + xs_index<F, L>(u, 4 * sidx)) = v;
-                    if ((q & 3) == 0) xsum[n * xcs + q / 4] = pt;
+            }
+#pragma unroll
+            for (uint32_t p = 0; p < SP; p++) {
+                const uint32_t q = q0 + p * nthr + tid, u = q / SL, sidx = q % SL;
+                const bool in = q < nslots;
+#pragma unroll
+                for (int n = 0; n < NC; n++) {
+                    const u32x4 v = slot_pack<F>(A[p][n], B[p][n]);
+                    float pt = slot_total(v);
+                    pt += __shfl_xor(pt, 1, 64);
+                    pt += __shfl_xor(pt, 2, 64);
+                    if (in) {
+                        *(u32x4 *)(xs + n * cs + xs_index<F, L>(u, 4 * sidx)) = v;
+                        if ((q & 3) == 0) xsum[n * xcs + q / 4] = pt;
+                    }
                 }
             }
         }

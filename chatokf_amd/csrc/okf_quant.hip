@@ -182,7 +182,7 @@ int launch_gemm(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t 
         const uint32_t tm = (M + QG_BM - 1) / QG_BM, tn = (N + QG_BN - 1) / QG_BN;
         const uint32_t tiles = tm * tn, per_xcd = (tiles + 7) / 8;
         hipLaunchKernelGGL(gemm_q4k_kernel, dim3(per_xcd * 8), dim3(256), 0, c->stream, W, rb, K, M,
-                           (const _Float16 *)c->xh, N, Y, tm, tiles, per_xcd);
+                           (const _Float16 *)c->xh, N, Y, tn, tiles, per_xcd);
         return OKF_OK;
     }
     dim3 grid((N + GB_N - 1) / GB_N, (M + GB_M - 1) / GB_M);
