@@ -173,19 +173,50 @@ __global__ __launch_bounds__(256) void x_to_f16_kernel(const float *__restrict__
     ((half4 *)Xh)[i] = half4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
 }
 
+// Work split.  The first `full` tiles (a multiple of 256 = one per CU per
+// round) are whole tiles; each of the remaining tiles is split over `ks` K
+// ranges, so that a grid of 2 x 256 + 32 tiles (pp512) costs 2 + 1/8 tile
+// times per CU instead of 3.  A split workgroup stores its partial tile to
+// `part`; gemm_split_sum_kernel then adds each tile's partials in K order
+// (a kernel boundary, not an in-kernel fence: a device-scope fence writes
+// back and invalidates the whole L2 of the XCD, which costs the concurrent
+// whole tiles their cached operands).
+struct GemmSplit {
+    uint32_t tiles_n, tiles;
+    uint32_t full, full_xcd;        // whole tiles, and per XCD
+    uint32_t ks, units, units_xcd;  // K ranges per split tile, split workgroups, per XCD
+    float *part;                    // [units][QG_BN][QG_BM] partial tiles
+};
+
 __global__ __launch_bounds__(256, 2) void gemm_q4k_kernel(const uint8_t *__restrict__ W, uint64_t row_bytes,
                                                        uint32_t K, uint32_t M,
                                                        const _Float16 *__restrict__ Xh, uint32_t N,
-                                                       float *__restrict__ Y, uint32_t tiles_n,
-                                                       uint32_t tiles, uint32_t per_xcd) {
+                                                       float *__restrict__ Y, GemmSplit sp) {
     __shared__ __attribute__((aligned(16))) _Float16 As[1][QG_BM * QG_LD];
     __shared__ __attribute__((aligned(16))) _Float16 Bs[1][QG_BN * QG_LD];
-    // XCD-contiguous tile index: workgroup b runs on XCD b % 8.  The N tiles
-    // of one row block are adjacent, so they run together on one XCD and
-    // read that block's Q4_K bytes from HBM once (the rest hit its L2).
-    const uint32_t tile = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
-    if (tile >= tiles) return;
-    const uint32_t nt = tile % tiles_n, mt = tile / tiles_n;
+    // Workgroup b runs on XCD b % 8; each XCD takes a contiguous range of
+    // whole tiles and of split units, with the split units spread evenly
+    // through its workgroup order (every third slot at pp512), so that
+    // whichever way the dispatcher fills CUs, each gets its share of both.
+    // The N tiles of one row block are adjacent, so they run together on one
+    // XCD and read that block's Q4_K bytes from HBM once (the rest hit its L2).
+    const uint32_t xcd = blockIdx.x % 8, slot = blockIdx.x / 8, pairs = K / (2 * QG_BK);
+    const uint32_t per = sp.full_xcd + sp.units_xcd;
+    const uint32_t sa = slot * sp.units_xcd / per, sb = (slot + 1) * sp.units_xcd / per;
+    uint32_t tile, unit = 0, s0 = 0, s1 = K / QG_BK;
+    const bool split = sb > sa;
+    if (!split) {
+        tile = xcd * sp.full_xcd + (slot - sa);
+    } else {
+        unit = xcd * sp.units_xcd + sa;
+        if (unit >= sp.units) return;
+        tile = sp.full + unit / sp.ks;
+        const uint32_t c = unit % sp.ks;  // K range c: whole step pairs
+        s0 = 2 * (c * pairs / sp.ks);
+        s1 = 2 * ((c + 1) * pairs / sp.ks);
+    }
+    if (tile >= sp.tiles) return;
+    const uint32_t nt = tile % sp.tiles_n, mt = tile / sp.tiles_n;
     const uint32_t m0 = mt * QG_BM, n0 = nt * QG_BN;
 
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -287,10 +318,11 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_kernel(const uint8_t *__restr
     // registers loaded a full step earlier, while the loads of step s + 2 are
     // in flight.
     Regs ra, rb;
-    fetch(0, ra);
-    fetch(1, rb);
-    // steps = K / 64 is a multiple of 4 (K is whole 256-weight superblocks)
-    for (uint32_t s = 0; s < steps; s += 2) {
+    fetch(s0, ra);
+    fetch(s0 + 1, rb);
+    // steps = K / 64 is a multiple of 4 (K is whole 256-weight superblocks),
+    // and every K range is a whole number of step pairs
+    for (uint32_t s = s0; s < s1; s += 2) {
         __syncthreads();
         stash(s, ra, 0);
         __syncthreads();
@@ -305,6 +337,24 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_kernel(const uint8_t *__restr
 
     // C fragment of a 32 x 32 tile: register e of lane l holds row
     // 8 (e / 4) + 4 (l / 32) + e % 4 (weight rows m) of column l % 32 (token n)
+    if (split) {
+        // partial tile, [n_local][m_local]
+        float *pt = sp.part + (uint64_t)unit * (QG_BM * QG_BN);
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const uint32_t nl = wn * 64 + j * 32 + (lane & 31);
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const uint32_t ml = wm * 64 + i * 32 + 8 * q + 4 * (lane >> 5);
+                    const floatx16 &c = acc[i][j];
+                    *(float4 *)(pt + nl * QG_BM + ml) =
+                        make_float4(c[4 * q], c[4 * q + 1], c[4 * q + 2], c[4 * q + 3]);
+                }
+            }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 2; i++)
 #pragma unroll
@@ -325,6 +375,41 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_kernel(const uint8_t *__restr
                 }
             }
         }
+}
+
+// Y of the split tiles: workgroup b sums float4 (b % 16) * 256 + t of split
+// tile b / 16 over its ks partials, in K order (all ks loads issued first).
+constexpr uint32_t QG_SUM_WG = QG_BM * QG_BN / (4 * 256);  // workgroups per tile
+__global__ __launch_bounds__(256) void gemm_split_sum_kernel(const float *__restrict__ part,
+                                                             float *__restrict__ Y, uint32_t M,
+                                                             uint32_t N, GemmSplit sp) {
+    const uint32_t lt = blockIdx.x / QG_SUM_WG, tile = sp.full + lt;
+    const uint32_t e = ((blockIdx.x % QG_SUM_WG) * 256 + threadIdx.x) * 4;
+    const uint32_t nl = e / QG_BM, ml = e % QG_BM;
+    const uint32_t m = tile / sp.tiles_n * QG_BM + ml, n = tile % sp.tiles_n * QG_BN + nl;
+    if (n >= N || m >= M) return;
+    const float *p0 = part + (uint64_t)lt * sp.ks * (QG_BM * QG_BN) + e;
+    float4 w[8];
+#pragma unroll
+    for (uint32_t c = 0; c < 8; c++)
+        if (c < sp.ks) w[c] = *(const float4 *)(p0 + (uint64_t)c * (QG_BM * QG_BN));
+    float4 v = w[0];
+#pragma unroll
+    for (uint32_t c = 1; c < 8; c++)
+        if (c < sp.ks) {
+            v.x += w[c].x;
+            v.y += w[c].y;
+            v.z += w[c].z;
+            v.w += w[c].w;
+        }
+    float *dst = Y + (uint64_t)n * M + m;
+    if (m + 3 < M && (M & 3) == 0) {
+        *(float4 *)dst = v;
+    } else {
+        const float vv[4] = {v.x, v.y, v.z, v.w};
+        for (int k = 0; k < 4; k++)
+            if (m + k < M) dst[k] = vv[k];
+    }
 }
 
 }  // namespace okf

@@ -17,6 +17,7 @@
 #include "okf_common.h"
 #include "okf_decode.h"
 #include "okf_gemm.h"
+#include <algorithm>
 #include "okf_gemv.h"
 
 #include "iq2xxs_grid.inc"
@@ -35,6 +36,8 @@ struct okf_ctx {
     int last_hip = 0;
     _Float16 *xh = nullptr;  // fp16 copy of the GEMM activations (grown on demand)
     size_t xh_bytes = 0;
+    float *part = nullptr;   // split-tile partial sums of the Q4_K GEMM (grown on demand)
+    size_t part_bytes = 0;
 };
 
 namespace {
@@ -180,9 +183,41 @@ int launch_gemm(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t 
         hipLaunchKernelGGL(x_to_f16_kernel, dim3((uint32_t)((n4 + 255) / 256)), dim3(256), 0, c->stream,
                            X, c->xh, n4);
         const uint32_t tm = (M + QG_BM - 1) / QG_BM, tn = (N + QG_BN - 1) / QG_BN;
-        const uint32_t tiles = tm * tn, per_xcd = (tiles + 7) / 8;
-        hipLaunchKernelGGL(gemm_q4k_kernel, dim3(per_xcd * 8), dim3(256), 0, c->stream, W, rb, K, M,
-                           (const _Float16 *)c->xh, N, Y, tn, tiles, per_xcd);
+        GemmSplit sp{};
+        sp.tiles_n = tn;
+        sp.tiles = tm * tn;
+        // whole rounds of 256 tiles stay whole; the remainder is split over
+        // up to 8 K ranges (whole step pairs) to give every CU a share
+        const uint32_t pairs = K / (2 * QG_BK), rem = sp.tiles % 256;
+        sp.full = sp.tiles - rem;
+        sp.ks = rem ? std::min(std::min(256u / rem, 8u), pairs) : 1;
+        if (sp.ks < 2) {
+            sp.full = sp.tiles + 7 & ~7u;  // no split: every tile whole
+            sp.ks = 1;
+        }
+        sp.full_xcd = sp.full / 8;
+        sp.units = sp.ks > 1 ? rem * sp.ks : 0;
+        sp.units_xcd = (sp.units + 7) / 8;
+        if (sp.units) {
+            const size_t pb = (size_t)sp.units * QG_BM * QG_BN * sizeof(float);
+            if (pb > c->part_bytes) {
+                hipError_t e = hipStreamSynchronize(c->stream);
+                if (e != hipSuccess) return hip_fail(c, e);
+                if (c->part) (void)hipFree(c->part);
+                c->part = nullptr;
+                c->part_bytes = 0;
+                e = hipMalloc((void **)&c->part, pb);
+                if (e != hipSuccess) return hip_fail(c, e);
+                c->part_bytes = pb;
+            }
+            sp.part = c->part;
+        }
+        const uint32_t grid = 8 * (sp.full_xcd + sp.units_xcd);
+        hipLaunchKernelGGL(gemm_q4k_kernel, dim3(grid), dim3(256), 0, c->stream, W, rb, K, M,
+                           (const _Float16 *)c->xh, N, Y, sp);
+        if (sp.units)
+            hipLaunchKernelGGL(gemm_split_sum_kernel, dim3((sp.tiles - sp.full) * QG_SUM_WG), dim3(256), 0, c->stream,
+                               (const float *)c->part, Y, M, N, sp);
         return OKF_OK;
     }
     dim3 grid((N + GB_N - 1) / GB_N, (M + GB_M - 1) / GB_M);
@@ -283,6 +318,7 @@ int okf_ctx_destroy(okf_ctx *c) {
         (void)hipFree(c->grid);
         (void)hipFree(c->tab);
         if (c->xh) (void)hipFree(c->xh);
+        if (c->part) (void)hipFree(c->part);
         (void)hipStreamDestroy(c->stream);
     }
     delete c;

@@ -176,8 +176,10 @@ def test_iq2_xxs_mtp_verify_full_config(enc):
 # (The metric is relative to max|ref| over the output, so every case keeps
 # enough outputs for that maximum to be representative; a single dot product
 # can cancel to near zero, where fp16 staging error is not bounded by 1e-3.)
+# The Q4_K kernel splits the tiles beyond whole rounds of 256 over K ranges:
+# (4224, 256, 512) has 132 tiles and no split, the others split 2..8 ways.
 TILE = [(Q8_0, 300, 2048, 37), (Q2_0, 130, 1024, 129), (Q4_K, 260, 2304, 77), (IQ2_XXS, 129, 1536, 6),
-        (Q4_K, 1, 256, 64), (Q8_0, 5, 96, 200)]
+        (Q4_K, 1, 256, 64), (Q8_0, 5, 96, 200), (Q4_K, 4224, 256, 512), (Q4_K, 1000, 512, 300)]
 
 
 @pytest.mark.parametrize("t,M,K,N", TILE)
