@@ -149,10 +149,17 @@ def main():
         dw = [ok.QuantTensor(d, M1, K1, ok.Q2_0).c() for d in downs]
         xp, hp, h2p, yp, hxp = (t.data_ptr() for t in (x, h, h2, y, hx))
 
+        # gate and up in one parallel group, as the reference's FFN encodes
+        # them (LLM/Qwen/QwenMetalEngine.swift:918-923, MetalEnc.parallel)
+        pbegin, pend, hctx = enc._lib.okf_parallel_begin, enc._lib.okf_parallel_end, enc.h
+
         def ffn_step(i):
             j = i % nrot
+            pbegin(hctx)
             gemv_c(gw[j], xp, hp)
             gemv_c(uw[j], xp, h2p)
+            if pend(hctx):
+                raise RuntimeError("okf_parallel_end failed")
             gemv_c(dw[j], hxp, yp)
 
         for i in range(args.warmup):
@@ -166,10 +173,17 @@ def main():
         value = step_bytes / step_s / 1e9
 
         # dominant kernel of the step: HIP events around batches of its launches
-        gate_t, _ = time_calls(lambda i: gemv_c(gw[i % nrot], xp, hp), args.steps, 5)
+        def gate_up(i):
+            j = i % nrot
+            pbegin(hctx)
+            gemv_c(gw[j], xp, hp)
+            gemv_c(uw[j], xp, h2p)
+            pend(hctx)
+
+        gate_t, _ = time_calls(gate_up, args.steps, 5)
         down_t, _ = time_calls(lambda i: gemv_c(dw[i % nrot], hxp, yp), args.steps, 5)
         if gate_t >= down_t:
-            dom = ("q2_0_matvec_6144x2048", gate_np.nbytes, gate_t)
+            dom = ("q2_0_matvec_gate_up_2x6144x2048", gate_np.nbytes + up_np.nbytes, gate_t)
         else:
             dom = ("q2_0_matvec_2048x6144", down_np.nbytes, down_t)
         roofline = {"kernel": f"okf::gemv_kernel<Q2_0> ({dom[0]})", "bound": "hbm",
@@ -177,7 +191,7 @@ def main():
                     "unit": "GB/s", "frac": round(dom[1] / dom[2] / HBM_PEAK, 4),
                     "traffic": load_traffic(dom[0]), "us_per_launch": round(dom[2] * 1e6, 3),
                     "algorithmic_bytes_per_launch": dom[1]}
-        log(f"bench: ffn step {step_s*1e6:.2f} us, {value:.1f} GB/s; gate {gate_t*1e6:.2f} us, "
+        log(f"bench: ffn step {step_s*1e6:.2f} us, {value:.1f} GB/s; gate+up {gate_t*1e6:.2f} us, "
             f"down {down_t*1e6:.2f} us")
         del gates, ups, downs
         torch.cuda.empty_cache()
@@ -188,6 +202,8 @@ def main():
         ("q8_0_matvec_2048x2048", ok.Q8_0, 2048, 2048, 1, 1001, 2001),
         ("q2_0_matvec_6144x2048", ok.Q2_0, 6144, 2048, 1, 1002, 2002),
         ("q2_0_matvec_2048x6144", ok.Q2_0, 2048, 6144, 1, 1102, 2102),
+        # gate and up as one parallel group (two weight seeds, one x)
+        ("q2_0_matvec_gate_up_2x6144x2048", ok.Q2_0, 6144, 2048, 1, (1002, 1202), 2002),
         ("q4_k_matvec_17408x5120", ok.Q4_K, 17408, 5120, 1, 1003, 2003),
         ("q4_k_matvec_5120x17408", ok.Q4_K, 5120, 17408, 1, 1103, 2103),
         ("iq2_xxs_matvec_17408x5120_m1", ok.IQ2_XXS, 17408, 5120, 1, 1004, 2004),
@@ -200,23 +216,31 @@ def main():
     for name, t, M, K, N, ws, xs in SUITE:
         if want is not None and name not in want:
             continue
-        key = (t, M, K, ws)
+        seeds = ws if isinstance(ws, tuple) else (ws,)
+        key = (t, M, K, seeds)
         if key not in wcache:
             wcache.clear()
             torch.cuda.empty_cache()
             log(f"bench: generating {name}")
-            w_np = synth.weights(t, M, K, ws)
-            wcache[key] = (w_np.nbytes, rotated(w_np))
-        wbytes, copies = wcache[key]
+            ws_np = [synth.weights(t, M, K, sd) for sd in seeds]
+            wcache[key] = (sum(w.nbytes for w in ws_np), [rotated(w) for w in ws_np])
+        wbytes, copies_l = wcache[key]
         X = torch.from_numpy(synth.activations(N, K, xs)).cuda()
-        Y = torch.empty((N, M), device="cuda")
-        nr = len(copies)
+        Ys = [torch.empty((N, M), device="cuda") for _ in seeds]
+        nr = len(copies_l[0])
+        wcs_l = [[ok.QuantTensor(c, K, M, t).c() for c in copies] for copies in copies_l]
+        xp_, yps = X.data_ptr(), [Y.data_ptr() for Y in Ys]
 
-        wcs = [ok.QuantTensor(c, K, M, t).c() for c in copies]
-        xp_, yp_ = X.data_ptr(), Y.data_ptr()
-
-        def call(i, wcs=wcs, N=N, xp_=xp_, yp_=yp_, nr=nr):
-            enc.raw_gemm(wcs[i % nr], xp_, N, yp_)
+        if len(seeds) == 1:
+            def call(i, wcs=wcs_l[0], N=N, xp_=xp_, yp_=yps[0], nr=nr):
+                enc.raw_gemm(wcs[i % nr], xp_, N, yp_)
+        else:
+            def call(i, wcs_l=wcs_l, xp_=xp_, yps=yps, nr=nr):
+                enc._lib.okf_parallel_begin(enc.h)
+                for wcs, yp_ in zip(wcs_l, yps):
+                    enc.raw_gemv(wcs[i % nr], xp_, yp_)
+                if enc._lib.okf_parallel_end(enc.h):
+                    raise RuntimeError("okf_parallel_end failed")
 
         n_calls = args.steps if N < 512 else max(10, args.steps // 10)
         mean_s, med_s = time_calls(call, n_calls, max(3, args.warmup // 2))  # (mean, best batch)
@@ -230,7 +254,7 @@ def main():
             rec["bound"], rec["frac"] = "hbm", round(wbytes / mean_s / HBM_PEAK, 4)
         log("bench:", json.dumps(rec))
         suite.append(rec)
-        del X, Y
+        del X, Ys
     wcache.clear()
 
     # ----------------------------------------------------------- CPU baseline
@@ -272,7 +296,8 @@ def main():
         "dtype": "f16 x f16 products, f32 accumulate (weights dequantized exactly to f16)",
         "data": "synthetic (reference LCG, BASELINE.json distributions); weights rotated over >= 1 GiB",
         "config": {"workload": "BASELINE configs[1]: Bonsai-1.7B ternary FFN decode step, one token: "
-                               "gate+up Q2_0 W 6144x2048 and down Q2_0 W 2048x6144 matvecs",
+                               "gate+up Q2_0 W 6144x2048 (one parallel group, as the reference "
+                               "encodes them) and down Q2_0 W 2048x6144 matvecs",
                    "weight_bytes_per_step": step_bytes, "parallelism": "single GPU"},
         "roofline": roofline,
         "cpu_baseline": cpu,

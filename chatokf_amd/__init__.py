@@ -11,6 +11,7 @@ binding raises.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 
@@ -24,8 +25,8 @@ OKF_OK, OKF_E_TYPE, OKF_E_SHAPE, OKF_E_HIP, OKF_E_INJECTED, OKF_E_ARG, OKF_E_NOD
 # Every symbol include/okf_quant.h declares.
 EXPORTS = (
     "okf_ctx_create", "okf_ctx_destroy", "okf_ctx_stream", "okf_row_bytes",
-    "okf_gemv", "okf_gemm", "okf_gemm_tile", "okf_dequant_row", "okf_sync",
-    "okf_set_fault_rate", "okf_last_hip_error", "okf_strerror",
+    "okf_gemv", "okf_gemm", "okf_gemm_tile", "okf_dequant_row", "okf_parallel_begin",
+    "okf_parallel_end", "okf_sync", "okf_set_fault_rate", "okf_last_hip_error", "okf_strerror",
 )
 
 
@@ -68,6 +69,8 @@ def _lib():
             "okf_gemm": [vp, W, vp, u32, vp],
             "okf_gemm_tile": [vp, W, vp, u32, vp],
             "okf_dequant_row": [vp, W, u32, vp],
+            "okf_parallel_begin": [vp],
+            "okf_parallel_end": [vp],
             "okf_sync": [vp],
             "okf_set_fault_rate": [vp, ctypes.c_double, u64],
             "okf_last_hip_error": [vp],
@@ -179,6 +182,16 @@ class Enc:
         wc = w.c()
         self._check(self._lib.okf_dequant_row(self.h, ctypes.byref(wc), int(n), _ptr(out)),
                     "okf_dequant_row")
+
+    @contextlib.contextmanager
+    def parallel(self):
+        """MetalEnc.parallel (``LLM/Base/MetalEnc.swift:42-47``): the matvecs
+        issued inside carry no order among themselves and launch together."""
+        self._check(self._lib.okf_parallel_begin(self.h), "okf_parallel_begin")
+        try:
+            yield self
+        finally:
+            self._check(self._lib.okf_parallel_end(self.h), "okf_parallel_end")
 
     def sync(self):
         self._check(self._lib.okf_sync(self.h), "okf_sync")

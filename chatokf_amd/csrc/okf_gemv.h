@@ -406,7 +406,8 @@ constexpr int GV_SLOTS = 4;
 template <int F, int NC, int R, int D, int S>
 __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ W, uint64_t row_bytes, uint32_t K,
                                           uint32_t M, const float *__restrict__ X, float *__restrict__ Y,
-                                          const u32x4 *__restrict__ tab_g, uint32_t cunits) {
+                                          const u32x4 *__restrict__ tab_g, uint32_t cunits,
+                                          uint32_t blk) {
     constexpr int L = GV_L;
     extern __shared__ u32x4 lds[];
     constexpr uint32_t TAB = F == IQ2_XXS ? 384 : 0;
@@ -419,7 +420,7 @@ __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ W, uint64_
     if constexpr (F == IQ2_XXS)
         for (uint32_t e = tid; e < TAB; e += nthr) tab[e] = tab_g[e];
 
-    const uint32_t m0 = ((blockIdx.x * groups + group) * GV_SLOTS + slot) * R;
+    const uint32_t m0 = ((blk * groups + group) * GV_SLOTS + slot) * R;
     const uint8_t *rows[R];
 #pragma unroll
     for (int r = 0; r < R; r++) rows[r] = W + (uint64_t)min(m0 + r, M - 1) * row_bytes;
@@ -543,14 +544,28 @@ __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ W, uint64_
 }
 
 
+// Up to GV_GROUP matrices of one format and one K in one launch (the
+// reference's concurrent dispatch group, MetalEnc.parallel): workgroups
+// [end[i-1], end[i]) compute y_i = W_i x_i.
+constexpr int GV_GROUP = 4;
+struct GemvGroup {
+    const uint8_t *W[GV_GROUP];
+    const float *X[GV_GROUP];
+    float *Y[GV_GROUP];
+    uint32_t M[GV_GROUP];
+    uint32_t end[GV_GROUP];
+    uint32_t n;
+};
+
 template <int F, int NC, int R, int D, int S>
-__global__ __launch_bounds__(256) void gemv_kernel(const uint8_t *__restrict__ W, uint64_t row_bytes,
-                                                   uint32_t K, uint32_t M,
-                                                   const float *__restrict__ X,
-                                                   float *__restrict__ Y,
-                                                   const u32x4 *__restrict__ tab_g,
-                                                   uint32_t cunits) {
-    gemv_body<F, NC, R, D, S>(W, row_bytes, K, M, X, Y, tab_g, cunits);
+__global__ __launch_bounds__(256) void gemv_kernel(GemvGroup g, uint64_t row_bytes, uint32_t K,
+                                                   const u32x4 *__restrict__ tab_g, uint32_t cunits) {
+    uint32_t i = 0;
+#pragma unroll
+    for (int k = 0; k + 1 < GV_GROUP; k++)
+        if (k + 1 < (int)g.n && blockIdx.x >= g.end[k]) i = k + 1;
+    const uint32_t blk = blockIdx.x - (i ? g.end[i - 1] : 0);
+    gemv_body<F, NC, R, D, S>(g.W[i], row_bytes, K, g.M[i], g.X[i], g.Y[i], tab_g, cunits, blk);
 }
 
 }  // namespace okf

@@ -18,9 +18,18 @@
 #include "okf_decode.h"
 #include "okf_gemm.h"
 #include <algorithm>
+#include <vector>
 #include "okf_gemv.h"
 
 #include "iq2xxs_grid.inc"
+
+// one matvec y = W x of a launch group
+struct GemvCall {
+    const uint8_t *W;
+    const float *X;
+    float *Y;
+    uint32_t M;
+};
 
 struct okf_ctx {
     int device = -1;
@@ -36,6 +45,15 @@ struct okf_ctx {
     int last_hip = 0;
     _Float16 *xh = nullptr;  // fp16 copy of the GEMM activations (grown on demand)
     size_t xh_bytes = 0;
+    // okf_parallel_begin .. okf_parallel_end: recorded matvecs
+    struct Pending {
+        int32_t type;
+        uint32_t K;
+        uint64_t rb;
+        GemvCall call;
+    };
+    bool grouping = false;
+    std::vector<Pending> pending;
     float *part = nullptr;   // split-tile partial sums of the Q4_K GEMM (grown on demand)
     size_t part_bytes = 0;
 };
@@ -109,8 +127,8 @@ void build_iq2_tables(uint32_t *t) {
 }
 
 template <int F, int NC, int S>
-void launch_gemv_s(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t M, const float *X,
-                   float *Y, uint32_t cunits, size_t lds) {
+void launch_gemv_s(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32_t K,
+                   uint32_t cunits, size_t lds) {
     constexpr int R = 1, D = 2, WAVES = 4;
     const void *fn = (const void *)gemv_kernel<F, NC, R, D, S>;
     static bool attr = false;  // one attribute call per instantiation
@@ -119,9 +137,19 @@ void launch_gemv_s(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32
         attr = true;
     }
     const uint32_t rows_per_wg = (WAVES / S) * GV_SLOTS * R;
-    dim3 grid((M + rows_per_wg - 1) / rows_per_wg);
-    hipLaunchKernelGGL((gemv_kernel<F, NC, R, D, S>), grid, dim3(64 * WAVES), lds, c->stream, W, rb, K,
-                       M, X, Y, c->tab, cunits);
+    GemvGroup g{};
+    uint32_t total = 0;
+    for (int i = 0; i < n; i++) {
+        g.W[i] = calls[i].W;
+        g.X[i] = calls[i].X;
+        g.Y[i] = calls[i].Y;
+        g.M[i] = calls[i].M;
+        total += (calls[i].M + rows_per_wg - 1) / rows_per_wg;
+        g.end[i] = total;
+    }
+    g.n = (uint32_t)n;
+    hipLaunchKernelGGL((gemv_kernel<F, NC, R, D, S>), dim3(total), dim3(64 * WAVES), lds, c->stream,
+                       g, rb, K, c->tab, cunits);
 }
 
 // Launch geometry: 256-thread workgroups of four wavefronts, each four row
@@ -130,8 +158,7 @@ void launch_gemv_s(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32
 // shorter wavefronts); measured on MI355X, a four-way split loses to the
 // extra activation staging it needs.
 template <int F, int NC>
-void launch_gemv_nc(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t M,
-                    const float *X, float *Y) {
+void launch_gemv_nc(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32_t K) {
     constexpr uint32_t UW = unit_weights<F>();
     const size_t tab = F == IQ2_XXS ? 384 * 16 : 0;
     const uint32_t units = K / UW;
@@ -142,22 +169,23 @@ void launch_gemv_nc(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint3
     const size_t budget = c->max_lds - tab - red;
     if (cunits * per_unit > budget) cunits = (uint32_t)(budget / per_unit) / 64 * 64;
     const size_t lds = tab + cunits * per_unit + red;
-    const uint32_t waves1 = (M + GV_SLOTS - 1) / GV_SLOTS;  // wavefronts without a split
+    uint32_t rows = 0;
+    for (int i = 0; i < n; i++) rows += calls[i].M;
+    const uint32_t waves1 = (rows + GV_SLOTS - 1) / GV_SLOTS;  // wavefronts without a split
     uint32_t S = c->gemv_s ? (uint32_t)c->gemv_s : (NC == 1 && waves1 < 3072 ? 2 : 1);
-    if (S >= 4) launch_gemv_s<F, NC, 4>(c, W, rb, K, M, X, Y, cunits, lds);
-    else if (S == 2) launch_gemv_s<F, NC, 2>(c, W, rb, K, M, X, Y, cunits, lds);
-    else launch_gemv_s<F, NC, 1>(c, W, rb, K, M, X, Y, cunits, lds);
+    if (S >= 4) launch_gemv_s<F, NC, 4>(c, calls, n, rb, K, cunits, lds);
+    else if (S == 2) launch_gemv_s<F, NC, 2>(c, calls, n, rb, K, cunits, lds);
+    else launch_gemv_s<F, NC, 1>(c, calls, n, rb, K, cunits, lds);
 }
 
 template <int F>
-void launch_gemv(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t M, const float *X,
-                 uint32_t N, float *Y) {
+void launch_gemv(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32_t K, uint32_t N) {
     switch (N) {
-    case 1: launch_gemv_nc<F, 1>(c, W, rb, K, M, X, Y); break;
-    case 2: launch_gemv_nc<F, 2>(c, W, rb, K, M, X, Y); break;
-    case 3: launch_gemv_nc<F, 3>(c, W, rb, K, M, X, Y); break;
-    case 4: launch_gemv_nc<F, 4>(c, W, rb, K, M, X, Y); break;
-    default: launch_gemv_nc<F, 5>(c, W, rb, K, M, X, Y); break;
+    case 1: launch_gemv_nc<F, 1>(c, calls, n, rb, K); break;
+    case 2: launch_gemv_nc<F, 2>(c, calls, n, rb, K); break;
+    case 3: launch_gemv_nc<F, 3>(c, calls, n, rb, K); break;
+    case 4: launch_gemv_nc<F, 4>(c, calls, n, rb, K); break;
+    default: launch_gemv_nc<F, 5>(c, calls, n, rb, K); break;
     }
 }
 
@@ -253,7 +281,13 @@ int run_gemm(okf_ctx *c, const okf_weight *w, const float *X, uint32_t N, float 
     if ((st = begin(c))) return st;
     const uint8_t *W = (const uint8_t *)w->base + w->off;
     if (path == Path::Auto && N <= 5) {
-        OKF_DISPATCH(w->ggml_type, launch_gemv, c, W, rb, w->K, w->M, X, N, Y);
+        const GemvCall call{W, X, Y, w->M};
+        if (c->grouping && N == 1) {
+            // inside a parallel group: launched together at okf_parallel_end
+            c->pending.push_back({w->ggml_type, w->K, rb, call});
+            return OKF_OK;
+        }
+        OKF_DISPATCH(w->ggml_type, launch_gemv, c, &call, 1, rb, w->K, N);
     } else {
         switch (w->ggml_type) {
         case Q8_0: st = launch_gemm<Q8_0>(c, W, rb, w->K, w->M, X, N, Y); break;
@@ -264,6 +298,26 @@ int run_gemm(okf_ctx *c, const okf_weight *w, const float *X, uint32_t N, float 
         if (st) return st;
     }
     return finish(c);
+}
+
+// Launches the recorded matvecs: those of one format and one K together,
+// GV_GROUP at a time, in recording order otherwise.
+int flush_group(okf_ctx *c) {
+    std::vector<okf_ctx::Pending> p;
+    p.swap(c->pending);
+    std::vector<bool> done(p.size(), false);
+    for (size_t i = 0; i < p.size(); i++) {
+        if (done[i]) continue;
+        GemvCall calls[GV_GROUP];
+        int n = 0;
+        for (size_t j = i; j < p.size() && n < GV_GROUP; j++)
+            if (!done[j] && p[j].type == p[i].type && p[j].K == p[i].K) {
+                calls[n++] = p[j].call;
+                done[j] = true;
+            }
+        OKF_DISPATCH(p[i].type, launch_gemv, c, calls, n, p[i].rb, p[i].K, 1u);
+    }
+    return p.empty() ? OKF_OK : finish(c);
 }
 
 }  // namespace
@@ -364,10 +418,32 @@ int okf_dequant_row(okf_ctx *c, const okf_weight *row, uint32_t n, float *out) {
     return finish(c);
 }
 
+int okf_parallel_begin(okf_ctx *c) {
+    if (!c) return OKF_E_ARG;
+    if (c->grouping) return OKF_E_ARG;
+    c->grouping = true;
+    return OKF_OK;
+}
+
+int okf_parallel_end(okf_ctx *c) {
+    if (!c) return OKF_E_ARG;
+    if (!c->grouping) return OKF_E_ARG;
+    c->grouping = false;
+    if (c->pending.empty()) return OKF_OK;
+    if (c->device < 0) return OKF_E_NODEV;
+    (void)hipSetDevice(c->device);
+    return flush_group(c);
+}
+
 int okf_sync(okf_ctx *c) {
     if (!c) return OKF_E_ARG;
     if (c->device < 0) return OKF_E_NODEV;
     (void)hipSetDevice(c->device);
+    if (!c->pending.empty()) {
+        c->grouping = false;
+        int st = flush_group(c);
+        if (st) return st;
+    }
     hipError_t e = hipStreamSynchronize(c->stream);
     return e == hipSuccess ? OKF_OK : hip_fail(c, e);
 }

@@ -94,6 +94,16 @@ int okf_gemm_tile(okf_ctx *ctx, const okf_weight *w, const float *X, uint32_t N,
  * ignored; n must be a whole number of blocks. */
 int okf_dequant_row(okf_ctx *ctx, const okf_weight *row, uint32_t n, float *out);
 
+/* MetalEnc.parallel (MetalEnc.swift:42-47, used for the FFN gate and up
+ * projections, LLM/Qwen/QwenMetalEngine.swift:918-923): okf_gemv calls
+ * between okf_parallel_begin and okf_parallel_end carry no order among
+ * themselves.  They are validated when called and launched at
+ * okf_parallel_end, those of one format and one K as a single grid (up to
+ * four matrices per launch).  Other calls in the group launch at once.
+ * okf_sync inside a group ends it.  Nesting is an OKF_E_ARG. */
+int okf_parallel_begin(okf_ctx *ctx);
+int okf_parallel_end(okf_ctx *ctx);
+
 /* Waits for all work on the context's stream: the analogue of
  * commit + waitUntilCompleted (LLM/Base/MetalGates.swift:144-149).  Returns
  * OKF_E_HIP if a kernel failed. */

@@ -100,3 +100,18 @@ def test_fault_injection_is_seeded(detached):
 def test_bad_device_id():
     with pytest.raises(ok.OkfError):
         ok.Enc(-2)
+
+
+def test_parallel_group_pairing(detached):
+    # MetalEnc.parallel analogue: begin/end pair, no nesting
+    lib, h = ok.lib(), detached.h
+    assert lib.okf_parallel_end(h) == ok.OKF_E_ARG
+    assert lib.okf_parallel_begin(h) == ok.OKF_OK
+    assert lib.okf_parallel_begin(h) == ok.OKF_E_ARG
+    # calls inside a group are validated when made
+    with pytest.raises(ok.OkfError) as e:
+        detached.gemv(ok.QuantTensor(FAKE, 5000, 16, ok.Q4_K), FAKE, FAKE)
+    assert e.value.status == ok.OKF_E_SHAPE
+    assert lib.okf_parallel_end(h) == ok.OKF_OK
+    with detached.parallel():
+        pass

@@ -172,6 +172,35 @@ def test_iq2_xxs_mtp_verify_full_config(enc):
     assert r <= TOL
 
 
+# ------------------------------------------------------------ parallel group
+def test_parallel_group_matches_single_calls(enc):
+    # MetalEnc.parallel { gate; up } (QwenMetalEngine.swift:918-923) plus more
+    # matrices than one launch takes, of two formats and two K: every output
+    # equals its single okf_gemv within float reassociation.
+    cases = [(Q2_0, 6144, 2048, 1002), (Q2_0, 6144, 2048, 1202), (Q8_0, 300, 2048, 61),
+             (Q2_0, 200, 2048, 62), (Q2_0, 130, 1024, 63), (Q2_0, 64, 2048, 64), (Q2_0, 96, 2048, 65),
+             (Q8_0, 40, 2048, 66)]
+    xs = {K: dev(acts(1, K, 70 + K)) for K in (1024, 2048)}
+    ws, ys, singles = [], [], []
+    for t, M, K, seed in cases:
+        w = dev(weights(t, M, K, seed))
+        ws.append(ok.QuantTensor(w, K, M, t))
+        ys.append(torch.full((M,), float("nan"), device="cuda"))
+        y1 = torch.full((M,), float("nan"), device="cuda")
+        enc.gemv(ws[-1], xs[K], y1)
+        singles.append(y1)
+    with enc.parallel():
+        for q, y in zip(ws, ys):
+            enc.gemv(q, xs[q.K], y)
+    enc.sync()
+    for (t, M, K, seed), y, y1 in zip(cases, ys, singles):
+        got, one = host(y), host(y1)
+        ref = oracle.matvec(t, weights(t, M, K, seed), K, M, acts(1, K, 70 + K)[0]).astype(np.float64)
+        say("group", NAMES[t], M, K, rel(got, ref))
+        assert rel(got, ref) <= TOL
+        assert rel(got, one.astype(np.float64)) <= 1e-5
+
+
 # ------------------------------------------------------------------ tile GEMM
 # (The metric is relative to max|ref| over the output, so every case keeps
 # enough outputs for that maximum to be representative; a single dot product
