@@ -403,6 +403,47 @@ __device__ __forceinline__ float slot_sum(float v) {
 constexpr int GV_L = 16;  // lanes per row slot
 constexpr int GV_SLOTS = 4;
 
+// Stages activation slots [0, nslots) of chunk c0 (all NC columns) into LDS
+// as packed fp16 and per-32 sums.  SP passes per round: every pass's global
+// loads are issued before the first is packed.
+template <int F, int NC, int L, uint32_t SP>
+__device__ __forceinline__ void stage_x(const float *__restrict__ X, uint32_t K, uint32_t c0,
+                                        uint32_t nslots, uint32_t tid, uint32_t nthr, uint32_t *xs,
+                                        uint32_t cs, float *xsum, uint32_t xcs) {
+    constexpr uint32_t UW = unit_weights<F>(), SL = UW / 8;
+    for (uint32_t q0 = 0; q0 < nslots; q0 += SP * nthr) {
+        floatx4 A[SP][NC], B[SP][NC];
+#pragma unroll
+        for (uint32_t p = 0; p < SP; p++) {
+            const uint32_t q = min(q0 + p * nthr + tid, nslots - 1), u = q / SL;
+            uint32_t kb;
+            const uint32_t ka = slot_first<F>(q % SL, kb);
+#pragma unroll
+            for (int n = 0; n < NC; n++) {
+                const float *xb = X + (uint64_t)n * K + (uint64_t)(c0 + u) * UW;
+                A[p][n] = *(const floatx4 *)(xb + ka);
+                B[p][n] = *(const floatx4 *)(xb + kb);
+            }
+        }
+#pragma unroll
+        for (uint32_t p = 0; p < SP; p++) {
+            const uint32_t q = q0 + p * nthr + tid, u = q / SL, sidx = q % SL;
+            const bool in = q < nslots;
+#pragma unroll
+            for (int n = 0; n < NC; n++) {
+                const u32x4 v = slot_pack<F>(A[p][n], B[p][n]);
+                float pt = slot_total(v);
+                pt += __shfl_xor(pt, 1, 64);
+                pt += __shfl_xor(pt, 2, 64);
+                if (in) {
+                    *(u32x4 *)(xs + n * cs + xs_index<F, L>(u, 4 * sidx)) = v;
+                    if ((q & 3) == 0) xsum[n * xcs + q / 4] = pt;
+                }
+            }
+        }
+    }
+}
+
 template <int F, int NC, int R, int D, int S>
 __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ W, uint64_t row_bytes, uint32_t K,
                                           uint32_t M, const float *__restrict__ X, float *__restrict__ Y,
@@ -456,40 +497,12 @@ __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ W, uint64_
         // group) sit in 4 consecutive lanes of a wavefront (nthr % 64 == 0)
         constexpr uint32_t SL = UW / 8;
         const uint32_t nslots = cn * SL;
-        // SP passes per round: every pass's global loads are issued before
-        // the first is packed, so staging costs one load latency, not SP
         constexpr uint32_t SP = NC == 1 ? 4 : NC == 2 ? 2 : 1;
-        for (uint32_t q0 = 0; q0 < nslots; q0 += SP * nthr) {
-            floatx4 A[SP][NC], B[SP][NC];
-#pragma unroll
-            for (uint32_t p = 0; p < SP; p++) {
-                const uint32_t q = min(q0 + p * nthr + tid, nslots - 1), u = q / SL;
-                uint32_t kb;
-                const uint32_t ka = slot_first<F>(q % SL, kb);
-#pragma unroll
-                for (int n = 0; n < NC; n++) {
-                    const float *xb = X + (uint64_t)n * K + (uint64_t)(c0 + u) * UW;
-                    A[p][n] = *(const floatx4 *)(xb + ka);
-                    B[p][n] = *(const floatx4 *)(xb + kb);
-                }
-            }
-#pragma unroll
-            for (uint32_t p = 0; p < SP; p++) {
-                const uint32_t q = q0 + p * nthr + tid, u = q / SL, sidx = q % SL;
-                const bool in = q < nslots;
-#pragma unroll
-                for (int n = 0; n < NC; n++) {
-                    const u32x4 v = slot_pack<F>(A[p][n], B[p][n]);
-                    float pt = slot_total(v);
-                    pt += __shfl_xor(pt, 1, 64);
-                    pt += __shfl_xor(pt, 2, 64);
-                    if (in) {
-                        *(u32x4 *)(xs + n * cs + xs_index<F, L>(u, 4 * sidx)) = v;
-                        if ((q & 3) == 0) xsum[n * xcs + q / 4] = pt;
-                    }
-                }
-            }
-        }
+        // (a chunk that one pass covers takes the one-pass copy: no idle passes)
+        if (nslots <= nthr)
+            stage_x<F, NC, L, 1>(X, K, c0, nslots, tid, nthr, xs, cs, xsum, xcs);
+        else
+            stage_x<F, NC, L, SP>(X, K, c0, nslots, tid, nthr, xs, cs, xsum, xcs);
         __syncthreads();
         // stream the wavefront's units u = c0 + i + L (part + S t) through
         // the ring
