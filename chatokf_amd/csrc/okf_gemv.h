@@ -498,9 +498,11 @@ __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ W, uint64_
         constexpr uint32_t SL = UW / 8;
         const uint32_t nslots = cn * SL;
         constexpr uint32_t SP = NC == 1 ? 4 : NC == 2 ? 2 : 1;
-        // (a chunk that one pass covers takes the one-pass copy: no idle passes)
+        // (a chunk that one or three passes cover takes that copy: no idle passes)
         if (nslots <= nthr)
             stage_x<F, NC, L, 1>(X, K, c0, nslots, tid, nthr, xs, cs, xsum, xcs);
+        else if (SP == 4 && nslots <= 3 * nthr)
+            stage_x<F, NC, L, (SP == 4 ? 3 : 1)>(X, K, c0, nslots, tid, nthr, xs, cs, xsum, xcs);
         else
             stage_x<F, NC, L, SP>(X, K, c0, nslots, tid, nthr, xs, cs, xsum, xcs);
         __syncthreads();
