@@ -382,11 +382,30 @@ struct Compute<Q2_0, NC, R> {
 };
 
 // Sum over the L lanes of a row slot (every lane of the slot gets it).
+// DPP lane moves (one VALU op, no LDS round trip): quad_perm [1,0,3,2] and
+// [2,3,0,1] swap neighbours and pairs within a quad; row_half_mirror (lane
+// i <- 7 - i of its 8) and row_mirror (i <- 15 - i of its 16) pair quads
+// and half-rows.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                                 0xF, 0xF, false));
+}
+constexpr int DPP_QUAD_XOR1 = 0xB1, DPP_QUAD_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141,
+              DPP_MIRROR = 0x140;
+
+// sum over the 4 lanes of a quad (every lane gets it)
+__device__ __forceinline__ float quad_sum(float v) {
+    v += dpp<DPP_QUAD_XOR1>(v);
+    return v + dpp<DPP_QUAD_XOR2>(v);
+}
+
 template <int L>
 __device__ __forceinline__ float slot_sum(float v) {
-#pragma unroll
-    for (int o = 1; o < L; o <<= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    static_assert(L == 16, "row slots are 16 lanes");
+    v = quad_sum(v);
+    v += dpp<DPP_HALF_MIRROR>(v);
+    return v + dpp<DPP_MIRROR>(v);
 }
 
 // ------------------------------------------------------------- kernel --
@@ -432,9 +451,7 @@ __device__ __forceinline__ void stage_x(const float *__restrict__ X, uint32_t K,
 #pragma unroll
             for (int n = 0; n < NC; n++) {
                 const u32x4 v = slot_pack<F>(A[p][n], B[p][n]);
-                float pt = slot_total(v);
-                pt += __shfl_xor(pt, 1, 64);
-                pt += __shfl_xor(pt, 2, 64);
+                const float pt = quad_sum(slot_total(v));
                 if (in) {
                     *(u32x4 *)(xs + n * cs + xs_index<F, L>(u, 4 * sidx)) = v;
                     if ((q & 3) == 0) xsum[n * xcs + q / 4] = pt;
