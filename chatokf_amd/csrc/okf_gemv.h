@@ -364,7 +364,7 @@ struct Compute<Q2_0, NC, R> {
 #pragma unroll
                 for (int c = 0; c < 8; c++) {
                     // codes c and c + 8 of the dword -> fp16 (1024 + code)
-                    const uint32_t hv = ((v >> (2 * c)) & 0x00030003u) | MAGIC2;
+                    const uint32_t hv = bfi(0x00030003u, v >> (2 * c), MAGIC2);
 #pragma unroll
                     for (int n = 0; n < NC; n++)
                         s[r][n] = dot2(hv, c < 4 ? xa[n][c] : xb[n][c - 4], s[r][n]);
