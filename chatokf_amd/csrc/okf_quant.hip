@@ -130,8 +130,9 @@ template <int F, int NC, int S>
 void launch_gemv_s(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32_t K,
                    uint32_t cunits, size_t lds) {
     // two rows per slot (each staged activation read serves both) where
-    // measured faster: IQ2_XXS with 2..5 columns, Q4_K and Q2_0 with 5
-    constexpr int R = ((F == IQ2_XXS && NC >= 2) || (NC == 5 && F != Q8_0)) ? 2 : 1, D = 2, WAVES = 4;
+    // measured faster: IQ2_XXS with 2..5 columns, Q4_K and Q2_0 with 5; a
+    // three-deep weight ring for the Q4_K matvec (its rows run 5+ steps)
+    constexpr int R = ((F == IQ2_XXS && NC >= 2) || (NC == 5 && F != Q8_0)) ? 2 : 1, D = (F == Q4_K && NC == 1) ? 3 : 2, WAVES = 4;
     const void *fn = (const void *)gemv_kernel<F, NC, R, D, S>;
     static bool attr = false;  // one attribute call per instantiation
     if (!attr) {
