@@ -138,7 +138,6 @@ def main():
         h = torch.empty(M1, device="cuda")
         h2 = torch.empty(M1, device="cuda")
         y = torch.empty(K1, device="cuda")
-        hx = torch.from_numpy(synth.activations(1, M1, 2102)).cuda()  # down-proj input
         nrot = len(gates)
         step_bytes = gate_np.nbytes + up_np.nbytes + down_np.nbytes
 
@@ -147,11 +146,14 @@ def main():
         gw = [ok.QuantTensor(g, K1, M1, ok.Q2_0).c() for g in gates]
         uw = [ok.QuantTensor(u, K1, M1, ok.Q2_0).c() for u in ups]
         dw = [ok.QuantTensor(d, M1, K1, ok.Q2_0).c() for d in downs]
-        xp, hp, h2p, yp, hxp = (t.data_ptr() for t in (x, h, h2, y, hx))
+        xp, hp, h2p, yp = (t.data_ptr() for t in (x, h, h2, y))
 
         # gate and up in one parallel group, as the reference's FFN encodes
         # them (LLM/Qwen/QwenMetalEngine.swift:918-923, MetalEnc.parallel)
         pbegin, pend, hctx = enc._lib.okf_parallel_begin, enc._lib.okf_parallel_end, enc.h
+
+        # then down on silu(gate) * up (siluMul + gemv, :924-928) as one call
+        silu_c = enc.raw_gemv_silu
 
         def ffn_step(i):
             j = i % nrot
@@ -160,7 +162,7 @@ def main():
             gemv_c(uw[j], xp, h2p)
             if pend(hctx):
                 raise RuntimeError("okf_parallel_end failed")
-            gemv_c(dw[j], hxp, yp)
+            silu_c(dw[j], hp, h2p, yp)
 
         for i in range(args.warmup):
             ffn_step(i)
@@ -181,11 +183,11 @@ def main():
             pend(hctx)
 
         gate_t, _ = time_calls(gate_up, args.steps, 5)
-        down_t, _ = time_calls(lambda i: gemv_c(dw[i % nrot], hxp, yp), args.steps, 5)
+        down_t, _ = time_calls(lambda i: silu_c(dw[i % nrot], hp, h2p, yp), args.steps, 5)
         if gate_t >= down_t:
             dom = ("q2_0_matvec_gate_up_2x6144x2048", gate_np.nbytes + up_np.nbytes, gate_t)
         else:
-            dom = ("q2_0_matvec_2048x6144", down_np.nbytes, down_t)
+            dom = ("q2_0_matvec_silu_2048x6144", down_np.nbytes, down_t)
         roofline = {"kernel": f"okf::gemv_kernel<Q2_0> ({dom[0]})", "bound": "hbm",
                     "achieved": round(dom[1] / dom[2] / 1e9, 1), "peak": HBM_PEAK / 1e9,
                     "unit": "GB/s", "frac": round(dom[1] / dom[2] / HBM_PEAK, 4),
@@ -202,6 +204,8 @@ def main():
         ("q8_0_matvec_2048x2048", ok.Q8_0, 2048, 2048, 1, 1001, 2001),
         ("q2_0_matvec_6144x2048", ok.Q2_0, 6144, 2048, 1, 1002, 2002),
         ("q2_0_matvec_2048x6144", ok.Q2_0, 2048, 6144, 1, 1102, 2102),
+        # down on silu(gate) * up (okf_gemv_silu)
+        ("q2_0_matvec_silu_2048x6144", ok.Q2_0, 2048, 6144, 1, 1102, 2102),
         # gate and up as one parallel group (two weight seeds, one x)
         ("q2_0_matvec_gate_up_2x6144x2048", ok.Q2_0, 6144, 2048, 1, (1002, 1202), 2002),
         ("q4_k_matvec_17408x5120", ok.Q4_K, 17408, 5120, 1, 1003, 2003),
@@ -231,7 +235,12 @@ def main():
         wcs_l = [[ok.QuantTensor(c, K, M, t).c() for c in copies] for copies in copies_l]
         xp_, yps = X.data_ptr(), [Y.data_ptr() for Y in Ys]
 
-        if len(seeds) == 1:
+        if "silu" in name:
+            U = torch.from_numpy(synth.activations(N, K, xs + 100)).cuda()
+
+            def call(i, wcs=wcs_l[0], xp_=xp_, up_=U.data_ptr(), yp_=yps[0], nr=nr):
+                enc.raw_gemv_silu(wcs[i % nr], xp_, up_, yp_)
+        elif len(seeds) == 1:
             def call(i, wcs=wcs_l[0], N=N, xp_=xp_, yp_=yps[0], nr=nr):
                 enc.raw_gemm(wcs[i % nr], xp_, N, yp_)
         else:
@@ -264,19 +273,18 @@ def main():
 
         cores = oracle.usable_cores()
         xn = synth.activations(1, K1, 2002)[0]
-        hn = synth.activations(1, M1, 2102)[0]
         times = []
         c0 = time.perf_counter()
         while time.perf_counter() - c0 < args.cpu_seconds or len(times) < 5:
             s = time.perf_counter()
-            oracle.matvec(ok.Q2_0, gate_np, K1, M1, xn, threads=cores)
-            oracle.matvec(ok.Q2_0, up_np, K1, M1, xn, threads=cores)
-            oracle.matvec(ok.Q2_0, down_np, M1, K1, hn, threads=cores)
+            gn = oracle.matvec(ok.Q2_0, gate_np, K1, M1, xn, threads=cores)
+            un = oracle.matvec(ok.Q2_0, up_np, K1, M1, xn, threads=cores)
+            oracle.matvec(ok.Q2_0, down_np, M1, K1, oracle.silu_mul(gn, un), threads=cores)
             times.append(time.perf_counter() - s)
         cpu_step = float(np.median(times))
         cpu = {"value": round(step_bytes / cpu_step / 1e9, 2), "unit": "GB/s", "cores": cores,
                "kind": "port",
-               "sample": f"median of {len(times)} ternary FFN steps (gate+up+down Q2_0 matvec, "
+               "sample": f"median of {len(times)} ternary FFN steps (gate, up, silu*mul, down; "
                          f"same inputs) in {time.perf_counter() - c0:.1f} s: C restatement of "
                          "Q2_0.matvec (LLM/Base/Quant.swift:28-65), row-parallel over cores",
                "us_per_step": round(cpu_step * 1e6, 1)}
@@ -297,7 +305,8 @@ def main():
         "data": "synthetic (reference LCG, BASELINE.json distributions); weights rotated over >= 1 GiB",
         "config": {"workload": "BASELINE configs[1]: Bonsai-1.7B ternary FFN decode step, one token: "
                                "gate+up Q2_0 W 6144x2048 (one parallel group, as the reference "
-                               "encodes them) and down Q2_0 W 2048x6144 matvecs",
+                               "encodes them), then down Q2_0 W 2048x6144 on silu(gate)*up "
+                               "(siluMul fused into the down matvec)",
                    "weight_bytes_per_step": step_bytes, "parallelism": "single GPU"},
         "roofline": roofline,
         "cpu_baseline": cpu,

@@ -25,7 +25,8 @@ OKF_OK, OKF_E_TYPE, OKF_E_SHAPE, OKF_E_HIP, OKF_E_INJECTED, OKF_E_ARG, OKF_E_NOD
 # Every symbol include/okf_quant.h declares.
 EXPORTS = (
     "okf_ctx_create", "okf_ctx_destroy", "okf_ctx_stream", "okf_row_bytes",
-    "okf_gemv", "okf_gemm", "okf_gemm_tile", "okf_dequant_row", "okf_parallel_begin",
+    "okf_gemv", "okf_gemv_silu", "okf_silu_mul", "okf_gemm", "okf_gemm_tile", "okf_dequant_row",
+    "okf_parallel_begin",
     "okf_parallel_end", "okf_sync", "okf_set_fault_rate", "okf_last_hip_error", "okf_strerror",
 )
 
@@ -66,6 +67,8 @@ def _lib():
             "okf_ctx_stream": [vp, ctypes.POINTER(vp)],
             "okf_row_bytes": [i32, u64, ctypes.POINTER(u64)],
             "okf_gemv": [vp, W, vp, vp],
+            "okf_gemv_silu": [vp, W, vp, vp, vp],
+            "okf_silu_mul": [vp, vp, vp, u32],
             "okf_gemm": [vp, W, vp, u32, vp],
             "okf_gemm_tile": [vp, W, vp, u32, vp],
             "okf_dequant_row": [vp, W, u32, vp],
@@ -156,6 +159,16 @@ class Enc:
         wc = w.c()
         self._check(self._lib.okf_gemv(self.h, ctypes.byref(wc), _ptr(x), _ptr(out)), "okf_gemv")
 
+    def gemv_silu(self, w: QuantTensor, gate, up, out):
+        """y = W (silu(gate) * up): MetalEnc.siluMul then gemv, one launch."""
+        wc = w.c()
+        self._check(self._lib.okf_gemv_silu(self.h, ctypes.byref(wc), _ptr(gate), _ptr(up), _ptr(out)),
+                    "okf_gemv_silu")
+
+    def silu_mul(self, a, b, n: int):
+        """a[:n] = silu(a) * b (MetalEnc.siluMul)."""
+        self._check(self._lib.okf_silu_mul(self.h, _ptr(a), _ptr(b), int(n)), "okf_silu_mul")
+
     def gemm(self, w: QuantTensor, X, out, N: int):
         wc = w.c()
         self._check(self._lib.okf_gemm(self.h, ctypes.byref(wc), _ptr(X), int(N), _ptr(out)), "okf_gemm")
@@ -166,6 +179,12 @@ class Enc:
         rc = self._lib.okf_gemv(self.h, ctypes.byref(wc), x, out)
         if rc:
             self._check(rc, "okf_gemv")
+
+    def raw_gemv_silu(self, wc: OkfWeight, gate: int, up: int, out: int):
+        """okf_gemv_silu on a prebuilt descriptor and raw device pointers."""
+        rc = self._lib.okf_gemv_silu(self.h, ctypes.byref(wc), gate, up, out)
+        if rc:
+            self._check(rc, "okf_gemv_silu")
 
     def raw_gemm(self, wc: OkfWeight, X: int, N: int, out: int):
         """okf_gemm on a prebuilt descriptor and raw device pointers."""

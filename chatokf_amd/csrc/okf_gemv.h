@@ -425,13 +425,37 @@ constexpr int GV_SLOTS = 4;
 // Stages activation slots [0, nslots) of chunk c0 (all NC columns) into LDS
 // as packed fp16 and per-32 sums.  SP passes per round: every pass's global
 // loads are issued before the first is packed.
-template <int F, int NC, int L, uint32_t SP>
-__device__ __forceinline__ void stage_x(const float *__restrict__ X, uint32_t K, uint32_t c0,
+// silu(g) * u in fp32 (the reference's silu, LLM/Base/Kernels.swift:3 and
+// LLM/metal/Kernels.metal:7: x / (1 + exp(-x))), with the hardware exp and
+// reciprocal (each about 1 ulp): a handful of instructions per value, which
+// matters because every workgroup stages the whole activation vector.
+// Large negative g gives exp = inf, rcp = 0 and silu = -0, as the formula.
+__device__ __forceinline__ float silu_mul1(float g, float u) {
+    return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
+}
+__device__ __forceinline__ floatx4 silu_mul4(floatx4 g, floatx4 u) {
+    return floatx4{silu_mul1(g[0], u[0]), silu_mul1(g[1], u[1]), silu_mul1(g[2], u[2]),
+                   silu_mul1(g[3], u[3])};
+}
+
+// a[i] = silu(a[i]) * b[i], the FFN glue between gate/up and down
+// (silu_mul, LLM/metal/Kernels.metal:3280-3285)
+__global__ __launch_bounds__(256) void silu_mul_kernel(float *__restrict__ a,
+                                                       const float *__restrict__ b, uint32_t n) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) a[i] = silu_mul1(a[i], b[i]);
+}
+
+// With SILU the activations are silu(X) * X2 (the FFN's gate and up
+// outputs), computed here in fp32 before the fp16 rounding.
+template <int F, int NC, int L, uint32_t SP, bool SILU>
+__device__ __forceinline__ void stage_x(const float *__restrict__ X, const float *__restrict__ X2,
+                                        uint32_t K, uint32_t c0,
                                         uint32_t nslots, uint32_t tid, uint32_t nthr, uint32_t *xs,
                                         uint32_t cs, float *xsum, uint32_t xcs) {
     constexpr uint32_t UW = unit_weights<F>(), SL = UW / 8;
     for (uint32_t q0 = 0; q0 < nslots; q0 += SP * nthr) {
-        floatx4 A[SP][NC], B[SP][NC];
+        floatx4 A[SP][NC], B[SP][NC], A2[SILU ? SP : 1][SILU ? NC : 1], B2[SILU ? SP : 1][SILU ? NC : 1];
 #pragma unroll
         for (uint32_t p = 0; p < SP; p++) {
             const uint32_t q = min(q0 + p * nthr + tid, nslots - 1), u = q / SL;
@@ -439,9 +463,13 @@ __device__ __forceinline__ void stage_x(const float *__restrict__ X, uint32_t K,
             const uint32_t ka = slot_first<F>(q % SL, kb);
 #pragma unroll
             for (int n = 0; n < NC; n++) {
-                const float *xb = X + (uint64_t)n * K + (uint64_t)(c0 + u) * UW;
-                A[p][n] = *(const floatx4 *)(xb + ka);
-                B[p][n] = *(const floatx4 *)(xb + kb);
+                const uint64_t xo = (uint64_t)n * K + (uint64_t)(c0 + u) * UW;
+                A[p][n] = *(const floatx4 *)(X + xo + ka);
+                B[p][n] = *(const floatx4 *)(X + xo + kb);
+                if constexpr (SILU) {
+                    A2[p][n] = *(const floatx4 *)(X2 + xo + ka);
+                    B2[p][n] = *(const floatx4 *)(X2 + xo + kb);
+                }
             }
         }
 #pragma unroll
@@ -450,6 +478,10 @@ __device__ __forceinline__ void stage_x(const float *__restrict__ X, uint32_t K,
             const bool in = q < nslots;
 #pragma unroll
             for (int n = 0; n < NC; n++) {
+                if constexpr (SILU) {
+                    A[p][n] = silu_mul4(A[p][n], A2[p][n]);
+                    B[p][n] = silu_mul4(B[p][n], B2[p][n]);
+                }
                 const u32x4 v = slot_pack<F>(A[p][n], B[p][n]);
                 const float pt = quad_sum(slot_total(v));
                 if (in) {
@@ -461,9 +493,10 @@ __device__ __forceinline__ void stage_x(const float *__restrict__ X, uint32_t K,
     }
 }
 
-template <int F, int NC, int R, int D, int S>
+template <int F, int NC, int R, int D, int S, bool SILU>
 __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ W, uint64_t row_bytes, uint32_t K,
-                                          uint32_t M, const float *__restrict__ X, float *__restrict__ Y,
+                                          uint32_t M, const float *__restrict__ X,
+                                          const float *__restrict__ X2, float *__restrict__ Y,
                                           const u32x4 *__restrict__ tab_g, uint32_t cunits,
                                           uint32_t blk) {
     constexpr int L = GV_L;
@@ -517,11 +550,11 @@ __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ W, uint64_
         constexpr uint32_t SP = NC == 1 ? 4 : NC == 2 ? 2 : 1;
         // (a chunk that one or three passes cover takes that copy: no idle passes)
         if (nslots <= nthr)
-            stage_x<F, NC, L, 1>(X, K, c0, nslots, tid, nthr, xs, cs, xsum, xcs);
+            stage_x<F, NC, L, 1, SILU>(X, X2, K, c0, nslots, tid, nthr, xs, cs, xsum, xcs);
         else if (SP == 4 && nslots <= 3 * nthr)
-            stage_x<F, NC, L, (SP == 4 ? 3 : 1)>(X, K, c0, nslots, tid, nthr, xs, cs, xsum, xcs);
+            stage_x<F, NC, L, (SP == 4 ? 3 : 1), SILU>(X, X2, K, c0, nslots, tid, nthr, xs, cs, xsum, xcs);
         else
-            stage_x<F, NC, L, SP>(X, K, c0, nslots, tid, nthr, xs, cs, xsum, xcs);
+            stage_x<F, NC, L, SP, SILU>(X, X2, K, c0, nslots, tid, nthr, xs, cs, xsum, xcs);
         __syncthreads();
         // stream the wavefront's units u = c0 + i + L (part + S t) through
         // the ring
@@ -583,13 +616,14 @@ constexpr int GV_GROUP = 4;
 struct GemvGroup {
     const uint8_t *W[GV_GROUP];
     const float *X[GV_GROUP];
+    const float *X2[GV_GROUP];  // with SILU: x = silu(X) * X2
     float *Y[GV_GROUP];
     uint32_t M[GV_GROUP];
     uint32_t end[GV_GROUP];
     uint32_t n;
 };
 
-template <int F, int NC, int R, int D, int S>
+template <int F, int NC, int R, int D, int S, bool SILU>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvGroup g, uint64_t row_bytes, uint32_t K,
                                                    const u32x4 *__restrict__ tab_g, uint32_t cunits) {
     uint32_t i = 0;
@@ -597,7 +631,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvGroup g, uint64_t row_byt
     for (int k = 0; k + 1 < GV_GROUP; k++)
         if (k + 1 < (int)g.n && blockIdx.x >= g.end[k]) i = k + 1;
     const uint32_t blk = blockIdx.x - (i ? g.end[i - 1] : 0);
-    gemv_body<F, NC, R, D, S>(g.W[i], row_bytes, K, g.M[i], g.X[i], g.Y[i], tab_g, cunits, blk);
+    gemv_body<F, NC, R, D, S, SILU>(g.W[i], row_bytes, K, g.M[i], g.X[i], g.X2[i], g.Y[i], tab_g, cunits,
+                                    blk);
 }
 
 }  // namespace okf

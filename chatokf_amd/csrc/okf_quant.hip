@@ -23,12 +23,13 @@
 
 #include "iq2xxs_grid.inc"
 
-// one matvec y = W x of a launch group
+// one matvec y = W x of a launch group (with X2: x = silu(X) * X2)
 struct GemvCall {
     const uint8_t *W;
     const float *X;
     float *Y;
     uint32_t M;
+    const float *X2 = nullptr;
 };
 
 struct okf_ctx {
@@ -126,14 +127,14 @@ void build_iq2_tables(uint32_t *t) {
     }
 }
 
-template <int F, int NC, int S>
+template <int F, int NC, int S, bool SILU>
 void launch_gemv_s(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32_t K,
                    uint32_t cunits, size_t lds) {
     // two rows per slot (each staged activation read serves both) where
     // measured faster: IQ2_XXS with 2..5 columns, Q4_K and Q2_0 with 5; a
     // three-deep weight ring for the Q4_K matvec (its rows run 5+ steps)
     constexpr int R = ((F == IQ2_XXS && NC >= 2) || (NC == 5 && F != Q8_0)) ? 2 : 1, D = (F == Q4_K && NC == 1) ? 3 : 2, WAVES = 4;
-    const void *fn = (const void *)gemv_kernel<F, NC, R, D, S>;
+    const void *fn = (const void *)gemv_kernel<F, NC, R, D, S, SILU>;
     static bool attr = false;  // one attribute call per instantiation
     if (!attr) {
         (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)c->max_lds);
@@ -145,13 +146,14 @@ void launch_gemv_s(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32
     for (int i = 0; i < n; i++) {
         g.W[i] = calls[i].W;
         g.X[i] = calls[i].X;
+        g.X2[i] = calls[i].X2;
         g.Y[i] = calls[i].Y;
         g.M[i] = calls[i].M;
         total += (calls[i].M + rows_per_wg - 1) / rows_per_wg;
         g.end[i] = total;
     }
     g.n = (uint32_t)n;
-    hipLaunchKernelGGL((gemv_kernel<F, NC, R, D, S>), dim3(total), dim3(64 * WAVES), lds, c->stream,
+    hipLaunchKernelGGL((gemv_kernel<F, NC, R, D, S, SILU>), dim3(total), dim3(64 * WAVES), lds, c->stream,
                        g, rb, K, c->tab, cunits);
 }
 
@@ -160,7 +162,7 @@ void launch_gemv_s(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32
 // of rows, K is split two ways across the wavefronts of a workgroup (more,
 // shorter wavefronts); measured on MI355X, a four-way split loses to the
 // extra activation staging it needs.
-template <int F, int NC>
+template <int F, int NC, bool SILU = false>
 void launch_gemv_nc(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32_t K) {
     constexpr uint32_t UW = unit_weights<F>();
     const size_t tab = F == IQ2_XXS ? 384 * 16 : 0;
@@ -176,13 +178,17 @@ void launch_gemv_nc(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint3
     for (int i = 0; i < n; i++) rows += calls[i].M;
     const uint32_t waves1 = (rows + GV_SLOTS - 1) / GV_SLOTS;  // wavefronts without a split
     uint32_t S = c->gemv_s ? (uint32_t)c->gemv_s : (NC == 1 && waves1 < 3072 ? 2 : 1);
-    if (S >= 4) launch_gemv_s<F, NC, 4>(c, calls, n, rb, K, cunits, lds);
-    else if (S == 2) launch_gemv_s<F, NC, 2>(c, calls, n, rb, K, cunits, lds);
-    else launch_gemv_s<F, NC, 1>(c, calls, n, rb, K, cunits, lds);
+    if (S >= 4) launch_gemv_s<F, NC, 4, SILU>(c, calls, n, rb, K, cunits, lds);
+    else if (S == 2) launch_gemv_s<F, NC, 2, SILU>(c, calls, n, rb, K, cunits, lds);
+    else launch_gemv_s<F, NC, 1, SILU>(c, calls, n, rb, K, cunits, lds);
 }
 
 template <int F>
 void launch_gemv(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32_t K, uint32_t N) {
+    if (calls[0].X2) {  // SiLU-gated activations: one column
+        launch_gemv_nc<F, 1, true>(c, calls, n, rb, K);
+        return;
+    }
     switch (N) {
     case 1: launch_gemv_nc<F, 1>(c, calls, n, rb, K); break;
     case 2: launch_gemv_nc<F, 2>(c, calls, n, rb, K); break;
@@ -274,17 +280,18 @@ void launch_dequant(okf_ctx *c, const uint8_t *row, uint32_t n, float *out) {
 
 enum class Path { Auto, Tile };
 
-int run_gemm(okf_ctx *c, const okf_weight *w, const float *X, uint32_t N, float *Y, Path path) {
+int run_gemm(okf_ctx *c, const okf_weight *w, const float *X, uint32_t N, float *Y, Path path,
+             const float *X2 = nullptr) {
     uint64_t rb = 0;
     int st = check_weight(w, &rb);
     if (st) return st;
     if (!X || !Y) return OKF_E_ARG;
     if (N == 0) return OKF_E_SHAPE;
-    if (!aligned16(X)) return OKF_E_SHAPE;
+    if (!aligned16(X) || (X2 && !aligned16(X2))) return OKF_E_SHAPE;
     if ((st = begin(c))) return st;
     const uint8_t *W = (const uint8_t *)w->base + w->off;
     if (path == Path::Auto && N <= 5) {
-        const GemvCall call{W, X, Y, w->M};
+        const GemvCall call{W, X, Y, w->M, X2};
         if (c->grouping && N == 1) {
             // inside a parallel group: launched together at okf_parallel_end
             c->pending.push_back({w->ggml_type, w->K, rb, call});
@@ -314,7 +321,8 @@ int flush_group(okf_ctx *c) {
         GemvCall calls[GV_GROUP];
         int n = 0;
         for (size_t j = i; j < p.size() && n < GV_GROUP; j++)
-            if (!done[j] && p[j].type == p[i].type && p[j].K == p[i].K) {
+            if (!done[j] && p[j].type == p[i].type && p[j].K == p[i].K &&
+                (p[j].call.X2 != nullptr) == (p[i].call.X2 != nullptr)) {
                 calls[n++] = p[j].call;
                 done[j] = true;
             }
@@ -418,6 +426,20 @@ int okf_dequant_row(okf_ctx *c, const okf_weight *row, uint32_t n, float *out) {
     if (st) return st;
     const uint8_t *p = (const uint8_t *)row->base + row->off;
     OKF_DISPATCH(row->ggml_type, launch_dequant, c, p, n, out);
+    return finish(c);
+}
+
+int okf_gemv_silu(okf_ctx *c, const okf_weight *w, const float *gate, const float *up, float *y) {
+    if (!gate || !up) return OKF_E_ARG;
+    return run_gemm(c, w, gate, 1, y, Path::Auto, up);
+}
+
+int okf_silu_mul(okf_ctx *c, float *a, const float *b, uint32_t n) {
+    if (!a || !b) return OKF_E_ARG;
+    if (n == 0) return OKF_E_SHAPE;
+    int st = begin(c);
+    if (st) return st;
+    hipLaunchKernelGGL(silu_mul_kernel, dim3((n + 255) / 256), dim3(256), 0, c->stream, a, b, n);
     return finish(c);
 }
 

@@ -79,6 +79,16 @@ int okf_row_bytes(int32_t ggml_type, uint64_t n, uint64_t *out);
  * Q4_K needs base + off 16-byte aligned; x must be 16-byte aligned. */
 int okf_gemv(okf_ctx *ctx, const okf_weight *w, const float *x, float *y);
 
+/* MetalEnc.siluMul (MetalEnc.swift:921, kernel silu_mul,
+ * LLM/metal/Kernels.metal:3280-3285) then MetalEnc.gemv on its output, the
+ * FFN down projection (LLM/Qwen/QwenMetalEngine.swift:924-928), as one
+ * launch: y[M] = W (silu(gate) * up), silu(x) = x / (1 + exp(-x)) in fp32.
+ * Unlike the reference's in-place siluMul, gate is left unchanged. */
+int okf_gemv_silu(okf_ctx *ctx, const okf_weight *w, const float *gate, const float *up, float *y);
+
+/* MetalEnc.siluMul (MetalEnc.swift:921): a[i] = silu(a[i]) * b[i], n values. */
+int okf_silu_mul(okf_ctx *ctx, float *a, const float *b, uint32_t n);
+
 /* MetalEnc.gemm (MetalEnc.swift:241-289): Y[N][M] = X[N][K] W^T.  Dispatch
  * policy as the reference: N == 1 -> gemv; 2 <= N <= 5 -> narrow (one weight
  * pass serving all N columns, gemmNarrow / gemmNarrowIQ :176-239);

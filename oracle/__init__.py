@@ -39,6 +39,8 @@ def _lib():
         lib.okf_ref_matvec.argtypes = [i32, vp, u32, u32, vp, vp, ctypes.c_int]
         lib.okf_ref_matmul.argtypes = [i32, vp, u32, u32, vp, u32, vp, ctypes.c_int]
         lib.okf_ref_usable_cores.argtypes = []
+        lib.okf_ref_silu_mul.argtypes = [vp, vp, u32, vp]
+        lib.okf_ref_silu_mul.restype = None
         _LIB = lib
     return _LIB
 
@@ -65,6 +67,16 @@ def dequant(t: int, row: np.ndarray, n: int) -> np.ndarray:
     out = np.empty(n, np.float32)
     if _lib().okf_ref_dequant(t, _p(row), n, _p(out)):
         raise ValueError("dequant failed")
+    return out
+
+
+def silu_mul(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """silu(a) * b, fp32 (the reference's FFN glue)."""
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    assert a.size == b.size
+    out = np.empty(a.size, np.float32)
+    _lib().okf_ref_silu_mul(_p(a), _p(b), a.size, _p(out))
     return out
 
 

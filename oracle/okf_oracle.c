@@ -11,6 +11,7 @@
 #include <pthread.h>
 #include <sched.h>
 #include <stdlib.h>
+#include <math.h>
 #include <string.h>
 
 #include "iq2xxs_grid.inc"
@@ -360,4 +361,13 @@ int okf_ref_matmul(int32_t type, const uint8_t *w, uint32_t K, uint32_t M,
         run_rows(&j, threads, 0);
     }
     return 0;
+}
+
+/* Swift silu, LLM/Base/Kernels.swift:3: x / (1 + expf(-x)); then times b. */
+void okf_ref_silu_mul(const float *a, const float *b, uint32_t n, float *out) {
+    for (uint32_t i = 0; i < n; i++) {
+        const float x = a[i];
+        const float s = x / (1.0f + expf(-x));
+        out[i] = s * b[i];
+    }
 }

@@ -62,6 +62,11 @@ int okf_ref_matmul(int32_t type, const uint8_t *w, uint32_t K, uint32_t M,
 /* Cores this process may run on (sched_getaffinity). */
 int okf_ref_usable_cores(void);
 
+/* silu(a) * b elementwise into out: silu(x) = x / (1 + expf(-x)) as Swift's
+ * silu (LLM/Base/Kernels.swift:3) and the Metal silu_mul kernel
+ * (LLM/metal/Kernels.metal:7, :3280-3285). */
+void okf_ref_silu_mul(const float *a, const float *b, uint32_t n, float *out);
+
 #ifdef __cplusplus
 }
 #endif

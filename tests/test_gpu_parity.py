@@ -172,6 +172,41 @@ def test_iq2_xxs_mtp_verify_full_config(enc):
     assert r <= TOL
 
 
+# ------------------------------------------------------------ SiLU-gated FFN
+def test_silu_mul_matches_oracle(enc):
+    a = np.random.default_rng(4).standard_normal(6144).astype(np.float32) * 3
+    b = np.random.default_rng(5).standard_normal(6144).astype(np.float32)
+    ad, bd = dev(a), dev(b)
+    enc.silu_mul(ad, bd, 6144)
+    got, ref = host(ad), oracle.silu_mul(a, b).astype(np.float64)
+    # device exp: a few ulp from the C library's expf
+    assert np.allclose(got, ref, rtol=1e-5, atol=1e-6)
+
+
+SILU_CASES = [(Q2_0, 2048, 6144, 1102), (Q8_0, 300, 2048, 81), (Q4_K, 260, 2304, 82),
+              (IQ2_XXS, 129, 1536, 83), (Q2_0, 130, 1024, 84)]
+
+
+@pytest.mark.parametrize("t,M,K,seed", SILU_CASES)
+def test_gemv_silu_matches_silu_mul_then_matvec(enc, t, M, K, seed):
+    # QwenMetalEngine.swift:924-928: siluMul(gate, up) then gemv(down)
+    w = weights(t, M, K, seed)
+    g, u = acts(1, K, seed + 1)[0] * 2, acts(1, K, seed + 2)[0]
+    ref = oracle.matvec(t, w, K, M, oracle.silu_mul(g, u)).astype(np.float64)
+    gd, ud = dev(g), dev(u)
+    y = torch.full((M,), float("nan"), device="cuda")
+    enc.gemv_silu(ok.QuantTensor(dev(w), K, M, t), gd, ud, y)
+    got = host(y)
+    say("gemv_silu", NAMES[t], M, K, rel(got, ref))
+    assert rel(got, ref) <= TOL
+    assert np.array_equal(host(gd), g)  # gate is not modified
+    # the two-call form: silu_mul in place, then gemv
+    enc.silu_mul(gd, ud, K)
+    y2 = torch.full((M,), float("nan"), device="cuda")
+    enc.gemv(ok.QuantTensor(dev(w), K, M, t), gd, y2)
+    assert rel(got, host(y2).astype(np.float64)) <= 1e-5
+
+
 # ------------------------------------------------------------ parallel group
 def test_parallel_group_matches_single_calls(enc):
     # MetalEnc.parallel { gate; up } (QwenMetalEngine.swift:918-923) plus more

@@ -265,3 +265,20 @@ def test_matvec_linear_in_x():
     assert np.array_equal(2 * a, b)
     c = oracle.matvec(IQ2_XXS, w, 512, 16, -x)
     assert np.array_equal(-a, c)
+
+
+def test_silu_mul_known_values_and_float64():
+    # Swift silu (LLM/Base/Kernels.swift:3): x / (1 + expf(-x)), times b
+    a = np.array([0.0, 1.0, -1.0, 20.0, -20.0, 88.0, -88.0, 0.5], np.float32)
+    b = np.array([3.0, 1.0, 1.0, 1.0, 1.0, 2.0, 2.0, -4.0], np.float32)
+    got = oracle.silu_mul(a, b)
+    a64, b64 = a.astype(np.float64), b.astype(np.float64)
+    ref = a64 / (1.0 + np.exp(-a64)) * b64
+    assert got[0] == 0.0
+    assert np.allclose(got, ref, rtol=2e-7, atol=1e-30)
+    assert abs(got[3] - 20.0) < 1e-5 and abs(got[4]) < 1e-7
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal(4096).astype(np.float32) * 4
+    y = rng.standard_normal(4096).astype(np.float32)
+    x64 = x.astype(np.float64)
+    assert np.allclose(oracle.silu_mul(x, y), x64 / (1 + np.exp(-x64)) * y, rtol=1e-6, atol=1e-7)
