@@ -26,6 +26,7 @@ OKF_OK, OKF_E_TYPE, OKF_E_SHAPE, OKF_E_HIP, OKF_E_INJECTED, OKF_E_ARG, OKF_E_NOD
 EXPORTS = (
     "okf_ctx_create", "okf_ctx_destroy", "okf_ctx_stream", "okf_row_bytes",
     "okf_gemv", "okf_gemv_silu", "okf_silu_mul", "okf_gemm", "okf_gemm_tile", "okf_dequant_row",
+    "okf_embed_batch",
     "okf_parallel_begin",
     "okf_parallel_end", "okf_sync", "okf_set_fault_rate", "okf_last_hip_error", "okf_strerror",
 )
@@ -72,6 +73,7 @@ def _lib():
             "okf_gemm": [vp, W, vp, u32, vp],
             "okf_gemm_tile": [vp, W, vp, u32, vp],
             "okf_dequant_row": [vp, W, u32, vp],
+            "okf_embed_batch": [vp, W, vp, u32, vp],
             "okf_parallel_begin": [vp],
             "okf_parallel_end": [vp],
             "okf_sync": [vp],
@@ -211,6 +213,12 @@ class Enc:
             yield self
         finally:
             self._check(self._lib.okf_parallel_end(self.h), "okf_parallel_end")
+
+    def embed_batch(self, w: QuantTensor, ids, N: int, out):
+        """out[n] = dequantized row ids[n] of w (MetalEnc.embedBatch)."""
+        wc = w.c()
+        self._check(self._lib.okf_embed_batch(self.h, ctypes.byref(wc), _ptr(ids), int(N), _ptr(out)),
+                    "okf_embed_batch")
 
     def sync(self):
         self._check(self._lib.okf_sync(self.h), "okf_sync")

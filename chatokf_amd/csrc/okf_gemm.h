@@ -140,6 +140,34 @@ __global__ __launch_bounds__(256) void dequant_row_kernel(const uint8_t *__restr
     for (int i = 0; i < 8; i++) o[i] = make_float4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
 }
 
+// Embedding gather (embedBatch, LLM/Base/MetalEnc.swift:1096-1146): row
+// ids[n] of W dequantized into out[n][K], one thread per 32-weight unit;
+// bit-exact with dequant_row.  An id outside [0, M) is clamped to the
+// nearest row, so a bad id cannot read outside the weights.
+template <int F>
+__global__ __launch_bounds__(256) void embed_batch_kernel(const uint8_t *__restrict__ W,
+                                                          uint64_t row_bytes, uint32_t M,
+                                                          const int32_t *__restrict__ ids,
+                                                          uint32_t units_per_row, uint32_t units,
+                                                          float *__restrict__ out,
+                                                          const uint2 *__restrict__ grid_g) {
+    __shared__ uint2 grid[F == IQ2_XXS ? 256 : 1];
+    if constexpr (F == IQ2_XXS) {
+        grid[threadIdx.x] = grid_g[threadIdx.x];
+        __syncthreads();
+    }
+    const uint32_t g = blockIdx.x * 256 + threadIdx.x;
+    if (g >= units) return;
+    const uint32_t n = g / units_per_row, u = g % units_per_row;
+    const int32_t id = ids[n];
+    const uint32_t row = id < 0 ? 0u : min((uint32_t)id, M - 1);
+    float w[32];
+    decode_unit<F>(W + (uint64_t)row * row_bytes, u, w, grid);
+    float4 *o = (float4 *)(out + ((uint64_t)n * units_per_row + u) * 32);
+#pragma unroll
+    for (int i = 0; i < 8; i++) o[i] = make_float4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
+}
+
 }  // namespace okf
 
 namespace okf {

@@ -270,6 +270,14 @@ void launch_dequant(okf_ctx *c, const uint8_t *row, uint32_t n, float *out) {
                        row, units, out, c->grid);
 }
 
+template <int F>
+void launch_embed(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t M,
+                  const int32_t *ids, uint32_t N, float *out) {
+    const uint32_t upr = K / 32, units = N * upr;
+    hipLaunchKernelGGL((embed_batch_kernel<F>), dim3((units + 255) / 256), dim3(256), 0, c->stream, W,
+                       rb, M, ids, upr, units, out, c->grid);
+}
+
 #define OKF_DISPATCH(type, fn, ...)                         \
     switch (type) {                                         \
     case Q8_0: fn<Q8_0>(__VA_ARGS__); break;                \
@@ -458,6 +466,19 @@ int okf_parallel_end(okf_ctx *c) {
     if (c->device < 0) return OKF_E_NODEV;
     (void)hipSetDevice(c->device);
     return flush_group(c);
+}
+
+int okf_embed_batch(okf_ctx *c, const okf_weight *w, const int32_t *ids, uint32_t N, float *out) {
+    uint64_t rb = 0;
+    int st = check_weight(w, &rb);
+    if (st) return st;
+    if (!ids || !out) return OKF_E_ARG;
+    if (N == 0 || (uint64_t)N * (w->K / 32) > 0xFFFFFFFFull) return OKF_E_SHAPE;
+    if (!aligned16(out)) return OKF_E_SHAPE;
+    if ((st = begin(c))) return st;
+    const uint8_t *W = (const uint8_t *)w->base + w->off;
+    OKF_DISPATCH(w->ggml_type, launch_embed, c, W, rb, w->K, w->M, ids, N, out);
+    return finish(c);
 }
 
 int okf_sync(okf_ctx *c) {

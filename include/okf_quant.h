@@ -114,6 +114,13 @@ int okf_dequant_row(okf_ctx *ctx, const okf_weight *row, uint32_t n, float *out)
 int okf_parallel_begin(okf_ctx *ctx);
 int okf_parallel_end(okf_ctx *ctx);
 
+/* MetalEnc.embedBatch (MetalEnc.swift:1096-1146; kernels embed_batch,
+ * q4_k_embed_batch, iq_embed_batch, LLM/metal/Kernels.metal:1444-1482):
+ * out[n][K] = row ids[n] of w dequantized to fp32, n < N, bit-identical to
+ * okf_dequant_row of that row.  ids is device memory; an id outside
+ * [0, M) is clamped to the nearest row. */
+int okf_embed_batch(okf_ctx *ctx, const okf_weight *w, const int32_t *ids, uint32_t N, float *out);
+
 /* Waits for all work on the context's stream: the analogue of
  * commit + waitUntilCompleted (LLM/Base/MetalGates.swift:144-149).  Returns
  * OKF_E_HIP if a kernel failed. */

@@ -301,3 +301,32 @@ def test_injected_fault_launches_nothing(enc):
     enc.gemv(ok.QuantTensor(w, K, M, t), x, y)
     enc.sync()
     assert not (host(y) == 7.0).all()
+
+
+# ------------------------------------------------------------------ embedding gather
+@pytest.mark.parametrize("t", [Q8_0, Q2_0, Q4_K, IQ2_XXS], ids=lambda t: NAMES[t])
+def test_embed_batch_bit_exact(enc, t):
+    # embedBatch (MetalEnc.swift:1096-1146) vs the oracle's dequant of each row
+    M, K = 300, 2048
+    w = weights(t, M, K, 91)
+    ids = np.array([0, 299, 17, 17, 150, 1, 298, 64], np.int32)
+    out = torch.full((len(ids), K), float("nan"), device="cuda")
+    enc.embed_batch(ok.QuantTensor(dev(w), K, M, t), dev(ids), len(ids), out)
+    got = host(out)
+    rb = row_bytes(t, K)
+    for n, i in enumerate(ids):
+        ref = oracle.dequant(t, w[i * rb:(i + 1) * rb], K)
+        assert np.array_equal(got[n].view(np.uint32), ref.view(np.uint32)), (NAMES[t], n, i)
+
+
+def test_embed_batch_clamps_ids(enc):
+    M, K = 8, 256
+    w = weights(Q4_K, M, K, 92)
+    ids = np.array([-5, 8, 1000], np.int32)
+    out = torch.empty((3, K), device="cuda")
+    enc.embed_batch(ok.QuantTensor(dev(w), K, M, Q4_K), dev(ids), 3, out)
+    got = host(out)
+    rb = row_bytes(Q4_K, K)
+    assert np.array_equal(got[0], oracle.dequant(Q4_K, w[:rb], K))
+    assert np.array_equal(got[1], oracle.dequant(Q4_K, w[7 * rb:8 * rb], K))
+    assert np.array_equal(got[2], got[1])
