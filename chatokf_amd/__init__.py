@@ -20,7 +20,8 @@ from .formats import Q8_0, Q4_K, IQ2_XXS, Q2_0, NAMES, BY_NAME, block_elems, row
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("OKF_LIB") or os.path.join(HERE, "libokf_quant.so")
 
-OKF_OK, OKF_E_TYPE, OKF_E_SHAPE, OKF_E_HIP, OKF_E_INJECTED, OKF_E_ARG, OKF_E_NODEV = range(7)
+(OKF_OK, OKF_E_TYPE, OKF_E_SHAPE, OKF_E_HIP, OKF_E_INJECTED, OKF_E_ARG, OKF_E_NODEV, OKF_E_IO,
+ OKF_E_FORMAT, OKF_E_NOTFOUND) = range(10)
 
 # Every symbol include/okf_quant.h declares.
 EXPORTS = (
@@ -29,7 +30,22 @@ EXPORTS = (
     "okf_embed_batch",
     "okf_parallel_begin",
     "okf_parallel_end", "okf_sync", "okf_set_fault_rate", "okf_last_hip_error", "okf_strerror",
+    "okf_gguf_open", "okf_gguf_close", "okf_gguf_tensor_count", "okf_gguf_tensor_at", "okf_gguf_find",
+    "okf_gguf_kv_int", "okf_gguf_kv_double", "okf_gguf_kv_string", "okf_gguf_data", "okf_gguf_upload",
+    "okf_gguf_free_device",
 )
+
+
+class OkfGGUFTensor(ctypes.Structure):
+    """``okf_gguf_tensor`` of include/okf_quant.h."""
+    _fields_ = [
+        ("name", ctypes.c_char_p),
+        ("n_dims", ctypes.c_uint32),
+        ("dims", ctypes.c_uint64 * 4),
+        ("ggml_type", ctypes.c_int32),
+        ("offset", ctypes.c_uint64),
+        ("bytes", ctypes.c_uint64),
+    ]
 
 
 class OkfWeight(ctypes.Structure):
@@ -79,6 +95,17 @@ def _lib():
             "okf_sync": [vp],
             "okf_set_fault_rate": [vp, ctypes.c_double, u64],
             "okf_last_hip_error": [vp],
+            "okf_gguf_open": [ctypes.c_char_p, ctypes.POINTER(vp)],
+            "okf_gguf_close": [vp],
+            "okf_gguf_tensor_count": [vp, ctypes.POINTER(u64)],
+            "okf_gguf_tensor_at": [vp, u64, ctypes.POINTER(OkfGGUFTensor)],
+            "okf_gguf_find": [vp, ctypes.c_char_p, ctypes.POINTER(OkfGGUFTensor)],
+            "okf_gguf_kv_int": [vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64)],
+            "okf_gguf_kv_double": [vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double)],
+            "okf_gguf_kv_string": [vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(u64)],
+            "okf_gguf_data": [vp, ctypes.POINTER(vp), ctypes.POINTER(u64)],
+            "okf_gguf_upload": [vp, vp, ctypes.POINTER(vp)],
+            "okf_gguf_free_device": [vp, vp],
         }
         for name, args in sig.items():
             f = getattr(lib, name)
@@ -227,7 +254,99 @@ class Enc:
         self._check(self._lib.okf_set_fault_rate(self.h, float(rate), int(seed)), "okf_set_fault_rate")
 
 
+class GGUF:
+    """A GGUF file mapped and parsed by the library (okf_gguf_open), the
+    counterpart of GGUF(path:) (``LLM/Base/GGUF.swift:99-151``)."""
+
+    def __init__(self, path: str):
+        self._lib = _lib()
+        h = ctypes.c_void_p()
+        rc = self._lib.okf_gguf_open(os.fsencode(path), ctypes.byref(h))
+        if rc:
+            raise OkfError(rc, "okf_gguf_open")
+        self.h = h
+
+    def close(self):
+        if self.h:
+            self._lib.okf_gguf_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @staticmethod
+    def _info(t: "OkfGGUFTensor") -> dict:
+        return {"name": t.name.decode(), "dims": [int(t.dims[d]) for d in range(t.n_dims)],
+                "type": int(t.ggml_type), "offset": int(t.offset), "bytes": int(t.bytes)}
+
+    def tensors(self) -> list:
+        n = ctypes.c_uint64()
+        self._lib.okf_gguf_tensor_count(self.h, ctypes.byref(n))
+        out = []
+        for i in range(n.value):
+            t = OkfGGUFTensor()
+            self._lib.okf_gguf_tensor_at(self.h, i, ctypes.byref(t))
+            out.append(self._info(t))
+        return out
+
+    def find(self, name: str):
+        t = OkfGGUFTensor()
+        rc = self._lib.okf_gguf_find(self.h, name.encode(), ctypes.byref(t))
+        if rc == OKF_E_NOTFOUND:
+            return None
+        if rc:
+            raise OkfError(rc, "okf_gguf_find")
+        return self._info(t)
+
+    def int(self, key: str):
+        v = ctypes.c_int64()
+        return v.value if self._lib.okf_gguf_kv_int(self.h, key.encode(), ctypes.byref(v)) == 0 else None
+
+    def double(self, key: str):
+        v = ctypes.c_double()
+        return v.value if self._lib.okf_gguf_kv_double(self.h, key.encode(), ctypes.byref(v)) == 0 else None
+
+    def string(self, key: str):
+        p, n = ctypes.c_char_p(), ctypes.c_uint64()
+        if self._lib.okf_gguf_kv_string(self.h, key.encode(), ctypes.byref(p), ctypes.byref(n)):
+            return None
+        return ctypes.string_at(p, n.value).decode()
+
+    def data(self) -> bytes:
+        p, n = ctypes.c_void_p(), ctypes.c_uint64()
+        self._lib.okf_gguf_data(self.h, ctypes.byref(p), ctypes.byref(n))
+        return ctypes.string_at(p, n.value)
+
+    def upload(self, enc: "Enc") -> int:
+        """Device copy of the data region; returns its device address."""
+        d = ctypes.c_void_p()
+        rc = self._lib.okf_gguf_upload(enc.h, self.h, ctypes.byref(d))
+        if rc:
+            raise OkfError(rc, "okf_gguf_upload")
+        return d.value
+
+    def weight(self, name: str, device_base: int) -> "QuantTensor":
+        """The okf_weight of a 2-D (or higher) tensor in an uploaded copy."""
+        t = self.find(name)
+        if t is None:
+            raise KeyError(name)
+        K = t["dims"][0]
+        M = 1
+        for d in t["dims"][1:]:
+            M *= d
+        return QuantTensor(device_base, K, M, t["type"], off=t["offset"])
+
+
 __all__ = [
     "Q8_0", "Q4_K", "IQ2_XXS", "Q2_0", "NAMES", "BY_NAME", "block_elems", "row_bytes",
-    "QuantTensor", "Enc", "OkfError", "OkfWeight", "lib", "EXPORTS", "LIB_PATH",
+    "QuantTensor", "Enc", "OkfError", "OkfWeight", "OkfGGUFTensor", "GGUF", "lib", "EXPORTS", "LIB_PATH",
 ]

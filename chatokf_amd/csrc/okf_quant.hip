@@ -20,6 +20,7 @@
 #include <algorithm>
 #include <vector>
 #include "okf_gemv.h"
+#include "okf_gguf.h"
 
 #include "iq2xxs_grid.inc"
 
@@ -30,6 +31,10 @@ struct GemvCall {
     float *Y;
     uint32_t M;
     const float *X2 = nullptr;
+};
+
+struct okf_gguf {
+    okf_gguf_impl::File f;
 };
 
 struct okf_ctx {
@@ -503,6 +508,128 @@ int okf_set_fault_rate(okf_ctx *c, double rate, uint64_t seed) {
 
 int okf_last_hip_error(okf_ctx *c) { return c ? c->last_hip : 0; }
 
+int okf_gguf_open(const char *path, okf_gguf **out) {
+    if (!path || !out) return OKF_E_ARG;
+    *out = nullptr;
+    okf_gguf *g = new (std::nothrow) okf_gguf();
+    if (!g) return OKF_E_ARG;
+    okf_gguf_impl::File &f = g->f;
+    f.fd = open(path, O_RDONLY);
+    struct stat st;
+    if (f.fd < 0 || fstat(f.fd, &st) != 0 || st.st_size <= 0) {
+        delete g;
+        return OKF_E_IO;
+    }
+    f.size = (uint64_t)st.st_size;
+    void *m = mmap(nullptr, f.size, PROT_READ, MAP_PRIVATE, f.fd, 0);
+    if (m == MAP_FAILED) {
+        delete g;
+        return OKF_E_IO;
+    }
+    f.map = (const uint8_t *)m;
+    const int st2 = okf_gguf_impl::parse(f);
+    if (st2) {
+        delete g;
+        return st2;
+    }
+    *out = g;
+    return OKF_OK;
+}
+
+int okf_gguf_close(okf_gguf *g) {
+    if (!g) return OKF_E_ARG;
+    delete g;
+    return OKF_OK;
+}
+
+int okf_gguf_tensor_count(const okf_gguf *g, uint64_t *n) {
+    if (!g || !n) return OKF_E_ARG;
+    *n = g->f.tensors.size();
+    return OKF_OK;
+}
+
+int okf_gguf_tensor_at(const okf_gguf *g, uint64_t i, okf_gguf_tensor *t) {
+    if (!g || !t) return OKF_E_ARG;
+    if (i >= g->f.tensors.size()) return OKF_E_NOTFOUND;
+    const okf_gguf_impl::Tensor &x = g->f.tensors[i];
+    t->name = x.name.c_str();
+    t->n_dims = x.n_dims;
+    for (int d = 0; d < 4; d++) t->dims[d] = x.dims[d];
+    t->ggml_type = x.type;
+    t->offset = x.offset;
+    t->bytes = x.bytes;
+    return OKF_OK;
+}
+
+int okf_gguf_find(const okf_gguf *g, const char *name, okf_gguf_tensor *t) {
+    if (!g || !name || !t) return OKF_E_ARG;
+    auto it = g->f.by_name.find(name);
+    if (it == g->f.by_name.end()) return OKF_E_NOTFOUND;
+    return okf_gguf_tensor_at(g, it->second, t);
+}
+
+int okf_gguf_kv_int(const okf_gguf *g, const char *key, int64_t *v) {
+    if (!g || !key || !v) return OKF_E_ARG;
+    auto it = g->f.meta.find(key);
+    if (it == g->f.meta.end()) return OKF_E_NOTFOUND;
+    const auto &x = it->second;
+    if (x.kind != okf_gguf_impl::Value::Int && x.kind != okf_gguf_impl::Value::Bool) return OKF_E_NOTFOUND;
+    *v = x.i;
+    return OKF_OK;
+}
+
+int okf_gguf_kv_double(const okf_gguf *g, const char *key, double *v) {
+    if (!g || !key || !v) return OKF_E_ARG;
+    auto it = g->f.meta.find(key);
+    if (it == g->f.meta.end()) return OKF_E_NOTFOUND;
+    const auto &x = it->second;
+    if (x.kind == okf_gguf_impl::Value::Double) *v = x.d;
+    else if (x.kind == okf_gguf_impl::Value::Int) *v = (double)x.i;
+    else return OKF_E_NOTFOUND;
+    return OKF_OK;
+}
+
+int okf_gguf_kv_string(const okf_gguf *g, const char *key, const char **s, uint64_t *len) {
+    if (!g || !key || !s || !len) return OKF_E_ARG;
+    auto it = g->f.meta.find(key);
+    if (it == g->f.meta.end() || it->second.kind != okf_gguf_impl::Value::String) return OKF_E_NOTFOUND;
+    *s = it->second.s.c_str();
+    *len = it->second.s.size();
+    return OKF_OK;
+}
+
+int okf_gguf_data(const okf_gguf *g, const void **host, uint64_t *bytes) {
+    if (!g || !host || !bytes) return OKF_E_ARG;
+    *host = g->f.map + g->f.data_start;
+    *bytes = g->f.size - g->f.data_start;
+    return OKF_OK;
+}
+
+int okf_gguf_upload(okf_ctx *c, const okf_gguf *g, void **device) {
+    if (!g || !device) return OKF_E_ARG;
+    *device = nullptr;
+    int st = begin(c);
+    if (st) return st;
+    const uint64_t n = g->f.size - g->f.data_start;
+    void *d = nullptr;
+    hipError_t e = hipMalloc(&d, n ? n : 1);
+    if (e == hipSuccess && n) e = hipMemcpy(d, g->f.map + g->f.data_start, n, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        if (d) (void)hipFree(d);
+        return hip_fail(c, e);
+    }
+    *device = d;
+    return OKF_OK;
+}
+
+int okf_gguf_free_device(okf_ctx *c, void *device) {
+    if (!c || !device) return OKF_E_ARG;
+    if (c->device < 0) return OKF_E_NODEV;
+    (void)hipSetDevice(c->device);
+    hipError_t e = hipFree(device);
+    return e == hipSuccess ? OKF_OK : hip_fail(c, e);
+}
+
 const char *okf_strerror(int s) {
     switch (s) {
     case OKF_OK: return "ok";
@@ -512,6 +639,9 @@ const char *okf_strerror(int s) {
     case OKF_E_INJECTED: return "injected fault";
     case OKF_E_ARG: return "bad argument";
     case OKF_E_NODEV: return "detached context has no device";
+    case OKF_E_IO: return "cannot open or map the file";
+    case OKF_E_FORMAT: return "malformed GGUF file";
+    case OKF_E_NOTFOUND: return "no such tensor or key";
     default: return "unknown status";
     }
 }

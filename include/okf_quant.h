@@ -37,7 +37,10 @@ typedef enum {
     OKF_E_HIP = 3,      /* a HIP runtime call failed (see okf_last_hip_error) */
     OKF_E_INJECTED = 4, /* fault injected by okf_set_fault_rate */
     OKF_E_ARG = 5,      /* null pointer or bad argument */
-    OKF_E_NODEV = 6     /* detached context (device -1): nothing can run */
+    OKF_E_NODEV = 6,    /* detached context (device -1): nothing can run */
+    OKF_E_IO = 7,       /* a file could not be opened or mapped */
+    OKF_E_FORMAT = 8,   /* a malformed GGUF file (GGUFErr.parse) */
+    OKF_E_NOTFOUND = 9  /* no such tensor or key */
 } okf_status;
 
 /* ggml type ids, LLM/Base/GGUF.swift:3-14 */
@@ -136,6 +139,44 @@ int okf_last_hip_error(okf_ctx *ctx);
 
 /* Static text for a status code. */
 const char *okf_strerror(int status);
+
+/* ---------------------------------------------------------------- GGUF --
+ * The weight source: GGUF(path:) (LLM/Base/GGUF.swift:99-151) maps a file and
+ * parses its metadata and tensor directory; MetalContext's weight windows
+ * (LLM/Base/MetalContext.swift:58-185) make the tensor data GPU-resident.
+ * Here okf_gguf_open maps and parses (host only), okf_gguf_upload copies the
+ * data region to device memory once, and a tensor's okf_weight is
+ * {device base, tensor offset, K = dims[0], M = dims[1] * dims[2] * dims[3],
+ * ggml_type}. */
+typedef struct okf_gguf okf_gguf;
+
+typedef struct {
+    const char *name;    /* NUL-terminated, valid while the file is open */
+    uint32_t n_dims;
+    uint64_t dims[4];    /* ggml order: dims[0] varies fastest; unused = 1 */
+    int32_t ggml_type;
+    uint64_t offset;     /* byte offset in the data region */
+    uint64_t bytes;      /* GGUF.rowByteCount(type, all elements) */
+} okf_gguf_tensor;
+
+int okf_gguf_open(const char *path, okf_gguf **out);
+int okf_gguf_close(okf_gguf *g);
+int okf_gguf_tensor_count(const okf_gguf *g, uint64_t *n);
+int okf_gguf_tensor_at(const okf_gguf *g, uint64_t i, okf_gguf_tensor *t);
+/* GGUF.tensor / GGUF.maybe (GGUF.swift:305-311): OKF_E_NOTFOUND if absent */
+int okf_gguf_find(const okf_gguf *g, const char *name, okf_gguf_tensor *t);
+/* GGUF.int (a bool reads as 0 / 1, GGUF.swift:193-214) */
+int okf_gguf_kv_int(const okf_gguf *g, const char *key, int64_t *v);
+/* GGUF.double (an int reads as its value) */
+int okf_gguf_kv_double(const okf_gguf *g, const char *key, double *v);
+/* GGUF.string: pointer and length, valid while the file is open */
+int okf_gguf_kv_string(const okf_gguf *g, const char *key, const char **s, uint64_t *len);
+/* the mapped data region (host memory) */
+int okf_gguf_data(const okf_gguf *g, const void **host, uint64_t *bytes);
+/* a device copy of the data region (hipMalloc + copy, synchronous) */
+int okf_gguf_upload(okf_ctx *ctx, const okf_gguf *g, void **device);
+/* frees a device copy made by okf_gguf_upload */
+int okf_gguf_free_device(okf_ctx *ctx, void *device);
 
 #ifdef __cplusplus
 }

@@ -6,6 +6,7 @@ narrow matmul and tile GEMM outputs within max|gpu - ref| / max|ref| <= 1e-3
 at the north-star tolerance); narrow-N vs N x gemv within 1e-5
 (QwenMetalSelfTest.swift:478-483).
 """
+import ctypes
 import functools
 import sys
 
@@ -330,3 +331,27 @@ def test_embed_batch_clamps_ids(enc):
     assert np.array_equal(got[0], oracle.dequant(Q4_K, w[:rb], K))
     assert np.array_equal(got[1], oracle.dequant(Q4_K, w[7 * rb:8 * rb], K))
     assert np.array_equal(got[2], got[1])
+
+
+# ------------------------------------------------------------------ GGUF weights
+def test_gguf_upload_then_gemv(enc, tmp_path):
+    # GGUF(path:) + the MetalContext weight window: a tensor read from a file,
+    # made device-resident, then used through its okf_weight
+    import ggufw as gw
+    w4 = weights(Q4_K, 96, 1024, 93)
+    w2 = weights(Q2_0, 64, 512, 94)
+    path = tmp_path / "m.gguf"
+    gw.write(path, [("general.alignment", gw.U32, 32)],
+             [("a.weight", [1024, 96], Q4_K, w4.tobytes()), ("b.weight", [512, 64], Q2_0, w2.tobytes())])
+    with ok.GGUF(str(path)) as g:
+        base = g.upload(enc)
+        try:
+            for name, t, M, K, w in (("a.weight", Q4_K, 96, 1024, w4), ("b.weight", Q2_0, 64, 512, w2)):
+                x = acts(1, K, 95)
+                y = torch.full((M,), float("nan"), device="cuda")
+                enc.gemv(g.weight(name, base), dev(x), y)
+                ref = oracle.matvec(t, w, K, M, x[0]).astype(np.float64)
+                assert rel(host(y), ref) <= TOL
+        finally:
+            enc.sync()
+            enc._lib.okf_gguf_free_device(enc.h, ctypes.c_void_p(base))
