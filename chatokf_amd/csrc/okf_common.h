@@ -5,15 +5,15 @@
 
 namespace okf {
 
-enum Fmt : int { Q8_0 = 8, Q4_K = 12, IQ2_XXS = 16, Q2_0 = 42 };
+enum Fmt : int { Q4_0 = 2, Q8_0 = 8, Q4_K = 12, IQ2_XXS = 16, IQ4_NL = 20, Q2_0 = 42 };
 
 // Bytes of one 256-weight span (Q8_0: 8 blocks, Q2_0: 2 blocks), matching the
 // reference's IQArgs.blk (LLM/Base/MetalEnc.swift:162-167).
 __host__ __device__ constexpr uint32_t block_bytes(int f) {
-    return f == Q8_0 ? 34 : f == Q2_0 ? 34 : f == Q4_K ? 144 : 66;
+    return f == Q8_0 ? 34 : f == Q2_0 ? 34 : f == Q4_K ? 144 : (f == Q4_0 || f == IQ4_NL) ? 18 : 66;
 }
 __host__ __device__ constexpr uint32_t block_elems(int f) {
-    return f == Q8_0 ? 32 : f == Q2_0 ? 128 : 256;
+    return (f == Q8_0 || f == Q4_0 || f == IQ4_NL) ? 32 : f == Q2_0 ? 128 : 256;
 }
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -49,6 +49,12 @@ __device__ __forceinline__ float wave_sum(float v) {
 // eighth that makes the count of set bits even.
 __device__ __forceinline__ uint32_t iq2_signs(uint32_t s7) {
     return s7 | ((__builtin_popcount(s7) & 1u) << 7);
+}
+
+// IQ4_NL's 16 levels (IQ4_NL.kvalues, LLM/Gemma/Gemma4Quant.swift:8-11)
+__host__ __device__ constexpr int8_t iq4nl_level(int i) {
+    constexpr int8_t v[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+    return v[i];
 }
 
 }  // namespace okf

@@ -105,12 +105,44 @@ __device__ __forceinline__ void decode_unit_iq2_xxs(const uint8_t *row, uint32_t
     }
 }
 
+// Q4_0.dequant, LLM/Gemma/Gemma4Quant.swift:30-49: byte j of the block gives
+// w[j] = (Float(b & 0xF) - 8) * d and w[j + 16] = (Float(b >> 4) - 8) * d.
+__device__ __forceinline__ void decode_unit_q4_0(const uint8_t *row, uint32_t u, float *w) {
+    const uint8_t *b = row + (uint64_t)u * 18;
+    float d = h2f(ldu<uint16_t>(b));
+    uint32_t q[4];
+    *(uint4 *)&q[0] = ldu<uint4>(b + 2);
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const uint32_t v = byte_of(q[j >> 2], j & 3);
+        w[j] = ((float)(v & 15) - 8.0f) * d;
+        w[j + 16] = ((float)(v >> 4) - 8.0f) * d;
+    }
+}
+
+// IQ4_NL.dequant, Gemma4Quant.swift:13-27: w = kvalues[nibble] * d, the same
+// nibble placement as Q4_0.
+__device__ __forceinline__ void decode_unit_iq4_nl(const uint8_t *row, uint32_t u, float *w) {
+    const uint8_t *b = row + (uint64_t)u * 18;
+    float d = h2f(ldu<uint16_t>(b));
+    uint32_t q[4];
+    *(uint4 *)&q[0] = ldu<uint4>(b + 2);
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const uint32_t v = byte_of(q[j >> 2], j & 3);
+        w[j] = (float)iq4nl_level(v & 15) * d;
+        w[j + 16] = (float)iq4nl_level(v >> 4) * d;
+    }
+}
+
 template <int F>
 __device__ __forceinline__ void decode_unit(const uint8_t *row, uint32_t u, float *w,
                                             const uint2 *grid) {
     if constexpr (F == Q8_0) decode_unit_q8_0(row, u, w);
     else if constexpr (F == Q2_0) decode_unit_q2_0(row, u, w);
     else if constexpr (F == Q4_K) decode_unit_q4_k(row, u, w);
+    else if constexpr (F == Q4_0) decode_unit_q4_0(row, u, w);
+    else if constexpr (F == IQ4_NL) decode_unit_iq4_nl(row, u, w);
     else decode_unit_iq2_xxs(row, u, w, grid);
 }
 

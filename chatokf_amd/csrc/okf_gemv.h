@@ -32,7 +32,9 @@ namespace okf {
 // Weights per unit: 64, except Q8_0 whose unit is one 32-weight block (so
 // any K that is a whole number of blocks works).
 template <int F>
-__host__ __device__ constexpr uint32_t unit_weights() { return F == Q8_0 ? 32 : 64; }
+__host__ __device__ constexpr uint32_t unit_weights() {
+    return (F == Q8_0 || F == Q4_0 || F == IQ4_NL) ? 32 : 64;
+}
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -83,6 +85,16 @@ struct Unit<Q2_0, R> {  // d + 16 code bytes (64 codes)
     uint32_t d[R];
     u32x4 q[R];
 };
+template <int R>
+struct Unit<Q4_0, R> {  // one block: d + 16 code bytes (32 nibbles)
+    uint32_t d[R];
+    u32x4 q[R];
+};
+template <int R>
+struct Unit<IQ4_NL, R> {  // as Q4_0
+    uint32_t d[R];
+    u32x4 q[R];
+};
 
 template <int F, int R>
 __device__ __forceinline__ void load_unit(const uint8_t *const rows[R], uint32_t u, Unit<F, R> &w) {
@@ -103,6 +115,10 @@ __device__ __forceinline__ void load_unit(const uint8_t *const rows[R], uint32_t
             w.d[r] = ldu<uint16_t>(b);
             w.q0[r] = ldu<u32x4>(b + 2);
             w.q1[r] = ldu<u32x4>(b + 18);
+        } else if constexpr (F == Q4_0 || F == IQ4_NL) {
+            const uint8_t *b = rows[r] + (uint64_t)u * 18;
+            w.d[r] = ldu<uint16_t>(b);
+            w.q[r] = ldu<u32x4>(b + 2);
         } else {
             const uint8_t *b = rows[r] + (uint64_t)(u >> 1) * 34;
             w.d[r] = ldu<uint16_t>(b);
@@ -121,7 +137,9 @@ __device__ __forceinline__ void load_unit(const uint8_t *const rows[R], uint32_t
 //  Q2_0: code dword j (16 codes, weights 16j..) gives pairs (c, c + 8); slot
 //        s = 2j + h is A = x[16j + 4h..], B = x[16j + 8 + 4h..] as
 //        A0 B0 A1 B1 A2 B2 A3 B3.
-//  Q8_0, IQ2_XXS: natural order, A = x[8s..], B = x[8s+4..].
+//  Q4_0: as Q4_K with 16 code bytes: slots 0, 1 are the low nibbles
+//        (weights 0..15), slots 2, 3 the high ones (16..31).
+//  Q8_0, IQ2_XXS, IQ4_NL: natural order, A = x[8s..], B = x[8s+4..].
 template <int F>
 __device__ __forceinline__ uint32_t slot_first(uint32_t s, uint32_t &second) {
     if constexpr (F == Q2_0) {
@@ -141,7 +159,7 @@ __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
 
 template <int F>
 __device__ __forceinline__ u32x4 slot_pack(floatx4 A, floatx4 B) {
-    if constexpr (F == Q4_K)
+    if constexpr (F == Q4_K || F == Q4_0)
         return u32x4{pack_h2(A[0], A[2]), pack_h2(A[1], A[3]), pack_h2(B[0], B[2]),
                      pack_h2(B[1], B[3])};
     else if constexpr (F == Q2_0)
@@ -323,6 +341,118 @@ struct Compute<Q8_0, NC, R> {
                     const uint32_t hv = perm(0x64646464u, dw, (e & 1) ? 0x04030402u : 0x04010400u);
 #pragma unroll
                     for (int n = 0; n < NC; n++) s[r][n] = dot2(hv, xv[n][e], s[r][n]);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const float d = h2f(w.d[r]);
+#pragma unroll
+            for (int n = 0; n < NC; n++) acc[r][n] += d * (s[r][n] - 1152.0f * xsum[n]);
+        }
+    }
+};
+
+template <int NC, int R>
+struct Compute<Q4_0, NC, R> {
+    // Code dword i (bytes 4i..4i+3): low nibbles are weights 4i..4i+3, high
+    // nibbles 16 + 4i..; each becomes fp16 1024 + q by v_bfi (the high ones
+    // shifted down first), so sum((q - 8) x) = sum((1024 + q) x) - 1032 sum(x).
+    __device__ __forceinline__ static void run(const Unit<Q4_0, R> &w, const uint32_t *xp, uint32_t ss, uint32_t cs,
+                                               const float *xsp, uint32_t xcs, uint32_t,
+                                               float (&acc)[R][NC], const u32x4 *) {
+        float xsum[NC], s[R][NC];
+#pragma unroll
+        for (int n = 0; n < NC; n++) xsum[n] = xsp[n * xcs];
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int n = 0; n < NC; n++) s[r][n] = 0;
+#pragma unroll
+        for (int sl = 0; sl < 2; sl++) {  // code dwords 2 sl, 2 sl + 1
+            u32x4 xl[NC], xh[NC];
+#pragma unroll
+            for (int n = 0; n < NC; n++) {
+                xl[n] = *(const u32x4 *)(xp + n * cs + sl * ss);
+                xh[n] = *(const u32x4 *)(xp + n * cs + (2 + sl) * ss);
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const uint32_t v = w.q[r][2 * sl + h], v4 = v >> 4;
+                    const uint32_t l02 = bfi(0x000F000Fu, v, MAGIC2);
+                    const uint32_t l13 = bfi(0x000F000Fu, v >> 8, MAGIC2);
+                    const uint32_t h02 = bfi(0x000F000Fu, v4, MAGIC2);
+                    const uint32_t h13 = bfi(0x000F000Fu, v4 >> 8, MAGIC2);
+#pragma unroll
+                    for (int n = 0; n < NC; n++) {
+                        s[r][n] = dot2(l02, xl[n][2 * h], s[r][n]);
+                        s[r][n] = dot2(l13, xl[n][2 * h + 1], s[r][n]);
+                        s[r][n] = dot2(h02, xh[n][2 * h], s[r][n]);
+                        s[r][n] = dot2(h13, xh[n][2 * h + 1], s[r][n]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const float d = h2f(w.d[r]);
+#pragma unroll
+            for (int n = 0; n < NC; n++) acc[r][n] += d * (s[r][n] - 1032.0f * xsum[n]);
+        }
+    }
+};
+
+template <int NC, int R>
+struct Compute<IQ4_NL, NC, R> {
+    // The 16 levels plus 128 as bytes: entries 0..7 and 8..15.  A code dword's
+    // four low (or high) nibbles index them with two v_perm and a per-byte
+    // select on bit 3 (v_perm selector 0x0C gives 0x00, 0x0D gives 0xFF);
+    // v_perm then puts each byte under 0x64, fp16 1024 + (level + 128), so
+    // sum(level x) = sum((1152 + level) x) - 1152 sum(x).
+    static constexpr uint32_t lvb(int i) { return (uint32_t)(uint8_t)(iq4nl_level(i) + 128); }
+    static constexpr uint32_t T0 = lvb(0) | lvb(1) << 8 | lvb(2) << 16 | lvb(3) << 24;
+    static constexpr uint32_t T1 = lvb(4) | lvb(5) << 8 | lvb(6) << 16 | lvb(7) << 24;
+    static constexpr uint32_t T2 = lvb(8) | lvb(9) << 8 | lvb(10) << 16 | lvb(11) << 24;
+    static constexpr uint32_t T3 = lvb(12) | lvb(13) << 8 | lvb(14) << 16 | lvb(15) << 24;
+    __device__ __forceinline__ static uint32_t levels(uint32_t nib) {  // 4 nibbles, one per byte
+        const uint32_t sel = nib & 0x07070707u;
+        const uint32_t lo = perm(T1, T0, sel), hi = perm(T3, T2, sel);
+        const uint32_t m = perm(0, 0, ((nib >> 3) & 0x01010101u) | 0x0C0C0C0Cu);
+        return (hi & m) | (lo & ~m);
+    }
+    __device__ __forceinline__ static void run(const Unit<IQ4_NL, R> &w, const uint32_t *xp, uint32_t ss, uint32_t cs,
+                                               const float *xsp, uint32_t xcs, uint32_t,
+                                               float (&acc)[R][NC], const u32x4 *) {
+        float xsum[NC], s[R][NC];
+#pragma unroll
+        for (int n = 0; n < NC; n++) xsum[n] = xsp[n * xcs];
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int n = 0; n < NC; n++) s[r][n] = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {  // code dword i: weights 4i.. (low), 16 + 4i.. (high)
+            u32x4 xl[NC], xh[NC];
+#pragma unroll
+            for (int n = 0; n < NC; n++) {
+                xl[n] = *(const u32x4 *)(xp + n * cs + (i >> 1) * ss);
+                xh[n] = *(const u32x4 *)(xp + n * cs + (2 + (i >> 1)) * ss);
+            }
+            const int e = 2 * (i & 1);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const uint32_t v = w.q[r][i];
+                const uint32_t bl = levels(v & 0x0F0F0F0Fu), bh = levels((v >> 4) & 0x0F0F0F0Fu);
+                const uint32_t l01 = perm(0x64646464u, bl, 0x04010400u), l23 = perm(0x64646464u, bl, 0x04030402u);
+                const uint32_t h01 = perm(0x64646464u, bh, 0x04010400u), h23 = perm(0x64646464u, bh, 0x04030402u);
+#pragma unroll
+                for (int n = 0; n < NC; n++) {
+                    s[r][n] = dot2(l01, xl[n][e], s[r][n]);
+                    s[r][n] = dot2(l23, xl[n][e + 1], s[r][n]);
+                    s[r][n] = dot2(h01, xh[n][e], s[r][n]);
+                    s[r][n] = dot2(h23, xh[n][e + 1], s[r][n]);
                 }
             }
         }

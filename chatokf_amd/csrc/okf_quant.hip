@@ -68,7 +68,9 @@ namespace {
 
 using namespace okf;
 
-bool supported(int32_t t) { return t == Q8_0 || t == Q4_K || t == IQ2_XXS || t == Q2_0; }
+bool supported(int32_t t) {
+    return t == Q8_0 || t == Q4_K || t == IQ2_XXS || t == Q2_0 || t == Q4_0 || t == IQ4_NL;
+}
 
 int hip_fail(okf_ctx *c, hipError_t e) {
     c->last_hip = (int)e;
@@ -288,6 +290,8 @@ void launch_embed(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_
     case Q8_0: fn<Q8_0>(__VA_ARGS__); break;                \
     case Q2_0: fn<Q2_0>(__VA_ARGS__); break;                \
     case Q4_K: fn<Q4_K>(__VA_ARGS__); break;                \
+    case Q4_0: fn<Q4_0>(__VA_ARGS__); break;                \
+    case IQ4_NL: fn<IQ4_NL>(__VA_ARGS__); break;            \
     default: fn<IQ2_XXS>(__VA_ARGS__); break;               \
     }
 
@@ -316,6 +320,8 @@ int run_gemm(okf_ctx *c, const okf_weight *w, const float *X, uint32_t N, float 
         case Q8_0: st = launch_gemm<Q8_0>(c, W, rb, w->K, w->M, X, N, Y); break;
         case Q2_0: st = launch_gemm<Q2_0>(c, W, rb, w->K, w->M, X, N, Y); break;
         case Q4_K: st = launch_gemm<Q4_K>(c, W, rb, w->K, w->M, X, N, Y); break;
+        case Q4_0: st = launch_gemm<Q4_0>(c, W, rb, w->K, w->M, X, N, Y); break;
+        case IQ4_NL: st = launch_gemm<IQ4_NL>(c, W, rb, w->K, w->M, X, N, Y); break;
         default: st = launch_gemm<IQ2_XXS>(c, W, rb, w->K, w->M, X, N, Y); break;
         }
         if (st) return st;

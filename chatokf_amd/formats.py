@@ -4,16 +4,19 @@ Type ids follow ``LLM/Base/GGUF.swift:3-14``; bytes per row follow
 ``GGUF.rowByteCount`` (``LLM/Base/GGUF.swift:160-188``) and elements per block
 follow ``GQ.blockElems`` (``LLM/Gemma/Gemma4Quant.swift:77-87``).
 """
+Q4_0 = 2
 Q8_0 = 8
+IQ4_NL = 20
 Q4_K = 12
 IQ2_XXS = 16
 Q2_0 = 42
 
-NAMES = {Q8_0: "q8_0", Q4_K: "q4_k", IQ2_XXS: "iq2_xxs", Q2_0: "q2_0"}
+NAMES = {Q8_0: "q8_0", Q4_K: "q4_k", IQ2_XXS: "iq2_xxs", Q2_0: "q2_0", Q4_0: "q4_0", IQ4_NL: "iq4_nl"}
 BY_NAME = {v: k for k, v in NAMES.items()}
 
 # type -> (weights per block, bytes per block)
-BLOCK = {Q8_0: (32, 34), Q2_0: (128, 34), Q4_K: (256, 144), IQ2_XXS: (256, 66)}
+BLOCK = {Q8_0: (32, 34), Q2_0: (128, 34), Q4_K: (256, 144), IQ2_XXS: (256, 66), Q4_0: (32, 18),
+         IQ4_NL: (32, 18)}
 
 
 def block_elems(t: int) -> int:

@@ -25,7 +25,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from .formats import Q8_0, Q2_0, Q4_K, IQ2_XXS, row_bytes
+from .formats import Q8_0, Q2_0, Q4_K, IQ2_XXS, Q4_0, IQ4_NL, row_bytes
 
 _A = 6364136223846793005
 _C = 1442695040888963407
@@ -87,6 +87,18 @@ def q8_0(M: int, K: int, seed: int, d_range=(1e-3, 1e-2)) -> np.ndarray:
     return blk.reshape(-1)
 
 
+def nibble32(M: int, K: int, seed: int, d_range=(1e-3, 1e-2)) -> np.ndarray:
+    """M rows of 18-byte 32-weight blocks (Q4_0 / IQ4_NL): d ~ U(d_range) as
+    fp16, the 16 code bytes uniform random."""
+    nb = M * (K // 32)
+    g = LCG(seed)
+    d = g.f16(*d_range, nb)
+    blk = np.empty((nb, 18), np.uint8)
+    blk[:, :2] = _f16_bytes(d)
+    blk[:, 2:] = g.bytes(nb * 16).reshape(nb, 16)
+    return blk.reshape(-1)
+
+
 def q2_0(M: int, K: int, seed: int, d_range=(0.01, 0.05), codes=3) -> np.ndarray:
     """M rows of Q2_0 (Bonsai ternary): codes uniform in {0..codes-1}, d ~ U."""
     nb = M * (K // 128)
@@ -125,7 +137,7 @@ def iq2_xxs(M: int, K: int, seed: int, d_range=(1e-3, 1e-2)) -> np.ndarray:
     return blk.reshape(-1)
 
 
-GENERATORS = {Q8_0: q8_0, Q2_0: q2_0, Q4_K: q4_k, IQ2_XXS: iq2_xxs}
+GENERATORS = {Q8_0: q8_0, Q2_0: q2_0, Q4_K: q4_k, IQ2_XXS: iq2_xxs, Q4_0: nibble32, IQ4_NL: nibble32}
 
 
 def weights(ggml_type: int, M: int, K: int, seed: int) -> np.ndarray:

@@ -1,7 +1,7 @@
 /*
  * okf_quant.h -- C ABI of the MI355X (gfx950) quantized weight x activation
  * path: fused dequantize-and-dot for GGUF Q8_0, Q4_K, IQ2_XXS and the Bonsai
- * ternary Q2_0 blocks.
+ * ternary Q2_0 blocks, plus Q4_0 and IQ4_NL.
  *
  * This ABI is the drop-in boundary for the reference's GPU dispatch surface
  * (LLM/Base/MetalEnc.swift) and the weight reference it takes
@@ -45,7 +45,9 @@ typedef enum {
 
 /* ggml type ids, LLM/Base/GGUF.swift:3-14 */
 enum {
+    OKF_TYPE_Q4_0 = 2,
     OKF_TYPE_Q8_0 = 8,
+    OKF_TYPE_IQ4_NL = 20,
     OKF_TYPE_Q4_K = 12,
     OKF_TYPE_IQ2_XXS = 16,
     OKF_TYPE_Q2_0 = 42

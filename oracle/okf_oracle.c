@@ -62,6 +62,8 @@ static inline float ldh(const uint8_t *p) { return okf_ref_f16_to_f32(ld16(p)); 
 static int block_geom(int32_t type, uint32_t *elems, uint32_t *bytes) {
     switch (type) {
     case OKF_REF_Q8_0: *elems = 32; *bytes = 34; return 0;
+    case OKF_REF_Q4_0: *elems = 32; *bytes = 18; return 0;
+    case OKF_REF_IQ4_NL: *elems = 32; *bytes = 18; return 0;
     case OKF_REF_Q2_0: *elems = 128; *bytes = 34; return 0;
     case OKF_REF_Q4_K: *elems = 256; *bytes = 144; return 0;
     case OKF_REF_IQ2_XXS: *elems = 256; *bytes = 66; return 0;
@@ -84,6 +86,33 @@ static void dq_q8_0(const uint8_t *p, uint64_t n, float *out) {
     for (uint64_t b = 0; b < n / 32; b++, p += 34, out += 32) {
         float d = ldh(p);
         for (int j = 0; j < 32; j++) out[j] = (float)(int8_t)p[2 + j] * d;
+    }
+}
+
+/* Q4_0.dequant, LLM/Gemma/Gemma4Quant.swift:30-49: byte j of the 16 gives
+ * w[j] = (Float(b & 0xF) - 8) * d and w[j + 16] = (Float(b >> 4) - 8) * d */
+static void dq_q4_0(const uint8_t *p, uint64_t n, float *out) {
+    for (uint64_t b = 0; b < n / 32; b++, p += 18, out += 32) {
+        float d = ldh(p);
+        for (int j = 0; j < 16; j++) {
+            out[j] = ((float)(p[2 + j] & 0xF) - 8) * d;
+            out[j + 16] = ((float)(p[2 + j] >> 4) - 8) * d;
+        }
+    }
+}
+
+/* IQ4_NL.kvalues, LLM/Gemma/Gemma4Quant.swift:8-11 (the format's table) */
+static const float iq4nl_values[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                       1,    13,   25,  38,  53,  69,  89,  113};
+
+/* IQ4_NL.dequant, Gemma4Quant.swift:13-27: w = kvalues[nibble] * d */
+static void dq_iq4_nl(const uint8_t *p, uint64_t n, float *out) {
+    for (uint64_t b = 0; b < n / 32; b++, p += 18, out += 32) {
+        float d = ldh(p);
+        for (int j = 0; j < 16; j++) {
+            out[j] = iq4nl_values[p[2 + j] & 0xF] * d;
+            out[j + 16] = iq4nl_values[p[2 + j] >> 4] * d;
+        }
     }
 }
 
@@ -172,6 +201,8 @@ int okf_ref_dequant(int32_t type, const uint8_t *p, uint64_t n, float *out) {
     switch (type) {
     case OKF_REF_Q8_0: dq_q8_0(p, n, out); break;
     case OKF_REF_Q2_0: dq_q2_0(p, n, out); break;
+    case OKF_REF_Q4_0: dq_q4_0(p, n, out); break;
+    case OKF_REF_IQ4_NL: dq_iq4_nl(p, n, out); break;
     default: { /* superBlockGather, Gemma4Quant.swift:351-360 */
         sb_decode_fn dec = sb_decoder(type);
         for (uint64_t b = 0; b < n / 256; b++) dec(p + b * bytes, out + b * 256);
@@ -202,6 +233,28 @@ static float row_q8_0(const job_t *j, uint32_t m) {
         float a = 0;
         float d = ldh(p);
         for (int t = 0; t < 32; t++) a += (float)(int8_t)p[2 + t] * j->x[k + t];
+        acc += a * d;
+    }
+    return acc;
+}
+
+/* GQ.matvec q4_0 / iq4_nl arms, Gemma4Quant.swift:93-114: per block, for j
+ * ascending acc_b += w(lo nibble j) * x[k + j], then += w(hi nibble j) *
+ * x[k + j + 16] (w = nibble - 8 or kvalues[nibble]); acc += acc_b * d. */
+static float row_nibble32(const job_t *j, uint32_t m) {
+    const uint8_t *p = j->w + (uint64_t)m * j->row_bytes;
+    const int nl = j->type == OKF_REF_IQ4_NL;
+    float acc = 0;
+    for (uint32_t k = 0; k < j->K; k += 32, p += 18) {
+        float a = 0;
+        float d = ldh(p);
+        for (int t = 0; t < 16; t++) {
+            const uint8_t b = p[2 + t];
+            const float lo = nl ? iq4nl_values[b & 0xF] : (float)(b & 0xF) - 8;
+            const float hi = nl ? iq4nl_values[b >> 4] : (float)(b >> 4) - 8;
+            a += lo * j->x[k + t];
+            a += hi * j->x[k + t + 16];
+        }
         acc += a * d;
     }
     return acc;
@@ -244,15 +297,17 @@ static float row_superblock(const job_t *j, uint32_t m) {
     return acc;
 }
 
-/* GQ.blockMatmul, Gemma4Quant.swift:172-223 (Q8_0): per row, every block is
- * dequantized once and acc[n] += w_j * XT[k + j][n]. */
+/* GQ.blockMatmul, Gemma4Quant.swift:172-223 (Q8_0, Q4_0): per row, every
+ * block is dequantized once and acc[n] += w_j * XT[k + j][n]. */
 static void row_block_matmul_q8_0(const job_t *j, uint32_t m, float *acc) {
     const uint8_t *p = j->w + (uint64_t)m * j->row_bytes;
     uint32_t N = j->N;
+    const int q4 = j->type == OKF_REF_Q4_0;
     float blk[32];
     for (uint32_t n = 0; n < N; n++) acc[n] = 0;
-    for (uint32_t k = 0; k < j->K; k += 32, p += 34) {
-        dq_q8_0(p, 32, blk);
+    for (uint32_t k = 0; k < j->K; k += 32, p += q4 ? 18 : 34) {
+        if (q4) dq_q4_0(p, 32, blk);
+        else dq_q8_0(p, 32, blk);
         for (int t = 0; t < 32; t++) {
             float wj = blk[t];
             const float *col = j->x + (uint64_t)(k + t) * N;
@@ -285,6 +340,7 @@ static void *run_slice(void *arg) {
         switch (j->type) {
         case OKF_REF_Q8_0: v = row_q8_0(j, m); break;
         case OKF_REF_Q2_0: v = row_q2_0(j, m); break;
+        case OKF_REF_Q4_0: case OKF_REF_IQ4_NL: v = row_nibble32(j, m); break;
         default: v = row_superblock(j, m); break;
         }
         j->y[m] = v;
@@ -344,7 +400,7 @@ int okf_ref_matmul(int32_t type, const uint8_t *w, uint32_t K, uint32_t M,
                    const float *X, uint32_t N, float *Y, int threads) {
     uint64_t rb;
     if (check(type, K, &rb)) return -1;
-    if (type == OKF_REF_Q8_0) {
+    if (type == OKF_REF_Q8_0 || type == OKF_REF_Q4_0) {
         /* X transposed to [K][N] (Gemma4Quant.swift:181-188) */
         float *XT = (float *)malloc(sizeof(float) * (uint64_t)N * K);
         if (!XT) return -1;

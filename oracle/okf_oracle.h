@@ -30,7 +30,9 @@ extern "C" {
 
 /* ggml type ids, LLM/Base/GGUF.swift:3-14 */
 enum {
+    OKF_REF_Q4_0 = 2,
     OKF_REF_Q8_0 = 8,
+    OKF_REF_IQ4_NL = 20,
     OKF_REF_Q4_K = 12,
     OKF_REF_IQ2_XXS = 16,
     OKF_REF_Q2_0 = 42,

@@ -9,6 +9,10 @@ imported or executed).  It reads two independent copies of the same tables:
   (``iq2xxs_grid_u32``, the u64 grid split low word first, per
   ``LLM/Quantize/IQTablesEmit.swift:31-39``), ``:1093`` and ``:1104``.
 
+It also reads the IQ4_NL levels from both places: ``IQ4_NL.kvalues``
+(``LLM/Gemma/Gemma4Quant.swift:8-11``) and ``kvalues_iq4nl`` in the Metal
+header.
+
 It refuses to write the fixture unless both copies agree, then stores the
 values (data only) in ``iq2xxs_tables.json`` next to this script.
 """
@@ -40,6 +44,13 @@ def main():
     ks_m = _array(metal, r"constant uchar ksigns_iq2xs\[128\] = \{")
     km_m = _array(metal, r"constant uchar kmask_iq2xs\[8\] = \{")
     assert len(grid) == 256 and len(ksigns) == 128 and len(kmask) == 8
+    gemma = open(os.path.join(REF, "LLM/Gemma/Gemma4Quant.swift")).read()
+    m = re.search(r"static let kvalues: \[Float\] = \[([^\]]*)\]", gemma)
+    nl_swift = [int(v) for v in re.findall(r"-?\d+", m.group(1))]
+    m = re.search(r"kvalues_iq4nl\[16\] = \{([^}]*)\}", metal)
+    nl_metal = [int(v) for v in re.findall(r"-?\d+", m.group(1))]
+    if len(nl_swift) != 16 or nl_swift != nl_metal:
+        raise SystemExit("IQ4_NL levels disagree")
     split = []
     for v in grid:
         split += [v & 0xFFFFFFFF, v >> 32]
@@ -50,6 +61,8 @@ def main():
         "iq2xxs_grid": [f"0x{v:016x}" for v in grid],
         "ksigns": ksigns,
         "kmask": kmask,
+        "kvalues_iq4nl": nl_swift,
+        "kvalues_iq4nl_source": "LLM/Gemma/Gemma4Quant.swift:8-11 == kvalues_iq4nl in LLM/metal/IQTables.h",
     }
     path = os.path.join(HERE, "iq2xxs_tables.json")
     with open(path, "w") as f:

@@ -35,7 +35,8 @@ def test_row_bytes_abi():
     assert lib.okf_row_bytes(ok.Q2_0, 6144, ctypes.byref(out)) == 0 and out.value == 1632
     assert lib.okf_row_bytes(ok.Q8_0, 2048, ctypes.byref(out)) == 0 and out.value == 2176
     assert lib.okf_row_bytes(ok.Q4_K, 100, ctypes.byref(out)) == ok.OKF_E_SHAPE
-    assert lib.okf_row_bytes(2, 64, ctypes.byref(out)) == ok.OKF_E_TYPE  # Q4_0: not on this path
+    assert lib.okf_row_bytes(ok.Q4_0, 64, ctypes.byref(out)) == 0 and out.value == 36
+    assert lib.okf_row_bytes(3, 64, ctypes.byref(out)) == ok.OKF_E_TYPE  # Q4_1: not on this path
 
 
 @pytest.fixture()
@@ -57,7 +58,7 @@ def test_detached_context_validates_then_reports_nodev(detached):
         detached.gemv(ok.QuantTensor(FAKE, 5000, 16, ok.Q4_K), FAKE, FAKE)
     assert e.value.status == ok.OKF_E_SHAPE
     with pytest.raises(ok.OkfError) as e:
-        detached.gemv(ok.QuantTensor(FAKE, 5120, 16, 2), FAKE, FAKE)
+        detached.gemv(ok.QuantTensor(FAKE, 5120, 16, 3), FAKE, FAKE)  # Q4_1: no kernel
     assert e.value.status == ok.OKF_E_TYPE
     with pytest.raises(ok.OkfError) as e:  # Q4_K wants 16-byte aligned blocks
         detached.gemv(ok.QuantTensor(FAKE + 8, 5120, 16, ok.Q4_K), FAKE, FAKE)

@@ -15,7 +15,7 @@ import pytest
 
 import oracle
 from chatokf_amd import synth
-from chatokf_amd.formats import Q8_0, Q2_0, Q4_K, IQ2_XXS, NAMES, row_bytes
+from chatokf_amd.formats import Q8_0, Q2_0, Q4_K, IQ2_XXS, Q4_0, IQ4_NL, NAMES, row_bytes
 
 torch = pytest.importorskip("torch")
 import chatokf_amd as ok  # noqa: E402
@@ -68,7 +68,8 @@ def run_gemm(enc, t, M, K, w, X, tile=False):
 
 
 # ------------------------------------------------------------------ dequant
-DQ_CASES = [(Q8_0, 6, 2048), (Q2_0, 6, 6144), (Q4_K, 4, 5120), (IQ2_XXS, 4, 5120)]
+DQ_CASES = [(Q8_0, 6, 2048), (Q2_0, 6, 6144), (Q4_K, 4, 5120), (IQ2_XXS, 4, 5120), (Q4_0, 6, 4096),
+            (IQ4_NL, 6, 4096)]
 
 
 @pytest.mark.parametrize("t,M,K", DQ_CASES, ids=[NAMES[c[0]] for c in DQ_CASES])
@@ -120,7 +121,9 @@ def test_gemv_full_config(enc, name, t, M, K, seed):
 # Shapes that exercise tails: M not a multiple of the rows per workgroup, a
 # single block per row, K not a multiple of 64 units.
 EDGE = [(Q8_0, 1, 32), (Q8_0, 3, 96), (Q8_0, 4099, 2080), (Q2_0, 5, 128), (Q2_0, 4097, 384),
-        (Q4_K, 1, 256), (Q4_K, 7, 768), (Q4_K, 4101, 2304), (IQ2_XXS, 2, 256), (IQ2_XXS, 4103, 1280)]
+        (Q4_K, 1, 256), (Q4_K, 7, 768), (Q4_K, 4101, 2304), (IQ2_XXS, 2, 256), (IQ2_XXS, 4103, 1280),
+        (Q4_0, 1, 32), (Q4_0, 4099, 2080), (Q4_0, 2048, 4096), (IQ4_NL, 3, 96), (IQ4_NL, 4099, 2080),
+        (IQ4_NL, 2048, 4096)]
 
 
 @pytest.mark.parametrize("t,M,K", EDGE)
@@ -147,7 +150,7 @@ def test_gemv_weight_offset(enc):
 
 
 # ------------------------------------------------------------------ narrow N = 2..5
-@pytest.mark.parametrize("t", [Q8_0, Q2_0, Q4_K, IQ2_XXS], ids=lambda t: NAMES[t])
+@pytest.mark.parametrize("t", [Q8_0, Q2_0, Q4_K, IQ2_XXS, Q4_0, IQ4_NL], ids=lambda t: NAMES[t])
 @pytest.mark.parametrize("N", [2, 3, 4, 5])
 def test_narrow_matches_oracle_and_gemv(enc, t, N):
     M, K = 1030, 2048
@@ -184,7 +187,7 @@ def test_silu_mul_matches_oracle(enc):
     assert np.allclose(got, ref, rtol=1e-5, atol=1e-6)
 
 
-SILU_CASES = [(Q2_0, 2048, 6144, 1102), (Q8_0, 300, 2048, 81), (Q4_K, 260, 2304, 82),
+SILU_CASES = [(Q2_0, 2048, 6144, 1102), (Q8_0, 300, 2048, 81), (Q4_K, 260, 2304, 82), (IQ4_NL, 96, 512, 85),
               (IQ2_XXS, 129, 1536, 83), (Q2_0, 130, 1024, 84)]
 
 
@@ -244,7 +247,8 @@ def test_parallel_group_matches_single_calls(enc):
 # The Q4_K kernel splits the tiles beyond whole rounds of 256 over K ranges:
 # (4224, 256, 512) has 132 tiles and no split, the others split 2..8 ways.
 TILE = [(Q8_0, 300, 2048, 37), (Q2_0, 130, 1024, 129), (Q4_K, 260, 2304, 77), (IQ2_XXS, 129, 1536, 6),
-        (Q4_K, 1, 256, 64), (Q8_0, 5, 96, 200), (Q4_K, 4224, 256, 512), (Q4_K, 1000, 512, 300)]
+        (Q4_K, 1, 256, 64), (Q8_0, 5, 96, 200), (Q4_K, 4224, 256, 512), (Q4_K, 1000, 512, 300),
+        (Q4_0, 300, 2048, 37), (IQ4_NL, 130, 1024, 70)]
 
 
 @pytest.mark.parametrize("t,M,K,N", TILE)
@@ -305,7 +309,7 @@ def test_injected_fault_launches_nothing(enc):
 
 
 # ------------------------------------------------------------------ embedding gather
-@pytest.mark.parametrize("t", [Q8_0, Q2_0, Q4_K, IQ2_XXS], ids=lambda t: NAMES[t])
+@pytest.mark.parametrize("t", [Q8_0, Q2_0, Q4_K, IQ2_XXS, Q4_0, IQ4_NL], ids=lambda t: NAMES[t])
 def test_embed_batch_bit_exact(enc, t):
     # embedBatch (MetalEnc.swift:1096-1146) vs the oracle's dequant of each row
     M, K = 300, 2048

@@ -14,7 +14,7 @@ import pytest
 
 import oracle
 from chatokf_amd import synth
-from chatokf_amd.formats import Q8_0, Q2_0, Q4_K, IQ2_XXS
+from chatokf_amd.formats import Q8_0, Q2_0, Q4_K, IQ2_XXS, Q4_0, IQ4_NL
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 GOLD = json.load(open(os.path.join(ROOT, "tests", "golden", "iq2xxs_tables.json")))
@@ -200,10 +200,22 @@ def np_dequant(t, w, M, K):
                 s = np.where(sg & (1 << j), np.float32(-1), np.float32(1))
                 out[..., l, j] = db * g * s
         return out.reshape(M, K)
+    if t in (Q4_0, IQ4_NL):
+        b = w.reshape(M, K // 32, 18)
+        d = b[:, :, :2].copy().view(np.float16).astype(np.float32)
+        q = np.concatenate([b[:, :, 2:] & 15, b[:, :, 2:] >> 4], -1)  # j, j + 16
+        v = q.astype(np.float32) - 8 if t == Q4_0 else IQ4NL_TABLE[q]
+        return (v * d).reshape(M, K)
     raise ValueError(t)
 
 
-SMALL = [(Q8_0, 64, 256), (Q2_0, 64, 512), (Q4_K, 32, 512), (IQ2_XXS, 32, 512)]
+# IQ4_NL's 16 non-linear levels, as published with the format (ggml's
+# kvalues_iq4nl); the golden test checks them against the reference's copy.
+IQ4NL_TABLE = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113],
+                       np.float32)
+
+SMALL = [(Q8_0, 64, 256), (Q2_0, 64, 512), (Q4_K, 32, 512), (IQ2_XXS, 32, 512), (Q4_0, 64, 256),
+         (IQ4_NL, 64, 256)]
 
 
 @pytest.mark.parametrize("t,M,K", SMALL)
@@ -243,7 +255,7 @@ def test_matmul_is_column_matvecs(t, M, K):
     Y = oracle.matmul(t, w, K, M, X)
     for n in range(3):
         y = oracle.matvec(t, w, K, M, X[n])
-        if t == Q8_0:  # block-reuse matmul sums in another order
+        if t in (Q8_0, Q4_0):  # block-reuse matmul sums in another order
             assert np.abs(Y[n] - y).max() <= 1e-5 * np.abs(y).max()
         else:  # GQ.matmul runs the matvec itself
             assert np.array_equal(Y[n], y)
@@ -282,3 +294,22 @@ def test_silu_mul_known_values_and_float64():
     y = rng.standard_normal(4096).astype(np.float32)
     x64 = x.astype(np.float64)
     assert np.allclose(oracle.silu_mul(x, y), x64 / (1 + np.exp(-x64)) * y, rtol=1e-6, atol=1e-7)
+
+
+def test_q4_0_and_iq4_nl_known_answer():
+    # d = 1: byte j holds codes for weights j (low nibble) and j + 16 (high)
+    d = np.array([1.0], np.float16).view(np.uint8)
+    qs = np.array([(j & 15) | ((15 - (j & 15)) << 4) for j in range(16)], np.uint8)
+    blk = np.concatenate([d, qs])
+    w = oracle.dequant(Q4_0, blk, 32)
+    assert np.array_equal(w[:16], np.arange(16, dtype=np.float32) - 8)
+    assert np.array_equal(w[16:], 15 - np.arange(16, dtype=np.float32) - 8)
+    w = oracle.dequant(IQ4_NL, blk, 32)
+    assert np.array_equal(w[:16], IQ4NL_TABLE)
+    assert np.array_equal(w[16:], IQ4NL_TABLE[::-1])
+
+
+def test_iq4_nl_table_matches_reference_golden():
+    """IQ4_NL.kvalues (LLM/Gemma/Gemma4Quant.swift:8-11), cross-checked against
+    the Metal header's copy by tests/golden/make_iq2_tables.py."""
+    assert np.array_equal(np.array(GOLD["kvalues_iq4nl"], np.float32), IQ4NL_TABLE)
