@@ -313,3 +313,4 @@ def test_iq4_nl_table_matches_reference_golden():
     """IQ4_NL.kvalues (LLM/Gemma/Gemma4Quant.swift:8-11), cross-checked against
     the Metal header's copy by tests/golden/make_iq2_tables.py."""
     assert np.array_equal(np.array(GOLD["kvalues_iq4nl"], np.float32), IQ4NL_TABLE)
+    assert np.all(np.diff(IQ4NL_TABLE) > 0) and IQ4NL_TABLE[0] == -127 and IQ4NL_TABLE[-1] == 113
