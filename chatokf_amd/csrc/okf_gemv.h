@@ -192,11 +192,11 @@ __device__ __forceinline__ uint32_t xs_index(uint32_t u, uint32_t p) {
 // ------------------------------------------------------------- compute --
 // acc[r][n] += unit contribution; xp = this lane's pairs of column 0 in
 // LDS (slot s at xp[s * 64]), cs = uint32 stride between columns.
-template <int F, int NC, int R>
+template <int F, int NC, int R, int TS = 1>
 struct Compute;
 
-template <int NC, int R>
-struct Compute<Q4_K, NC, R> {
+template <int NC, int R, int TS>
+struct Compute<Q4_K, NC, R, TS> {
     // xsum: this unit's two 32-weight sums of the staged fp16 x per column
     // (low-nibble half, high-nibble half), columns xcs floats apart.
     __device__ __forceinline__ static void run(const Unit<Q4_K, R> &w, const uint32_t *xp, uint32_t ss, uint32_t cs,
@@ -264,10 +264,12 @@ struct Compute<Q4_K, NC, R> {
     }
 };
 
-template <int NC, int R>
-struct Compute<IQ2_XXS, NC, R> {
+template <int NC, int R, int TS>
+struct Compute<IQ2_XXS, NC, R, TS> {
     // tab: [0, 256) fp16 grid entries (8 halves), [256, 384) sign masks
-    // (fp16 sign bits of the 8 weights, the eighth from the parity rule).
+    // (fp16 sign bits of the 8 weights, the eighth from the parity rule);
+    // entry e at tab[e * TS] (TS = 16: the replicated, conflict-free layout
+    // of gemv_wide_kernel, tab offset by the lane's copy).
     __device__ __forceinline__ static void run(const Unit<IQ2_XXS, R> &w, const uint32_t *xp, uint32_t ss,
                                                uint32_t cs, const float *, uint32_t, uint32_t,
                                                float (&acc)[R][NC], const u32x4 *tab) {
@@ -289,8 +291,8 @@ struct Compute<IQ2_XXS, NC, R> {
 #pragma unroll
                 for (int r = 0; r < R; r++) {
                     const uint32_t a0 = w.a[r][2 * sb], a1 = w.a[r][2 * sb + 1];
-                    const u32x4 gv = tab[(a0 >> (8 * l)) & 0xFF];
-                    const u32x4 sg = tab[256 + ((a1 >> (7 * l)) & 127)];
+                    const u32x4 gv = tab[((a0 >> (8 * l)) & 0xFF) * TS];
+                    const u32x4 sg = tab[(256 + ((a1 >> (7 * l)) & 127)) * TS];
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
                         const uint32_t wv = gv[e] ^ sg[e];
@@ -310,8 +312,8 @@ struct Compute<IQ2_XXS, NC, R> {
     }
 };
 
-template <int NC, int R>
-struct Compute<Q8_0, NC, R> {
+template <int NC, int R, int TS>
+struct Compute<Q8_0, NC, R, TS> {
     // Code byte j is byte j & 3 of code dword j >> 2; XOR 0x80 turns int8 q
     // into q + 128, so the fp16 0x64 | (q + 128) is 1152 + q.
     __device__ __forceinline__ static void run(const Unit<Q8_0, R> &w, const uint32_t *xp, uint32_t ss, uint32_t cs,
@@ -353,8 +355,8 @@ struct Compute<Q8_0, NC, R> {
     }
 };
 
-template <int NC, int R>
-struct Compute<Q4_0, NC, R> {
+template <int NC, int R, int TS>
+struct Compute<Q4_0, NC, R, TS> {
     // Code dword i (bytes 4i..4i+3): low nibbles are weights 4i..4i+3, high
     // nibbles 16 + 4i..; each becomes fp16 1024 + q by v_bfi (the high ones
     // shifted down first), so sum((q - 8) x) = sum((1024 + q) x) - 1032 sum(x).
@@ -404,8 +406,8 @@ struct Compute<Q4_0, NC, R> {
     }
 };
 
-template <int NC, int R>
-struct Compute<IQ4_NL, NC, R> {
+template <int NC, int R, int TS>
+struct Compute<IQ4_NL, NC, R, TS> {
     // The 16 levels plus 128 as bytes: entries 0..7 and 8..15.  A code dword's
     // four low (or high) nibbles index them with two v_perm and a per-byte
     // select on bit 3 (v_perm selector 0x0C gives 0x00, 0x0D gives 0xFF);
@@ -465,8 +467,8 @@ struct Compute<IQ4_NL, NC, R> {
     }
 };
 
-template <int NC, int R>
-struct Compute<Q2_0, NC, R> {
+template <int NC, int R, int TS>
+struct Compute<Q2_0, NC, R, TS> {
     __device__ __forceinline__ static void run(const Unit<Q2_0, R> &w, const uint32_t *xp, uint32_t ss, uint32_t cs,
                                                const float *xsp, uint32_t xcs, uint32_t,
                                                float (&acc)[R][NC], const u32x4 *) {

@@ -1,0 +1,181 @@
+// okf_gemv_wide.h -- matvec / narrow matmul for matrices large enough to
+// give every CU many rows: one 1024-thread workgroup per CU.
+//
+// Workgroup b owns the contiguous rows [b M / G, (b + 1) M / G).  Its 64 row
+// slots (16 wavefronts x 4 slots of 16 lanes) split those rows' steps (a step
+// = 16 consecutive units of one row, one unit per lane) into 64 contiguous
+// ranges, so every slot does the same work whatever M and K are.  A range
+// may start or end inside a row: at each row boundary the slot reduces its
+// partial sum over its 16 lanes and parks it in LDS, and after one barrier
+// each row adds the partials of the slots that cover it, in slot order (a
+// fixed order, so the result does not depend on timing).
+//
+// All of a lane's weight loads for its first D steps are issued before the
+// activations are staged, and each slot runs only ~M K / (16 * 64 * G * UW)
+// steps, so at the configurations of this path (17408 x 5120) every weight
+// byte of the kernel is requested in the first microsecond.
+//
+// IQ2_XXS: the grid and sign tables (384 rows of 16 bytes) are replicated
+// 16 times in LDS as [row][copy], so that lane i of a slot reads copy i: the
+// 16 lanes of a slot then always hit 16 different 16-byte bank groups, where
+// a single copy read at random rows conflicts.  Measured on MI355X with
+// random rows: 11.5 clocks per wavefront-wide 16-byte read and CU with one
+// copy, 4.7 (the conflict-free rate) with 16.
+#pragma once
+#include "okf_gemv.h"
+
+namespace okf {
+
+constexpr int GW_THREADS = 1024;
+constexpr uint32_t GW_SLOTS = GW_THREADS / GV_L;  // row slots per workgroup
+constexpr uint32_t GW_TAB = 384 * GV_L;           // replicated IQ2_XXS table rows (u32x4)
+
+// Step s of the workgroup -> first step of slot z: floor(z T / 64).
+__device__ __forceinline__ uint32_t gw_start(uint32_t z, uint32_t T) {
+    return (uint32_t)((uint64_t)z * T / GW_SLOTS);
+}
+
+// Dynamic LDS: [replicated IQ2_XXS tables], NC columns of staged pairs
+// (cs uint32 each), NC columns of 32-weight sums (xcs floats each), then
+// the parked partials [64 slots][kmax rows][NC].
+template <int F, int NC, int D, uint32_t SP>
+__global__ __launch_bounds__(GW_THREADS) void gemv_wide_kernel(const uint8_t *__restrict__ W,
+                                                               uint64_t row_bytes, uint32_t K, uint32_t M,
+                                                               const float *__restrict__ X,
+                                                               float *__restrict__ Y,
+                                                               const u32x4 *__restrict__ tab_g,
+                                                               uint32_t kmax) {
+    constexpr int L = GV_L;
+    constexpr uint32_t UW = unit_weights<F>(), SL = UW / 8;
+    constexpr uint32_t TAB = F == IQ2_XXS ? GW_TAB : 0;
+    extern __shared__ u32x4 lds[];
+    const uint32_t tid = threadIdx.x, i = tid % L, z = tid / L;
+    const uint32_t r0 = (uint32_t)((uint64_t)blockIdx.x * M / gridDim.x);
+    const uint32_t r1 = (uint32_t)((uint64_t)(blockIdx.x + 1) * M / gridDim.x);
+    if (r0 == r1) return;  // whole workgroup: no rows (M < grid)
+    const uint32_t units = K / UW, P = (units + L - 1) / L;  // steps per row
+    const uint32_t T = (r1 - r0) * P, s0 = gw_start(z, T), s1 = gw_start(z + 1, T);
+    const uint32_t cunits = P * L, cs = cunits * (UW / 2), xcs = cunits * (UW / 32);
+    u32x4 *tab = lds;
+    uint32_t *xs = (uint32_t *)(lds + TAB);
+    float *xsum = (float *)(xs + NC * cs);
+    float *part = xsum + NC * xcs;
+
+    // Weight loads walk the slot's steps in order: step ls is unit
+    // lsu L + i of row lrow.  The cursor stops at the range's last step, so
+    // the loads past it (and those of an empty range) re-read that unit and
+    // stay in bounds (s0 < T for every slot).
+    const uint8_t *lrow = W + (uint64_t)(r0 + s0 / P) * row_bytes;
+    uint32_t ls = s0, lsu = s0 % P;
+    auto load_next = [&](Unit<F, 1> &w) {
+        const uint8_t *rows[1] = {lrow};
+        load_unit<F, 1>(rows, min(lsu * L + i, units - 1), w);
+        if (ls + 1 < s1) {
+            ls++;
+            if (++lsu == P) {
+                lsu = 0;
+                lrow += row_bytes;
+            }
+        }
+    };
+    // Loads in this order: the table row and the activations this thread
+    // stages, then the weight ring.  Loads complete in issue order, so the
+    // staging then waits for its own loads only, while the weights stream.
+    // (every thread loads and writes TAB / 1024 = 6 table entries, no branch,
+    // so the compiler keeps the loads here)
+    constexpr uint32_t TPT = TAB / GW_THREADS;
+    static_assert(TAB % GW_THREADS == 0, "table entries per thread");
+    u32x4 trow[TPT ? TPT : 1];
+#pragma unroll
+    for (uint32_t k = 0; k < TPT; k++) trow[k] = tab_g[(tid + k * GW_THREADS) / L];
+    const uint32_t nslots = units * SL;  // <= SP * GW_THREADS (host-checked)
+    floatx4 A[SP][NC], B[SP][NC];
+#pragma unroll
+    for (uint32_t p = 0; p < SP; p++) {
+        const uint32_t q = min(p * GW_THREADS + tid, nslots - 1), u = q / SL;
+        uint32_t kb;
+        const uint32_t ka = slot_first<F>(q % SL, kb);
+#pragma unroll
+        for (int n = 0; n < NC; n++) {
+            const uint64_t xo = (uint64_t)n * K + (uint64_t)u * UW;
+            A[p][n] = *(const floatx4 *)(X + xo + ka);
+            B[p][n] = *(const floatx4 *)(X + xo + kb);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // (keep the order of the loads)
+    Unit<F, 1> buf[D];
+#pragma unroll
+    for (int j = 0; j < D; j++) load_next(buf[j]);
+    __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+    for (uint32_t k = 0; k < TPT; k++) tab[tid + k * GW_THREADS] = trow[k];
+    // x as packed fp16 slots and per-32 sums (as stage_x)
+#pragma unroll
+    for (uint32_t p = 0; p < SP; p++) {
+        const uint32_t q = p * GW_THREADS + tid, u = q / SL, sidx = q % SL;
+#pragma unroll
+        for (int n = 0; n < NC; n++) {
+            const u32x4 v = slot_pack<F>(A[p][n], B[p][n]);
+            const float pt = quad_sum(slot_total(v));
+            if (q < nslots) {
+                *(u32x4 *)(xs + n * cs + xs_index<F, L>(u, 4 * sidx)) = v;
+                if ((q & 3) == 0) xsum[n * xcs + q / 4] = pt;
+            }
+        }
+    }
+    __syncthreads();
+
+    // walk the slot's steps; (rl, su) = (row, step within row) of step s
+    float acc[1][NC];
+#pragma unroll
+    for (int n = 0; n < NC; n++) acc[0][n] = 0;
+    uint32_t rl = s0 / P, su = s0 - rl * P, k = 0;
+    auto flush = [&]() {
+#pragma unroll
+        for (int n = 0; n < NC; n++) {
+            const float v = slot_sum<L>(acc[0][n]);
+            if (i == 0) part[(z * kmax + k) * NC + n] = v;
+            acc[0][n] = 0;
+        }
+    };
+    for (uint32_t t = s0; t < s1; t += D) {
+#pragma unroll
+        for (int j = 0; j < D; j++) {
+            if (t + j < s1) {
+                const uint32_t u = su * L + i;
+                if (u < units)
+                    Compute<F, NC, 1, (F == IQ2_XXS ? L : 1)>::run(
+                        buf[j], xs + xs_index<F, L>(u, 0), 4 * L, cs, xsum + u * (UW / 32), xcs, u, acc,
+                        tab + i);
+                if (++su == P && t + j + 1 < s1) {  // next step starts a row
+                    flush();
+                    su = 0;
+                    rl++;
+                    k++;
+                }
+            }
+            load_next(buf[j]);
+        }
+    }
+    if (s0 < s1) flush();
+    __syncthreads();
+
+    // each row: the partials of slots zA..zB (those whose range meets it)
+    const uint32_t n_rows = r1 - r0;
+    for (uint32_t e = tid; e < n_rows * NC; e += GW_THREADS) {
+        const uint32_t rho = e / NC, n = e % NC;
+        const uint32_t sa = rho * P, sb = sa + P - 1;
+        // (T * 64 < 2^32, host-checked)
+        const uint32_t za = ((sa + 1) * GW_SLOTS - 1) / T, zb = ((sb + 1) * GW_SLOTS - 1) / T;
+        float v = 0;
+        for (uint32_t zz = za; zz <= zb; zz++) {
+            const uint32_t st = gw_start(zz, T);
+            if (st < gw_start(zz + 1, T)) v += part[(zz * kmax + (rho - st / P)) * NC + n];
+        }
+        Y[(uint64_t)n * M + r0 + rho] = v;
+    }
+    (void)rl;
+}
+
+}  // namespace okf

@@ -20,6 +20,7 @@
 #include <algorithm>
 #include <vector>
 #include "okf_gemv.h"
+#include "okf_gemv_wide.h"
 #include "okf_gguf.h"
 
 #include "iq2xxs_grid.inc"
@@ -46,6 +47,8 @@ struct okf_ctx {
     // matvec tuning (defaults chosen per shape; OKF_GEMV_* environment
     // variables override them for measurements)
     int gemv_s = 0;      // K split across a workgroup's wavefronts (0 = auto)
+    int gemv_wide = -1;  // one-workgroup-per-CU matvec: -1 auto, 0 never, 1 where it fits
+    uint32_t cus = 256;  // compute units of the device
     double fault_rate = 0;
     uint64_t fault_state = 0;
     int last_hip = 0;
@@ -169,8 +172,68 @@ void launch_gemv_s(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32
 // of rows, K is split two ways across the wavefronts of a workgroup (more,
 // shorter wavefronts); measured on MI355X, a four-way split loses to the
 // extra activation staging it needs.
+template <int F, int NC, uint32_t SP>
+void launch_wide_sp(okf_ctx *c, const GemvCall &call, uint64_t rb, uint32_t K, uint32_t G, size_t lds,
+                    uint32_t kmax) {
+    // weight ring depth: as deep as the registers allow without spills
+    constexpr int D = (F == Q4_K || F == Q8_0) ? (NC == 1 ? 3 : 2)
+                      : F == Q2_0                ? (NC == 1 ? 6 : 2)
+                                                 : (NC <= 2 ? 6 : NC == 3 ? 4 : 3);
+    const void *fn = (const void *)gemv_wide_kernel<F, NC, D, SP>;
+    static bool attr = false;
+    if (!attr) {
+        (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)c->max_lds);
+        attr = true;
+    }
+    hipLaunchKernelGGL((gemv_wide_kernel<F, NC, D, SP>), dim3(G), dim3(GW_THREADS), lds, c->stream, call.W,
+                       rb, K, call.M, call.X, call.Y, c->tab, kmax);
+}
+
+// Where the one-workgroup-per-CU kernel measured faster on MI355X than the
+// many-workgroup one (A/B in one process, configuration shapes): IQ2_XXS
+// with 2..5 columns (conflict-free tables; 28.2 -> 22.5 us at N = 4),
+// Q4_0 / IQ4_NL and long-K Q2_0 with 4..5 columns, and the long-K Q4_K
+// matvec (5120 x 17408: 16.0 -> 15.4 us).
+template <int F, int NC>
+bool wide_auto(const okf_ctx *c, uint32_t M, uint32_t K) {
+    if (M < 8 * c->cus) return F == Q2_0 && NC >= 4 && K >= 4096;
+    if (F == IQ2_XXS) return NC >= 2;
+    if (F == Q4_0 || F == IQ4_NL) return NC >= 4;
+    if (F == Q2_0) return NC >= 4 && K >= 4096;
+    if (F == Q4_K) return NC == 1 && K >= 8192;
+    return false;
+}
+
+// One workgroup per CU (gemv_wide_kernel) for a single matrix: true when
+// launched.
+template <int F, int NC>
+bool launch_gemv_wide(okf_ctx *c, const GemvCall &call, uint64_t rb, uint32_t K) {
+    const int mode = c->gemv_wide;
+    if (mode == 0 || (mode < 0 && !wide_auto<F, NC>(c, call.M, K))) return false;
+    constexpr uint32_t UW = unit_weights<F>();
+    const uint32_t G = std::min(c->cus, call.M), units = K / UW, P = (units + GV_L - 1) / GV_L;
+    const uint64_t nmax = (call.M + G - 1) / G, lmax = (nmax * P + GW_SLOTS - 1) / GW_SLOTS;
+    const uint32_t kmax = (uint32_t)((lmax + P - 1) / P + 1);
+    const uint64_t cunits = (uint64_t)P * GV_L;
+    const size_t lds = (F == IQ2_XXS ? GW_TAB * 16 : 0) + (size_t)NC * cunits * (UW * 2 + UW / 32 * 4) +
+                       (size_t)GW_SLOTS * kmax * NC * sizeof(float);
+    // one staging round (x slots per thread <= SP), step indices in 32 bits
+    const uint32_t nslots = K / 8, sp = (nslots + GW_THREADS - 1) / GW_THREADS;
+    if (lds > c->max_lds || sp > (NC == 1 ? 3u : 1u) || nmax * P * GW_SLOTS >= (1ull << 32)) return false;
+    if constexpr (NC == 1)
+        if (sp > 1) {
+            launch_wide_sp<F, NC, 3>(c, call, rb, K, G, lds, kmax);
+            return true;
+        }
+    launch_wide_sp<F, NC, 1>(c, call, rb, K, G, lds, kmax);
+    return true;
+}
+
 template <int F, int NC, bool SILU = false>
 void launch_gemv_nc(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32_t K) {
+    // (Q4_K and Q8_0 units are too large for a deep ring at N > 1)
+    if constexpr (!SILU && !((F == Q4_K || F == Q8_0) && NC > 1))
+        if (n == 1 && launch_gemv_wide<F, NC>(c, calls[0], rb, K)) return;
     constexpr uint32_t UW = unit_weights<F>();
     const size_t tab = F == IQ2_XXS ? 384 * 16 : 0;
     const uint32_t units = K / UW;
@@ -384,7 +447,11 @@ int okf_ctx_create(int device, okf_ctx **out) {
         if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, device) ==
                 hipSuccess && v > 0)
             c->max_lds = (size_t)v;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess &&
+            v > 0)
+            c->cus = (uint32_t)v;
         if (const char *e = getenv("OKF_GEMV_S")) c->gemv_s = atoi(e);
+        if (const char *e = getenv("OKF_GEMV_WIDE")) c->gemv_wide = atoi(e);
     } else if (device != -1) {
         delete c;
         return OKF_E_ARG;

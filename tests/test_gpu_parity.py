@@ -176,6 +176,41 @@ def test_iq2_xxs_mtp_verify_full_config(enc):
     assert r <= TOL
 
 
+# ------------------------------------------- one workgroup per CU (wide)
+# With OKF_GEMV_WIDE=1 every single-matrix matvec / narrow call that the
+# one-workgroup-per-CU kernel takes goes through it (the automatic policy
+# sends it large IQ2_XXS matrices only).  The shapes cover M below the grid
+# size, rows per workgroup that do not divide evenly, K whose units leave a
+# partial last step, and slot ranges that cross row boundaries.
+WIDE = [(IQ2_XXS, 3, 256, 1), (IQ2_XXS, 257, 1280, 2), (IQ2_XXS, 1000, 5120, 4), (IQ2_XXS, 4103, 1280, 1),
+        (IQ2_XXS, 2048, 2304, 5), (IQ2_XXS, 300, 17408, 1), (Q2_0, 1000, 2048, 1), (Q2_0, 2048, 6144, 2),
+        (Q2_0, 5, 384, 3), (Q4_K, 4101, 2304, 1), (Q4_K, 100, 17408, 1), (Q8_0, 4099, 2080, 1),
+        (Q4_0, 1030, 2048, 4), (IQ4_NL, 1030, 2048, 5)]
+
+
+@pytest.fixture(scope="module")
+def enc_wide():
+    import os
+    os.environ["OKF_GEMV_WIDE"] = "1"
+    try:
+        e = ok.Enc(0)
+    finally:
+        del os.environ["OKF_GEMV_WIDE"]
+    yield e
+    e.close()
+
+
+@pytest.mark.parametrize("t,M,K,N", WIDE)
+def test_wide_matches_oracle_and_default(enc, enc_wide, t, M, K, N):
+    say("wide", NAMES[t], M, K, N)
+    w = weights(t, M, K, 21)
+    X = acts(N, K, 22)
+    ref = oracle.matmul(t, w, K, M, X).astype(np.float64)
+    got = run_gemm(enc_wide, t, M, K, w, X)
+    assert rel(got, ref) <= TOL
+    assert rel(got, run_gemm(enc, t, M, K, w, X).astype(np.float64)) <= 1e-5
+
+
 # ------------------------------------------------------------ SiLU-gated FFN
 def test_silu_mul_matches_oracle(enc):
     a = np.random.default_rng(4).standard_normal(6144).astype(np.float32) * 3
