@@ -178,4 +178,176 @@ __global__ __launch_bounds__(GW_THREADS) void gemv_wide_kernel(const uint8_t *__
     (void)rl;
 }
 
+// ------------------------------------------------------------------------
+// IQ2_XXS with 2..4 activation columns on the matrix cores.
+//
+// v_mfma_f32_4x4x4_16b_f16 computes 16 independent 4x4x4 products; in block
+// b (lanes 4b..4b+3) lane t supplies row t of A and column t of B and
+// receives column t of D (one VGPR per row of D).  Here A = 4 activation
+// columns x 4 consecutive k (zero for columns past NC) and B = 4 k of 4
+// weight rows, so a wavefront is one row quad (lane t: row t of the quad)
+// times 16 units (block b: unit b of the step), and lane t's D is row t's
+// dot product with each of the 4 columns for its unit: sub-block scales
+// are applied lane-locally, and the 16 blocks are summed over lanes once
+// per row quad.  Each lane's 4 weights x 4 columns take one MFMA where the
+// dot2 kernel takes 2 v_dot2 per column, so the weight decode (table reads
+// + sign XOR) is what remains, shared by the columns.  Measured at
+// 17408 x 5120: N = 2 18.6 -> 16.2 us, N = 4 22.7 -> 17.3 us.
+//
+// Activations in LDS, per unit u: 8 k-slots s of 8 halves for each of the 4
+// columns c at 16-byte slot u * 36 + s * 4 + c (4 slots of padding per unit
+// put the 16 lanes of a read on 16 distinct 16-byte bank groups).
+constexpr uint32_t GM_WAVES = GW_THREADS / 64;
+constexpr uint32_t GM_UNIT = 36;  // 16-byte x slots per unit
+
+typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t gm_start(uint32_t z, uint32_t T) {
+    return (uint32_t)((uint64_t)z * T / GM_WAVES);
+}
+
+template <int NC, int D, uint32_t SP>
+__global__ __launch_bounds__(GW_THREADS) void gemv_wide_iq2mm_kernel(const uint8_t *__restrict__ W,
+                                                                     uint64_t row_bytes, uint32_t K,
+                                                                     uint32_t M, const float *__restrict__ X,
+                                                                     float *__restrict__ Y,
+                                                                     const u32x4 *__restrict__ tab_g,
+                                                                     uint32_t kmax) {
+    constexpr int L = GV_L;
+    constexpr uint32_t UW = 64;
+    extern __shared__ u32x4 lds[];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, z = tid >> 6;
+    const uint32_t t = lane & 3, q = lane >> 2;  // row in the quad, unit in the step
+    const uint32_t r0 = (uint32_t)((uint64_t)blockIdx.x * M / gridDim.x);
+    const uint32_t r1 = (uint32_t)((uint64_t)(blockIdx.x + 1) * M / gridDim.x);
+    if (r0 == r1) return;
+    const uint32_t units = K / UW, P = (units + L - 1) / L;
+    const uint32_t nq = (r1 - r0 + 3) / 4, T = nq * P, s0 = gm_start(z, T), s1 = gm_start(z + 1, T);
+    u32x4 *tab = lds;
+    u32x4 *xs = lds + GW_TAB;
+    float *part = (float *)(xs + (size_t)P * L * GM_UNIT);
+
+    // loads: table entries, then activations, then the weight ring
+    constexpr uint32_t TPT = GW_TAB / GW_THREADS;
+    u32x4 trow[TPT];
+#pragma unroll
+    for (uint32_t k = 0; k < TPT; k++) trow[k] = tab_g[(tid + k * GW_THREADS) / L];
+    const uint32_t nx = units * 8 * 4;  // (unit, k-slot, column) entries, <= SP * 1024
+    floatx4 A[SP], B[SP];
+#pragma unroll
+    for (uint32_t p = 0; p < SP; p++) {
+        const uint32_t e = min(p * GW_THREADS + tid, nx - 1), c = e & 3;
+        const uint64_t xo = (uint64_t)min(c, (uint32_t)NC - 1) * K + (e >> 2) * 8;
+        A[p] = *(const floatx4 *)(X + xo);
+        B[p] = *(const floatx4 *)(X + xo + 4);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // weight cursor: step ls = unit lsu * 16 + q of row 4 quad + t
+    const uint32_t lrow0 = r0 + (s0 / P) * 4 + t;
+    const uint8_t *lrow = W + (uint64_t)min(lrow0, r1 - 1) * row_bytes;
+    uint32_t ls = s0, lsu = s0 % P, lr = lrow0;
+    auto load_next = [&](Unit<IQ2_XXS, 1> &w) {
+        const uint8_t *rows[1] = {lrow};
+        load_unit<IQ2_XXS, 1>(rows, min(lsu * L + q, units - 1), w);
+        if (ls + 1 < s1) {
+            ls++;
+            if (++lsu == P) {
+                lsu = 0;
+                lr += 4;
+                lrow = W + (uint64_t)min(lr, r1 - 1) * row_bytes;
+            }
+        }
+    };
+    Unit<IQ2_XXS, 1> buf[D];
+#pragma unroll
+    for (int j = 0; j < D; j++) load_next(buf[j]);
+    __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+    for (uint32_t k = 0; k < TPT; k++) tab[tid + k * GW_THREADS] = trow[k];
+#pragma unroll
+    for (uint32_t p = 0; p < SP; p++) {
+        const uint32_t e = p * GW_THREADS + tid;
+        if (e < nx) {
+            const uint32_t c = e & 3, sl = (e >> 2) & 7, u = e >> 5;
+            u32x4 v = slot_pack<IQ2_XXS>(A[p], B[p]);
+            if (c >= (uint32_t)NC) v = u32x4{0, 0, 0, 0};
+            xs[u * GM_UNIT + sl * 4 + c] = v;
+        }
+    }
+    __syncthreads();
+
+    floatx4 tot = {0, 0, 0, 0};
+    uint32_t su = s0 % P, k = 0;
+    const u32x4 *tl = tab + (lane & (L - 1));  // this lane's table copy
+    auto flush = [&]() {
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            float v = tot[c];
+            v += __shfl_xor(v, 4);
+            v += __shfl_xor(v, 8);
+            v += __shfl_xor(v, 16);
+            v += __shfl_xor(v, 32);
+            tot[c] = v;
+        }
+        if (q == 0)
+#pragma unroll
+            for (int c = 0; c < NC; c++) part[((z * kmax + k) * 4 + t) * NC + c] = tot[c];
+        tot = floatx4{0, 0, 0, 0};
+    };
+    for (uint32_t st = s0; st < s1; st += D) {
+#pragma unroll
+        for (int j = 0; j < D; j++) {
+            if (st + j < s1) {
+                const uint32_t u = su * L + q;
+                const Unit<IQ2_XXS, 1> &w = buf[j];
+                const bool live = u < units;
+                const u32x4 *xp = xs + min(u, units - 1) * GM_UNIT + t;
+#pragma unroll
+                for (int sb = 0; sb < 2; sb++) {
+                    const uint32_t a0 = w.a[0][2 * sb], a1 = w.a[0][2 * sb + 1];
+                    floatx4 acc = {0, 0, 0, 0};
+#pragma unroll
+                    for (int l = 0; l < 4; l++) {
+                        const u32x4 gv = tl[((a0 >> (8 * l)) & 0xFF) * L];
+                        const u32x4 sg = tl[(256 + ((a1 >> (7 * l)) & 127)) * L];
+                        const u32x4 xv = xp[(4 * sb + l) * 4];
+                        const u32x4 wv = gv ^ sg;
+                        acc = __builtin_amdgcn_mfma_f32_4x4x4f16(
+                            __builtin_bit_cast(half4v, uint2{xv[0], xv[1]}),
+                            __builtin_bit_cast(half4v, uint2{wv[0], wv[1]}), acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_4x4x4f16(
+                            __builtin_bit_cast(half4v, uint2{xv[2], xv[3]}),
+                            __builtin_bit_cast(half4v, uint2{wv[2], wv[3]}), acc, 0, 0, 0);
+                    }
+                    const float db = live ? h2f(w.d[0]) * (0.5f + (float)(a1 >> 28)) * 0.25f : 0.0f;
+                    tot += db * acc;
+                }
+                if (++su == P && st + j + 1 < s1) {  // next step starts a row quad
+                    flush();
+                    su = 0;
+                    k++;
+                }
+            }
+            load_next(buf[j]);
+        }
+    }
+    // every lane of the wavefront takes part in the shuffles
+    if (s0 < s1) flush();
+    __syncthreads();
+
+    const uint32_t n_rows = r1 - r0;
+    for (uint32_t e = tid; e < n_rows * NC; e += GW_THREADS) {
+        const uint32_t rho = e / NC, n = e % NC, qd = rho / 4;
+        const uint32_t sa = qd * P, sb = sa + P - 1;
+        const uint32_t za = ((sa + 1) * GM_WAVES - 1) / T, zb = ((sb + 1) * GM_WAVES - 1) / T;
+        float v = 0;
+        for (uint32_t zz = za; zz <= zb; zz++) {
+            const uint32_t st = gm_start(zz, T);
+            if (st < gm_start(zz + 1, T)) v += part[((zz * kmax + (qd - st / P)) * 4 + rho % 4) * NC + n];
+        }
+        Y[(uint64_t)n * M + r0 + rho] = v;
+    }
+}
+
 }  // namespace okf

@@ -18,6 +18,7 @@
 #include "okf_decode.h"
 #include "okf_gemm.h"
 #include <algorithm>
+#include <type_traits>
 #include <vector>
 #include "okf_gemv.h"
 #include "okf_gemv_wide.h"
@@ -204,12 +205,42 @@ bool wide_auto(const okf_ctx *c, uint32_t M, uint32_t K) {
     return false;
 }
 
+// IQ2_XXS with 2..4 columns on the matrix cores (gemv_wide_iq2mm_kernel):
+// true when launched.
+template <int NC>
+bool launch_iq2mm(okf_ctx *c, const GemvCall &call, uint64_t rb, uint32_t K) {
+    const uint32_t G = std::min(c->cus, call.M), units = K / 64, P = (units + GV_L - 1) / GV_L;
+    const uint64_t nq = ((call.M + G - 1) / G + 3) / 4, lmax = (nq * P + GM_WAVES - 1) / GM_WAVES;
+    const uint32_t kmax = (uint32_t)((lmax + P - 1) / P + 1);
+    const size_t lds = GW_TAB * 16 + (size_t)P * GV_L * GM_UNIT * 16 + (size_t)GM_WAVES * kmax * 4 * NC * 4;
+    const uint32_t sp = (units * 32 + GW_THREADS - 1) / GW_THREADS;
+    if (lds > c->max_lds || sp > 3 || nq * P * GM_WAVES >= (1ull << 32)) return false;
+    constexpr int D = 4;
+    auto go = [&](auto spc) {
+        constexpr uint32_t SP = decltype(spc)::value;
+        const void *fn = (const void *)gemv_wide_iq2mm_kernel<NC, D, SP>;
+        static bool attr = false;
+        if (!attr) {
+            (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)c->max_lds);
+            attr = true;
+        }
+        hipLaunchKernelGGL((gemv_wide_iq2mm_kernel<NC, D, SP>), dim3(G), dim3(GW_THREADS), lds, c->stream,
+                           call.W, rb, K, call.M, call.X, call.Y, c->tab, kmax);
+    };
+    if (sp <= 1) go(std::integral_constant<uint32_t, 1>{});
+    else if (sp == 2) go(std::integral_constant<uint32_t, 2>{});
+    else go(std::integral_constant<uint32_t, 3>{});
+    return true;
+}
+
 // One workgroup per CU (gemv_wide_kernel) for a single matrix: true when
 // launched.
 template <int F, int NC>
 bool launch_gemv_wide(okf_ctx *c, const GemvCall &call, uint64_t rb, uint32_t K) {
     const int mode = c->gemv_wide;
     if (mode == 0 || (mode < 0 && !wide_auto<F, NC>(c, call.M, K))) return false;
+    if constexpr (F == IQ2_XXS && NC >= 2 && NC <= 4)  // (mode 2: the dot2 kernel)
+        if (mode != 2 && launch_iq2mm<NC>(c, call, rb, K)) return true;
     constexpr uint32_t UW = unit_weights<F>();
     const uint32_t G = std::min(c->cus, call.M), units = K / UW, P = (units + GV_L - 1) / GV_L;
     const uint64_t nmax = (call.M + G - 1) / G, lmax = (nmax * P + GW_SLOTS - 1) / GW_SLOTS;

@@ -181,9 +181,11 @@ def test_iq2_xxs_mtp_verify_full_config(enc):
 # one-workgroup-per-CU kernel takes goes through it (the automatic policy
 # sends it large IQ2_XXS matrices only).  The shapes cover M below the grid
 # size, rows per workgroup that do not divide evenly, K whose units leave a
-# partial last step, and slot ranges that cross row boundaries.
+# partial last step, and slot ranges that cross row boundaries; IQ2_XXS
+# with 2..4 columns takes the matrix-core variant (row quads).
 WIDE = [(IQ2_XXS, 3, 256, 1), (IQ2_XXS, 257, 1280, 2), (IQ2_XXS, 1000, 5120, 4), (IQ2_XXS, 4103, 1280, 1),
-        (IQ2_XXS, 2048, 2304, 5), (IQ2_XXS, 300, 17408, 1), (Q2_0, 1000, 2048, 1), (Q2_0, 2048, 6144, 2),
+        (IQ2_XXS, 2048, 2304, 5), (IQ2_XXS, 300, 17408, 1), (IQ2_XXS, 3, 256, 2), (IQ2_XXS, 4103, 1280, 3),
+        (IQ2_XXS, 300, 5120, 4), (IQ2_XXS, 2049, 2048, 2), (Q2_0, 1000, 2048, 1), (Q2_0, 2048, 6144, 2),
         (Q2_0, 5, 384, 3), (Q4_K, 4101, 2304, 1), (Q4_K, 100, 17408, 1), (Q8_0, 4099, 2080, 1),
         (Q4_0, 1030, 2048, 4), (IQ4_NL, 1030, 2048, 5)]
 
