@@ -25,6 +25,7 @@ plain device copies of known size to scale the counters); otherwise null.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -265,6 +266,40 @@ def main():
         suite.append(rec)
         del X, Ys
     wcache.clear()
+
+    # the FFN's neighbours: add + RMSNorm over a pp512 batch (x, r, w read,
+    # x and y written) and argmax over one 248320-wide vocabulary row
+    NEIGH = [("add_rmsnorm_512x5120", 512, 5120), ("argmax_rows_1x248320", 1, 248320)]
+    for name, rows, n in NEIGH:
+        if want is not None and name not in want:
+            continue
+        g = torch.Generator(device="cuda").manual_seed(7)
+        xs_ = [torch.randn(rows, n, device="cuda", generator=g) for _ in range(max(2, ROTATE_BYTES // (rows * n * 4)))]
+        nr = len(xs_)
+        if name.startswith("add"):
+            r_ = torch.randn(rows, n, device="cuda", generator=g)
+            w_ = torch.rand(n, device="cuda", generator=g) + 0.5
+            y_ = torch.empty(rows, n, device="cuda")
+            fn, args_ = enc._lib.okf_add_rmsnorm_batch, (r_.data_ptr(), w_.data_ptr(), y_.data_ptr())
+            nbytes = (5 * rows + 1) * n * 4
+
+            def call(i, xs_=xs_, nr=nr):
+                if fn(enc.h, xs_[i % nr].data_ptr(), *args_, n, rows, ctypes.c_float(1e-6)):
+                    raise RuntimeError("okf_add_rmsnorm_batch failed")
+        else:
+            o_ = torch.empty(rows, dtype=torch.int32, device="cuda")
+            nbytes = rows * n * 4
+
+            def call(i, xs_=xs_, nr=nr):
+                if enc._lib.okf_argmax_rows(enc.h, xs_[i % nr].data_ptr(), n, rows, o_.data_ptr()):
+                    raise RuntimeError("okf_argmax_rows failed")
+        mean_s, best_s = time_calls(call, args.steps, max(3, args.warmup // 2))
+        rec = {"name": name, "us": round(mean_s * 1e6, 3), "us_best": round(best_s * 1e6, 3),
+               "bytes": nbytes, "GBps": round(nbytes / mean_s / 1e9, 1), "bound": "hbm",
+               "frac": round(nbytes / mean_s / HBM_PEAK, 4)}
+        log("bench:", json.dumps(rec))
+        suite.append(rec)
+        del xs_
 
     # ----------------------------------------------------------- CPU baseline
     cpu = None

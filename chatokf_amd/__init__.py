@@ -27,7 +27,7 @@ LIB_PATH = os.environ.get("OKF_LIB") or os.path.join(HERE, "libokf_quant.so")
 EXPORTS = (
     "okf_ctx_create", "okf_ctx_destroy", "okf_ctx_stream", "okf_row_bytes",
     "okf_gemv", "okf_gemv_silu", "okf_silu_mul", "okf_gemm", "okf_gemm_tile", "okf_dequant_row",
-    "okf_embed_batch",
+    "okf_embed_batch", "okf_add_rmsnorm_batch", "okf_argmax_rows",
     "okf_parallel_begin",
     "okf_parallel_end", "okf_sync", "okf_set_fault_rate", "okf_last_hip_error", "okf_strerror",
     "okf_gguf_open", "okf_gguf_close", "okf_gguf_tensor_count", "okf_gguf_tensor_at", "okf_gguf_find",
@@ -90,6 +90,8 @@ def _lib():
             "okf_gemm_tile": [vp, W, vp, u32, vp],
             "okf_dequant_row": [vp, W, u32, vp],
             "okf_embed_batch": [vp, W, vp, u32, vp],
+            "okf_add_rmsnorm_batch": [vp, vp, vp, vp, vp, u32, u32, ctypes.c_float],
+            "okf_argmax_rows": [vp, vp, u32, u32, vp],
             "okf_parallel_begin": [vp],
             "okf_parallel_end": [vp],
             "okf_sync": [vp],
@@ -246,6 +248,17 @@ class Enc:
         wc = w.c()
         self._check(self._lib.okf_embed_batch(self.h, ctypes.byref(wc), _ptr(ids), int(N), _ptr(out)),
                     "okf_embed_batch")
+
+    def add_rmsnorm(self, x, r, w, y, n: int, rows: int, eps: float):
+        """x += r; y = rmsnorm(x) * w per row (MetalEnc.addRmsnormBatch);
+        r = None is MetalEnc.rmsnormBatch."""
+        self._check(self._lib.okf_add_rmsnorm_batch(self.h, _ptr(x), _ptr(r), _ptr(w), _ptr(y), int(n),
+                                                    int(rows), float(eps)), "okf_add_rmsnorm_batch")
+
+    def argmax_rows(self, x, n: int, rows: int, out):
+        """out[row] = argmax of row (MetalEnc.argmaxRows)."""
+        self._check(self._lib.okf_argmax_rows(self.h, _ptr(x), int(n), int(rows), _ptr(out)),
+                    "okf_argmax_rows")
 
     def sync(self):
         self._check(self._lib.okf_sync(self.h), "okf_sync")

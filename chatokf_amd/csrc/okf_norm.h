@@ -1,0 +1,160 @@
+// okf_norm.h -- the FFN path's two non-matvec neighbours: the residual add +
+// RMSNorm in front of the projections and the argmax over the lm_head output
+// behind them.  Both are HBM-streaming row reductions.
+#pragma once
+#include "okf_common.h"
+
+namespace okf {
+
+constexpr int NORM_THREADS = 256;
+
+// Sum over a workgroup of NORM_THREADS threads (every thread gets it):
+// the wavefront's 64 lanes with cross-lane adds, then the 4 wavefront sums
+// through LDS in wavefront order.
+__device__ __forceinline__ float block_sum(float v, float *red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    const uint32_t w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    const float s = (red[0] + red[1]) + (red[2] + red[3]);
+    __syncthreads();  // red is reused by the next call
+    return s;
+}
+
+// add_rmsnorm_batch (LLM/metal/Kernels.metal:2839-2862) and, with R null,
+// rmsnorm_batch (:2818-2836): per row, x += r (stored back), then
+// y = x * (1 / sqrt(mean(x^2) + eps)) * w, with w fp32 (llama.cpp's
+// build_norm: the stored weight multiplies directly).  One workgroup per
+// row; a row is read once into registers when it fits (n <= 4 * 256 * 8),
+// else read twice.
+template <bool ADD>
+__global__ __launch_bounds__(NORM_THREADS) void add_rmsnorm_kernel(float *X,
+                                                                   const float *__restrict__ R,
+                                                                   const float *__restrict__ Wn,
+                                                                   float *Y, uint32_t n,
+                                                                   float eps) {
+    __shared__ float red[4];
+    const uint64_t row = blockIdx.x;
+    float *x = X + row * n;
+    const float *r = R + (ADD ? row * n : 0);
+    float *y = Y + row * n;
+    const uint32_t tid = threadIdx.x;
+    constexpr uint32_t V = 8;  // float4 per thread kept in registers
+    const uint32_t n4 = n / 4;
+    floatx4 v[V];
+    float ss = 0;
+    const bool vec = (n % 4) == 0 && n4 <= V * NORM_THREADS &&
+                     (((uintptr_t)X | (uintptr_t)R | (uintptr_t)Wn | (uintptr_t)Y) & 15) == 0;
+    if (vec) {
+#pragma unroll
+        for (uint32_t k = 0; k < V; k++) {
+            const uint32_t i = tid + k * NORM_THREADS;
+            if (i < n4) {
+                floatx4 a = ((const floatx4 *)x)[i];
+                if constexpr (ADD) {
+                    a += ((const floatx4 *)r)[i];
+                    ((floatx4 *)x)[i] = a;
+                }
+                v[k] = a;
+                ss += a[0] * a[0] + a[1] * a[1] + a[2] * a[2] + a[3] * a[3];
+            }
+        }
+    } else {
+        for (uint32_t i = tid; i < n; i += NORM_THREADS) {
+            float a = x[i];
+            if constexpr (ADD) {
+                a += r[i];
+                x[i] = a;
+            }
+            ss += a * a;
+        }
+    }
+    const float scale = 1.0f / sqrtf(block_sum(ss, red) / (float)n + eps);
+    if (vec) {
+#pragma unroll
+        for (uint32_t k = 0; k < V; k++) {
+            const uint32_t i = tid + k * NORM_THREADS;
+            if (i < n4) ((floatx4 *)y)[i] = v[k] * scale * ((const floatx4 *)Wn)[i];
+        }
+    } else {
+        // (each thread re-reads only the elements it wrote itself)
+        for (uint32_t i = tid; i < n; i += NORM_THREADS) y[i] = x[i] * scale * Wn[i];
+    }
+}
+
+// argmax_rows (LLM/metal/Kernels.metal:2756-2795): per row the index of the
+// largest value, ties to the lower index; NaN never wins, and a row with no
+// value above -inf gives 0 (the kernel's start, bv = -inf, bi = 0).
+//
+// A 248320-wide vocabulary row is 1 MB, so one row is split over many
+// workgroups: stage 1 reduces ARGMAX_CHUNK values per workgroup to a
+// (value, index) pair, stage 2 reduces a row's pairs in chunk order.
+constexpr uint32_t ARGMAX_CHUNK = NORM_THREADS * 4;  // one float4 per thread: ~240 workgroups per row
+
+struct ArgPair {
+    float v;
+    int32_t i;
+};
+
+__device__ __forceinline__ void arg_take(float &bv, int32_t &bi, float ov, int32_t oi) {
+    if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+    }
+}
+
+__device__ __forceinline__ void block_argmax(float &bv, int32_t &bi, ArgPair *red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) arg_take(bv, bi, __shfl_xor(bv, o), __shfl_xor(bi, o));
+    const uint32_t w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[w] = ArgPair{bv, bi};
+    __syncthreads();
+    bv = red[0].v;
+    bi = red[0].i;
+    for (int k = 1; k < NORM_THREADS / 64; k++) arg_take(bv, bi, red[k].v, red[k].i);
+}
+
+// grid (chunks, rows): pairs[row * chunks + chunk]
+__global__ __launch_bounds__(NORM_THREADS) void argmax_chunk_kernel(const float *__restrict__ X, uint32_t n,
+                                                                    ArgPair *__restrict__ pairs) {
+    __shared__ ArgPair red[NORM_THREADS / 64];
+    const uint32_t c = blockIdx.x, chunks = gridDim.x;
+    const float *x = X + (uint64_t)blockIdx.y * n;
+    const uint32_t b = c * ARGMAX_CHUNK, e = min(b + ARGMAX_CHUNK, n);
+    float bv = -__builtin_inff();
+    int32_t bi = 0;
+    if ((n & 3) == 0 && ((uintptr_t)X & 15) == 0) {
+        // float4 loads: thread t takes quads t, t + 256, ... of the chunk
+        for (uint32_t i = b + 4 * threadIdx.x; i < e; i += 4 * NORM_THREADS) {
+            const floatx4 q = *(const floatx4 *)(x + i);
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                if (q[k] > bv) {  // (in index order: a tie keeps the first)
+                    bv = q[k];
+                    bi = (int32_t)(i + k);
+                }
+        }
+    } else {
+        for (uint32_t i = b + threadIdx.x; i < e; i += NORM_THREADS)
+            if (x[i] > bv) {
+                bv = x[i];
+                bi = (int32_t)i;
+            }
+    }
+    block_argmax(bv, bi, red);
+    if (threadIdx.x == 0) pairs[(uint64_t)blockIdx.y * chunks + c] = ArgPair{bv, bi};
+}
+
+__global__ __launch_bounds__(NORM_THREADS) void argmax_final_kernel(const ArgPair *__restrict__ pairs,
+                                                                    uint32_t chunks, int32_t *__restrict__ out) {
+    __shared__ ArgPair red[NORM_THREADS / 64];
+    const ArgPair *p = pairs + (uint64_t)blockIdx.x * chunks;
+    float bv = -__builtin_inff();
+    int32_t bi = 0;
+    for (uint32_t c = threadIdx.x; c < chunks; c += NORM_THREADS) arg_take(bv, bi, p[c].v, p[c].i);
+    block_argmax(bv, bi, red);
+    if (threadIdx.x == 0) out[blockIdx.x] = bi;
+}
+
+}  // namespace okf

@@ -23,6 +23,7 @@
 #include "okf_gemv.h"
 #include "okf_gemv_wide.h"
 #include "okf_gguf.h"
+#include "okf_norm.h"
 
 #include "iq2xxs_grid.inc"
 
@@ -299,6 +300,21 @@ void launch_gemv(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32_t
     }
 }
 
+// The context's scratch (split-tile partial sums, argmax pairs), grown to at
+// least `need` bytes; the stream is drained before an old buffer is freed.
+int grow_part(okf_ctx *c, size_t need) {
+    if (need <= c->part_bytes) return OKF_OK;
+    hipError_t e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) return hip_fail(c, e);
+    if (c->part) (void)hipFree(c->part);
+    c->part = nullptr;
+    c->part_bytes = 0;
+    e = hipMalloc((void **)&c->part, need);
+    if (e != hipSuccess) return hip_fail(c, e);
+    c->part_bytes = need;
+    return OKF_OK;
+}
+
 template <int F>
 int launch_gemm(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t M, const float *X,
                 uint32_t N, float *Y) {
@@ -337,17 +353,8 @@ int launch_gemm(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t 
         sp.units = sp.ks > 1 ? rem * sp.ks : 0;
         sp.units_xcd = (sp.units + 7) / 8;
         if (sp.units) {
-            const size_t pb = (size_t)sp.units * QG_BM * QG_BN * sizeof(float);
-            if (pb > c->part_bytes) {
-                hipError_t e = hipStreamSynchronize(c->stream);
-                if (e != hipSuccess) return hip_fail(c, e);
-                if (c->part) (void)hipFree(c->part);
-                c->part = nullptr;
-                c->part_bytes = 0;
-                e = hipMalloc((void **)&c->part, pb);
-                if (e != hipSuccess) return hip_fail(c, e);
-                c->part_bytes = pb;
-            }
+            const int st = grow_part(c, (size_t)sp.units * QG_BM * QG_BN * sizeof(float));
+            if (st) return st;
             sp.part = c->part;
         }
         const uint32_t grid = 8 * (sp.full_xcd + sp.units_xcd);
@@ -557,6 +564,34 @@ int okf_silu_mul(okf_ctx *c, float *a, const float *b, uint32_t n) {
     int st = begin(c);
     if (st) return st;
     hipLaunchKernelGGL(silu_mul_kernel, dim3((n + 255) / 256), dim3(256), 0, c->stream, a, b, n);
+    return finish(c);
+}
+
+int okf_add_rmsnorm_batch(okf_ctx *c, float *x, const float *r, const float *w, float *y, uint32_t n,
+                          uint32_t rows, float eps) {
+    if (!x || !w || !y) return OKF_E_ARG;
+    if (n == 0 || rows == 0) return OKF_E_SHAPE;
+    int st = begin(c);
+    if (st) return st;
+    if (r)
+        hipLaunchKernelGGL(add_rmsnorm_kernel<true>, dim3(rows), dim3(NORM_THREADS), 0, c->stream, x, r, w, y,
+                           n, eps);
+    else
+        hipLaunchKernelGGL(add_rmsnorm_kernel<false>, dim3(rows), dim3(NORM_THREADS), 0, c->stream, x, r, w,
+                           y, n, eps);
+    return finish(c);
+}
+
+int okf_argmax_rows(okf_ctx *c, const float *x, uint32_t n, uint32_t rows, int32_t *out) {
+    if (!x || !out) return OKF_E_ARG;
+    if (n == 0 || rows == 0 || n > 0x7FFFFFFFu || rows > 65535) return OKF_E_SHAPE;
+    int st = begin(c);
+    if (st) return st;
+    const uint32_t chunks = (n + ARGMAX_CHUNK - 1) / ARGMAX_CHUNK;
+    if ((st = grow_part(c, (size_t)chunks * rows * sizeof(ArgPair)))) return st;
+    ArgPair *pairs = (ArgPair *)c->part;
+    hipLaunchKernelGGL(argmax_chunk_kernel, dim3(chunks, rows), dim3(NORM_THREADS), 0, c->stream, x, n, pairs);
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(rows), dim3(NORM_THREADS), 0, c->stream, pairs, chunks, out);
     return finish(c);
 }
 

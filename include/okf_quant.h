@@ -119,6 +119,21 @@ int okf_dequant_row(okf_ctx *ctx, const okf_weight *row, uint32_t n, float *out)
 int okf_parallel_begin(okf_ctx *ctx);
 int okf_parallel_end(okf_ctx *ctx);
 
+/* MetalEnc.addRmsnormBatch (MetalEnc.swift:532-546; kernel add_rmsnorm_batch,
+ * LLM/metal/Kernels.metal:2839-2862): for each of `rows` rows of n values,
+ * x += r (written back to x), then y = x * w / sqrt(mean(x^2) + eps) with w
+ * n fp32 weights.  With r = NULL this is MetalEnc.rmsnormBatch
+ * (MetalEnc.swift:516-530, kernel rmsnorm_batch): x is only read.  All
+ * pointers are device memory, rows stored contiguously (stride n). */
+int okf_add_rmsnorm_batch(okf_ctx *ctx, float *x, const float *r, const float *w, float *y, uint32_t n,
+                          uint32_t rows, float eps);
+
+/* MetalEnc.argmaxRows (MetalEnc.swift:496-503; kernel argmax_rows,
+ * LLM/metal/Kernels.metal:2756-2795): out[row] = index of the largest of the
+ * row's n values, ties to the lower index; NaN never wins and a row with no
+ * value above -inf gives 0.  x and out are device memory; rows <= 65535. */
+int okf_argmax_rows(okf_ctx *ctx, const float *x, uint32_t n, uint32_t rows, int32_t *out);
+
 /* MetalEnc.embedBatch (MetalEnc.swift:1096-1146; kernels embed_batch,
  * q4_k_embed_batch, iq_embed_batch, LLM/metal/Kernels.metal:1444-1482):
  * out[n][K] = row ids[n] of w dequantized to fp32, n < N, bit-identical to

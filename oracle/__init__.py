@@ -41,6 +41,10 @@ def _lib():
         lib.okf_ref_usable_cores.argtypes = []
         lib.okf_ref_silu_mul.argtypes = [vp, vp, u32, vp]
         lib.okf_ref_silu_mul.restype = None
+        lib.okf_ref_add_rmsnorm.argtypes = [vp, vp, vp, vp, u32, u32, ctypes.c_float]
+        lib.okf_ref_add_rmsnorm.restype = None
+        lib.okf_ref_argmax_rows.argtypes = [vp, u32, u32, vp]
+        lib.okf_ref_argmax_rows.restype = None
         _LIB = lib
     return _LIB
 
@@ -77,6 +81,28 @@ def silu_mul(a: np.ndarray, b: np.ndarray) -> np.ndarray:
     assert a.size == b.size
     out = np.empty(a.size, np.float32)
     _lib().okf_ref_silu_mul(_p(a), _p(b), a.size, _p(out))
+    return out
+
+
+def add_rmsnorm(x: np.ndarray, r, w: np.ndarray, eps: float):
+    """(x + r, rmsnorm(x + r) * w) per row of x's last axis; r may be None."""
+    x = np.array(x, np.float32, order="C", copy=True)
+    n = x.shape[-1]
+    rows = x.size // n
+    rr = None if r is None else np.ascontiguousarray(r, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    assert w.size == n and (rr is None or rr.size == x.size)
+    y = np.empty_like(x)
+    _lib().okf_ref_add_rmsnorm(_p(x), None if rr is None else _p(rr), _p(w), _p(y), n, rows, eps)
+    return x, y
+
+
+def argmax_rows(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    n = x.shape[-1]
+    rows = x.size // n
+    out = np.empty(rows, np.int32)
+    _lib().okf_ref_argmax_rows(_p(x), n, rows, _p(out))
     return out
 
 

@@ -419,6 +419,38 @@ int okf_ref_matmul(int32_t type, const uint8_t *w, uint32_t K, uint32_t M,
     return 0;
 }
 
+/* Kern.rmsnorm, LLM/Base/Kernels.swift:12-20, after the residual add of
+ * add_rmsnorm_batch (LLM/metal/Kernels.metal:2850-2854) */
+void okf_ref_add_rmsnorm(float *x, const float *r, const float *w, float *y, uint32_t n, uint32_t rows,
+                         float eps) {
+    for (uint32_t row = 0; row < rows; row++) {
+        float *xr = x + (uint64_t)row * n, *yr = y + (uint64_t)row * n;
+        float ss = 0;
+        for (uint32_t i = 0; i < n; i++) {
+            if (r) xr[i] += r[(uint64_t)row * n + i];
+            ss += xr[i] * xr[i];
+        }
+        const float scale = 1.0f / sqrtf(ss / (float)n + eps);
+        for (uint32_t i = 0; i < n; i++) yr[i] = xr[i] * scale * w[i];
+    }
+}
+
+/* argmax_rows, LLM/metal/Kernels.metal:2766-2772: bv = -inf, bi = 0, take a
+ * strictly larger value (so ties keep the lower index and NaN never wins) */
+void okf_ref_argmax_rows(const float *x, uint32_t n, uint32_t rows, int32_t *out) {
+    for (uint32_t row = 0; row < rows; row++) {
+        const float *xr = x + (uint64_t)row * n;
+        float bv = -INFINITY;
+        int32_t bi = 0;
+        for (uint32_t i = 0; i < n; i++)
+            if (xr[i] > bv) {
+                bv = xr[i];
+                bi = (int32_t)i;
+            }
+        out[row] = bi;
+    }
+}
+
 /* Swift silu, LLM/Base/Kernels.swift:3: x / (1 + expf(-x)); then times b. */
 void okf_ref_silu_mul(const float *a, const float *b, uint32_t n, float *out) {
     for (uint32_t i = 0; i < n; i++) {

@@ -69,6 +69,19 @@ int okf_ref_usable_cores(void);
  * (LLM/metal/Kernels.metal:7, :3280-3285). */
 void okf_ref_silu_mul(const float *a, const float *b, uint32_t n, float *out);
 
+/* Per row of n: x += r (r may be NULL: no add), then
+ * y = x * (1 / sqrt(sum(x^2) / n + eps)) * w, sequential fp32 sum, as
+ * Kern.rmsnorm (LLM/Base/Kernels.swift:12-20) applied to the residual sum
+ * that add_rmsnorm_batch forms (LLM/metal/Kernels.metal:2839-2862). */
+void okf_ref_add_rmsnorm(float *x, const float *r, const float *w, float *y, uint32_t n, uint32_t rows,
+                         float eps);
+
+/* Per row of n: the index of the largest value, ties to the lower index, NaN
+ * skipped, 0 when nothing exceeds -inf (argmax_rows,
+ * LLM/metal/Kernels.metal:2756-2795; Vectors.argmax,
+ * LLM/Base/Vectors.swift:11-18, scans the same way from a finite floor). */
+void okf_ref_argmax_rows(const float *x, uint32_t n, uint32_t rows, int32_t *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -74,6 +74,23 @@ def test_detached_context_validates_then_reports_nodev(detached):
     assert e.value.status == ok.OKF_E_SHAPE
 
 
+def test_norm_and_argmax_validate_then_report_nodev(detached):
+    cases = [
+        (lambda: detached.add_rmsnorm(FAKE, FAKE, FAKE, FAKE, 2048, 1, 1e-6), ok.OKF_E_NODEV),
+        (lambda: detached.add_rmsnorm(FAKE, None, FAKE, FAKE, 2048, 1, 1e-6), ok.OKF_E_NODEV),
+        (lambda: detached.add_rmsnorm(None, FAKE, FAKE, FAKE, 2048, 1, 1e-6), ok.OKF_E_ARG),
+        (lambda: detached.add_rmsnorm(FAKE, FAKE, FAKE, FAKE, 0, 1, 1e-6), ok.OKF_E_SHAPE),
+        (lambda: detached.argmax_rows(FAKE, 248320, 1, FAKE), ok.OKF_E_NODEV),
+        (lambda: detached.argmax_rows(FAKE, 0, 1, FAKE), ok.OKF_E_SHAPE),
+        (lambda: detached.argmax_rows(FAKE, 16, 65536, FAKE), ok.OKF_E_SHAPE),
+        (lambda: detached.argmax_rows(None, 16, 1, FAKE), ok.OKF_E_ARG),
+    ]
+    for call, status in cases:
+        with pytest.raises(ok.OkfError) as e:
+            call()
+        assert e.value.status == status
+
+
 def test_fault_injection_is_seeded(detached):
     # GPUGate.simulate analogue (LLM/Base/MetalGates.swift:101-108): with a
     # rate the calls fail with OKF_E_INJECTED, deterministically per seed.

@@ -213,6 +213,56 @@ def test_wide_matches_oracle_and_default(enc, enc_wide, t, M, K, N):
     assert rel(got, run_gemm(enc, t, M, K, w, X).astype(np.float64)) <= 1e-5
 
 
+# ---------------------------------------------- add + RMSNorm, argmax
+# n: vector path (multiple of 4, <= 8192), scalar paths (odd n, n > 8192, a
+# pointer off 16-byte alignment); rows as decode (1) and MTP verify (5)
+NORM = [(2048, 1, 0), (5120, 5, 0), (6144, 3, 0), (10000, 2, 0), (1001, 3, 0), (2048, 2, 1)]
+
+
+@pytest.mark.parametrize("n,rows,skew", NORM)
+@pytest.mark.parametrize("add", [True, False], ids=["add", "plain"])
+def test_add_rmsnorm_matches_oracle(enc, n, rows, skew, add):
+    say("add_rmsnorm", n, rows, skew, add)
+    rng = np.random.default_rng(n + rows)
+    x = rng.standard_normal((rows, n)).astype(np.float32) * 4
+    r = rng.standard_normal((rows, n)).astype(np.float32) if add else None
+    w = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    xs, ref = oracle.add_rmsnorm(x, r, w, 1e-6)
+    buf = torch.zeros(rows * n + skew, device="cuda")
+    xd = buf[skew:].view(rows, n)
+    xd.copy_(dev(x))
+    yd = torch.full((rows, n), float("nan"), device="cuda")
+    enc.add_rmsnorm(xd, None if r is None else dev(r), dev(w), yd, n, rows, 1e-6)
+    got_x, got_y = host(xd), host(yd)
+    assert np.array_equal(got_x, xs)  # one fp32 add per element (or untouched)
+    assert np.abs(got_y - ref).max() <= 1e-5 * np.abs(ref).max()  # summation order only
+
+
+ARGMAX = [(248320, 1, 0), (248320, 5, 0), (1, 1, 0), (1003, 3, 0), (8192 * 3 + 5, 2, 1), (100000, 4, 0)]
+
+
+@pytest.mark.parametrize("n,rows,skew", ARGMAX)
+def test_argmax_rows_matches_oracle(enc, n, rows, skew):
+    say("argmax", n, rows, skew)
+    rng = np.random.default_rng(n * 7 + rows)
+    x = rng.standard_normal((rows, n)).astype(np.float32)
+    if n > 16:
+        x[0, n // 3] = x[0, n - 2] = 9.0  # a tie across chunks: the lower index wins
+        x[0, 5] = np.nan
+    if rows > 1:
+        x[1, :] = np.nan  # nothing wins: 0
+    if rows > 2:
+        x[2, :] = -np.inf
+        x[2, n - 1] = -1e30
+    ref = oracle.argmax_rows(x)
+    buf = torch.zeros(rows * n + skew, device="cuda")
+    xd = buf[skew:].view(rows, n)
+    xd.copy_(dev(x))
+    out = torch.full((rows,), -7, dtype=torch.int32, device="cuda")
+    enc.argmax_rows(xd, n, rows, out)
+    assert np.array_equal(host(out), ref)
+
+
 # ------------------------------------------------------------ SiLU-gated FFN
 def test_silu_mul_matches_oracle(enc):
     a = np.random.default_rng(4).standard_normal(6144).astype(np.float32) * 3

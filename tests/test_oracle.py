@@ -296,6 +296,44 @@ def test_silu_mul_known_values_and_float64():
     assert np.allclose(oracle.silu_mul(x, y), x64 / (1 + np.exp(-x64)) * y, rtol=1e-6, atol=1e-7)
 
 
+def test_add_rmsnorm_closed_forms():
+    # a constant row c with eps = 0 normalizes to exactly 1 (c / sqrt(c^2))
+    x = np.full((2, 64), 3.0, np.float32)
+    xs, y = oracle.add_rmsnorm(x, None, np.ones(64, np.float32), 0.0)
+    assert np.array_equal(xs, x) and np.array_equal(y, np.ones((2, 64), np.float32))
+    # residual add is one fp32 add per element; the norm matches float64
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((5, 2048)).astype(np.float32)
+    r = rng.standard_normal((5, 2048)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, 2048).astype(np.float32)
+    xs, y = oracle.add_rmsnorm(x, r, w, 1e-6)
+    assert np.array_equal(xs, x + r)
+    s = (x + r).astype(np.float64)
+    ref = s / np.sqrt((s * s).mean(axis=1, keepdims=True) + 1e-6) * w
+    assert np.abs(y - ref).max() <= 1e-5 * np.abs(ref).max()
+    # scale invariance with eps = 0: rmsnorm(2x) == rmsnorm(x)
+    _, y1 = oracle.add_rmsnorm(x, None, w, 0.0)
+    _, y2 = oracle.add_rmsnorm(2 * x, None, w, 0.0)
+    assert np.allclose(y1, y2, rtol=1e-6, atol=0)
+
+
+def _argmax_ref(x):
+    # numpy's argmax takes the first maximum; NaN never wins, a row with
+    # nothing above -inf gives 0
+    z = np.where(np.isnan(x), -np.inf, x)
+    return np.argmax(z, axis=-1).astype(np.int32)
+
+
+def test_argmax_rows_ties_nan_and_brute_force():
+    x = np.array([[1, 3, 3, 2], [np.nan, 5, np.nan, 5], [np.nan] * 4, [-np.inf] * 4, [0, -np.inf, np.nan, 0]],
+                 np.float32)
+    assert oracle.argmax_rows(x).tolist() == [1, 1, 0, 0, 0]
+    rng = np.random.default_rng(4)
+    x = rng.integers(-50, 50, (7, 1000)).astype(np.float32)  # many ties
+    x[2, ::7] = np.nan
+    assert np.array_equal(oracle.argmax_rows(x), _argmax_ref(x))
+
+
 def test_q4_0_and_iq4_nl_known_answer():
     # d = 1: byte j holds codes for weights j (low nibble) and j + 16 (high)
     d = np.array([1.0], np.float16).view(np.uint8)
