@@ -5,12 +5,14 @@
 
 namespace okf {
 
-enum Fmt : int { Q4_0 = 2, Q8_0 = 8, Q4_K = 12, IQ2_XXS = 16, IQ4_NL = 20, Q2_0 = 42 };
+enum Fmt : int { Q4_0 = 2, Q8_0 = 8, Q4_K = 12, Q5_K = 13, Q6_K = 14, IQ2_XXS = 16, IQ4_NL = 20, IQ4_XS = 23,
+                 Q2_0 = 42 };
 
 // Bytes of one 256-weight span (Q8_0: 8 blocks, Q2_0: 2 blocks), matching the
 // reference's IQArgs.blk (LLM/Base/MetalEnc.swift:162-167).
 __host__ __device__ constexpr uint32_t block_bytes(int f) {
-    return f == Q8_0 ? 34 : f == Q2_0 ? 34 : f == Q4_K ? 144 : (f == Q4_0 || f == IQ4_NL) ? 18 : 66;
+    return f == Q8_0 ? 34 : f == Q2_0 ? 34 : f == Q4_K ? 144 : (f == Q4_0 || f == IQ4_NL) ? 18
+         : f == Q5_K ? 176 : f == Q6_K ? 210 : f == IQ4_XS ? 136 : 66;
 }
 __host__ __device__ constexpr uint32_t block_elems(int f) {
     return (f == Q8_0 || f == Q4_0 || f == IQ4_NL) ? 32 : f == Q2_0 ? 128 : 256;

@@ -135,6 +135,78 @@ __device__ __forceinline__ void decode_unit_iq4_nl(const uint8_t *row, uint32_t 
     }
 }
 
+// KQuant.q5K, LLM/Quantize/KQuants.swift:127-155, sub-block j = u & 7 of
+// superblock u >> 3: code group g = j >> 1 (bytes 48 + 32 g ..), low
+// nibbles for even j, high for odd; the fifth bit is bit j of qh[l] (bytes
+// 16..47); w = (d * sc) * Float(q) - dmin * m.
+__device__ __forceinline__ void decode_unit_q5_k(const uint8_t *row, uint32_t u, float *w) {
+    const uint8_t *b = row + (uint64_t)(u >> 3) * 176;
+    const uint4 hdr = ldu<uint4>(b);
+    const uint32_t j = u & 7, g = j >> 1, hi = j & 1;
+    uint32_t sc, mn;
+    q4k_scale_min(hdr.y, hdr.z, hdr.w, j, sc, mn);
+    const float d = h2f(hdr.x & 0xFFFF), dmin = h2f(hdr.x >> 16);
+    const float d1 = d * (float)sc, o1 = dmin * (float)mn;
+    uint32_t q[8], h[8];
+    *(uint4 *)&q[0] = ldu<uint4>(b + 48 + g * 32);
+    *(uint4 *)&q[4] = ldu<uint4>(b + 64 + g * 32);
+    *(uint4 *)&h[0] = ldu<uint4>(b + 16);
+    *(uint4 *)&h[4] = ldu<uint4>(b + 32);
+#pragma unroll
+    for (int l = 0; l < 32; l++) {
+        const uint32_t nib = (byte_of(q[l >> 2], l & 3) >> (hi * 4)) & 0xF;
+        const uint32_t hb = (byte_of(h[l >> 2], l & 3) >> j) & 1;
+        w[l] = d1 * (float)(nib + 16 * hb) - o1;
+    }
+}
+
+// KQuant.q6K, LLM/Quantize/KQuants.swift:157-176, 32-weight group u & 7 =
+// (n, r) of superblock u >> 3: weight n*128 + r*32 + l is the low (r < 2) or
+// high nibble of ql[n*64 + l] (r even) or ql[n*64 + 32 + l] (r odd), with
+// bits 2r, 2r + 1 of qh[n*32 + l] on top; w = d * Float(s) * Float(q - 32),
+// s = int8 scales[n*8 + 2r + l/16], d at byte 208.
+__device__ __forceinline__ void decode_unit_q6_k(const uint8_t *row, uint32_t u, float *w) {
+    const uint8_t *b = row + (uint64_t)(u >> 3) * 210;
+    const uint32_t n = (u >> 2) & 1, r = u & 3;
+    const float d = h2f(ldu<uint16_t>(b + 208));
+    uint32_t q[8], h[8];
+    const uint8_t *qb = b + n * 64 + (r & 1) * 32;
+    *(uint4 *)&q[0] = ldu<uint4>(qb);
+    *(uint4 *)&q[4] = ldu<uint4>(qb + 16);
+    *(uint4 *)&h[0] = ldu<uint4>(b + 128 + n * 32);
+    *(uint4 *)&h[4] = ldu<uint4>(b + 144 + n * 32);
+    const uint2 sc2 = make_uint2(byte_of(ldu<uint16_t>(b + 192 + n * 8 + 2 * r), 0),
+                                 byte_of(ldu<uint16_t>(b + 192 + n * 8 + 2 * r), 1));
+#pragma unroll
+    for (int l = 0; l < 32; l++) {
+        const uint32_t nib = (byte_of(q[l >> 2], l & 3) >> ((r >> 1) * 4)) & 0xF;
+        const uint32_t hb = (byte_of(h[l >> 2], l & 3) >> (2 * r)) & 3;
+        const int s = (int8_t)(l < 16 ? sc2.x : sc2.y);
+        w[l] = d * (float)s * (float)((int)(nib | (hb << 4)) - 32);
+    }
+}
+
+// IQX.iq4XS, LLM/Quantize/IQ3.swift:118-133, sub-block ib = u & 7 of
+// superblock u >> 3: ls = (nibble ib of scales_l) | (bits 2 ib of scales_h)
+// << 4, dl = d * Float(ls - 32), w = dl * level(nibble) with the IQ4_NL
+// levels, low nibbles of qs[ib*16 + j] for j < 16, high for j + 16.
+__device__ __forceinline__ void decode_unit_iq4_xs(const uint8_t *row, uint32_t u, float *w) {
+    const uint8_t *b = row + (uint64_t)(u >> 3) * 136;
+    const uint32_t ib = u & 7;
+    const float d = h2f(ldu<uint16_t>(b));
+    const uint32_t sh = ldu<uint16_t>(b + 2), sl = b[4 + ib / 2];
+    const int ls = (int)(((sl >> (4 * (ib & 1))) & 0xF) | (((sh >> (2 * ib)) & 3) << 4));
+    const float dl = d * (float)(ls - 32);
+    uint32_t q[4];
+    *(uint4 *)&q[0] = ldu<uint4>(b + 8 + ib * 16);
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const uint32_t v = byte_of(q[j >> 2], j & 3);
+        w[j] = dl * (float)iq4nl_level(v & 15);
+        w[j + 16] = dl * (float)iq4nl_level(v >> 4);
+    }
+}
+
 template <int F>
 __device__ __forceinline__ void decode_unit(const uint8_t *row, uint32_t u, float *w,
                                             const uint2 *grid) {
@@ -143,6 +215,9 @@ __device__ __forceinline__ void decode_unit(const uint8_t *row, uint32_t u, floa
     else if constexpr (F == Q4_K) decode_unit_q4_k(row, u, w);
     else if constexpr (F == Q4_0) decode_unit_q4_0(row, u, w);
     else if constexpr (F == IQ4_NL) decode_unit_iq4_nl(row, u, w);
+    else if constexpr (F == Q5_K) decode_unit_q5_k(row, u, w);
+    else if constexpr (F == Q6_K) decode_unit_q6_k(row, u, w);
+    else if constexpr (F == IQ4_XS) decode_unit_iq4_xs(row, u, w);
     else decode_unit_iq2_xxs(row, u, w, grid);
 }
 

@@ -33,7 +33,7 @@ namespace okf {
 // any K that is a whole number of blocks works).
 template <int F>
 __host__ __device__ constexpr uint32_t unit_weights() {
-    return (F == Q8_0 || F == Q4_0 || F == IQ4_NL) ? 32 : 64;
+    return (F == Q8_0 || F == Q4_0 || F == IQ4_NL || F == Q6_K) ? 32 : 64;
 }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -96,6 +96,21 @@ struct Unit<IQ4_NL, R> {  // as Q4_0
     u32x4 q[R];
 };
 
+template <int R>
+struct Unit<Q5_K, R> {  // header, the 32 qh bytes, 32 code bytes of group g
+    u32x4 hdr[R], h0[R], h1[R], q0[R], q1[R];
+};
+template <int R>
+struct Unit<Q6_K, R> {  // d, the two scales, 32 ql bytes, 32 qh bytes
+    uint32_t d[R], sc[R];
+    u32x4 q0[R], q1[R], h0[R], h1[R];
+};
+template <int R>
+struct Unit<IQ4_XS, R> {  // d, scales_h, scales_l (8 bytes) + 32 code bytes of sub-blocks 2g, 2g + 1
+    uint2 hdr[R];
+    u32x4 q0[R], q1[R];
+};
+
 template <int F, int R>
 __device__ __forceinline__ void load_unit(const uint8_t *const rows[R], uint32_t u, Unit<F, R> &w) {
 #pragma unroll
@@ -115,6 +130,29 @@ __device__ __forceinline__ void load_unit(const uint8_t *const rows[R], uint32_t
             w.d[r] = ldu<uint16_t>(b);
             w.q0[r] = ldu<u32x4>(b + 2);
             w.q1[r] = ldu<u32x4>(b + 18);
+        } else if constexpr (F == Q5_K) {  // unit = code group g of superblock u >> 2
+            const uint8_t *b = rows[r] + (uint64_t)(u >> 2) * 176;
+            const uint32_t g = u & 3;
+            w.hdr[r] = ldu<u32x4>(b);
+            w.h0[r] = ldu<u32x4>(b + 16);
+            w.h1[r] = ldu<u32x4>(b + 32);
+            w.q0[r] = ldu<u32x4>(b + 48 + g * 32);
+            w.q1[r] = ldu<u32x4>(b + 64 + g * 32);
+        } else if constexpr (F == Q6_K) {  // unit = 32 weights (n, r) of superblock u >> 3
+            const uint8_t *b = rows[r] + (uint64_t)(u >> 3) * 210;
+            const uint32_t n = (u >> 2) & 1, rr = u & 3;
+            w.d[r] = ldu<uint16_t>(b + 208);
+            w.sc[r] = ldu<uint16_t>(b + 192 + n * 8 + 2 * rr);
+            w.q0[r] = ldu<u32x4>(b + n * 64 + (rr & 1) * 32);
+            w.q1[r] = ldu<u32x4>(b + n * 64 + (rr & 1) * 32 + 16);
+            w.h0[r] = ldu<u32x4>(b + 128 + n * 32);
+            w.h1[r] = ldu<u32x4>(b + 144 + n * 32);
+        } else if constexpr (F == IQ4_XS) {  // unit = sub-blocks 2g, 2g + 1 of superblock u >> 2
+            const uint8_t *b = rows[r] + (uint64_t)(u >> 2) * 136;
+            const uint32_t g = u & 3;
+            w.hdr[r] = ldu<uint2>(b);
+            w.q0[r] = ldu<u32x4>(b + 8 + g * 32);
+            w.q1[r] = ldu<u32x4>(b + 24 + g * 32);
         } else if constexpr (F == Q4_0 || F == IQ4_NL) {
             const uint8_t *b = rows[r] + (uint64_t)u * 18;
             w.d[r] = ldu<uint16_t>(b);
@@ -139,7 +177,10 @@ __device__ __forceinline__ void load_unit(const uint8_t *const rows[R], uint32_t
 //        A0 B0 A1 B1 A2 B2 A3 B3.
 //  Q4_0: as Q4_K with 16 code bytes: slots 0, 1 are the low nibbles
 //        (weights 0..15), slots 2, 3 the high ones (16..31).
-//  Q8_0, IQ2_XXS, IQ4_NL: natural order, A = x[8s..], B = x[8s+4..].
+//  Q5_K: as Q4_K (32 code bytes of one group: low nibbles, then high).
+//  Q6_K: as Q4_K within its 32 weights (code dword i gives pairs (4i, 4i+2),
+//        (4i+1, 4i+3)).
+//  Q8_0, IQ2_XXS, IQ4_NL, IQ4_XS: natural order, A = x[8s..], B = x[8s+4..].
 template <int F>
 __device__ __forceinline__ uint32_t slot_first(uint32_t s, uint32_t &second) {
     if constexpr (F == Q2_0) {
@@ -159,7 +200,7 @@ __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
 
 template <int F>
 __device__ __forceinline__ u32x4 slot_pack(floatx4 A, floatx4 B) {
-    if constexpr (F == Q4_K || F == Q4_0)
+    if constexpr (F == Q4_K || F == Q4_0 || F == Q5_K || F == Q6_K)
         return u32x4{pack_h2(A[0], A[2]), pack_h2(A[1], A[3]), pack_h2(B[0], B[2]),
                      pack_h2(B[1], B[3])};
     else if constexpr (F == Q2_0)
@@ -509,6 +550,188 @@ struct Compute<Q2_0, NC, R, TS> {
             // sum((code - 1) x) = sum((1024 + code) x) - 1025 sum(x)
 #pragma unroll
             for (int n = 0; n < NC; n++) acc[r][n] += d * (s[r][n] - 1025.0f * xsum[n]);
+        }
+    }
+};
+
+template <int NC, int R, int TS>
+struct Compute<Q5_K, NC, R, TS> {
+    // As Q4_K, with the fifth bit of weight l from qh byte l: bit 2g for the
+    // low nibbles (sub-block 2g), bit 2g + 1 for the high ones.  The 5-bit
+    // values become bytes, then fp16 1024 + q by v_bfi, so
+    // sum(q x) = sum((1024 + q) x) - 1024 sum(x).
+    __device__ __forceinline__ static void run(const Unit<Q5_K, R> &w, const uint32_t *xp, uint32_t ss, uint32_t cs,
+                                               const float *xsum, uint32_t xcs, uint32_t u,
+                                               float (&acc)[R][NC], const u32x4 *) {
+        const uint32_t g = u & 3;
+        float slo[R][NC], shi[R][NC];
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int n = 0; n < NC; n++) slo[r][n] = shi[r][n] = 0;
+#pragma unroll
+        for (int s = 0; s < 4; s++) {  // code dwords 2s, 2s + 1
+            u32x4 xl[NC], xh[NC];
+#pragma unroll
+            for (int n = 0; n < NC; n++) {
+                xl[n] = *(const u32x4 *)(xp + n * cs + s * ss);
+                xh[n] = *(const u32x4 *)(xp + n * cs + (4 + s) * ss);
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const int i = 2 * s + h;
+                    const uint32_t v = i < 4 ? w.q0[r][i] : w.q1[r][i - 4];
+                    const uint32_t hq = (i < 4 ? w.h0[r][i] : w.h1[r][i - 4]) >> (2 * g);
+                    const uint32_t lo = (v & 0x0F0F0F0Fu) | ((hq & 0x01010101u) << 4);
+                    const uint32_t hi = ((v >> 4) & 0x0F0F0F0Fu) | ((hq & 0x02020202u) << 3);
+                    const uint32_t l02 = bfi(0x001F001Fu, lo, MAGIC2), l13 = bfi(0x001F001Fu, lo >> 8, MAGIC2);
+                    const uint32_t h02 = bfi(0x001F001Fu, hi, MAGIC2), h13 = bfi(0x001F001Fu, hi >> 8, MAGIC2);
+#pragma unroll
+                    for (int n = 0; n < NC; n++) {
+                        slo[r][n] = dot2(l02, xl[n][2 * h], slo[r][n]);
+                        slo[r][n] = dot2(l13, xl[n][2 * h + 1], slo[r][n]);
+                        shi[r][n] = dot2(h02, xh[n][2 * h], shi[r][n]);
+                        shi[r][n] = dot2(h13, xh[n][2 * h + 1], shi[r][n]);
+                    }
+                }
+            }
+        }
+        float xlo[NC], xhi[NC];
+#pragma unroll
+        for (int n = 0; n < NC; n++) {
+            const float2 t = *(const float2 *)(xsum + n * xcs);
+            xlo[n] = t.x;
+            xhi[n] = t.y;
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            uint32_t sc0, mn0, sc1, mn1;
+            const uint4 hv = make_uint4(w.hdr[r][0], w.hdr[r][1], w.hdr[r][2], w.hdr[r][3]);
+            q4k_scale_min_pair(hv, g, sc0, mn0, sc1, mn1);
+            const float d = h2f(w.hdr[r][0] & 0xFFFF), dmin = h2f(w.hdr[r][0] >> 16);
+            const float a0 = d * (float)sc0, a1 = d * (float)sc1;
+            const float b0 = 1024.0f * a0 + dmin * (float)mn0, b1 = 1024.0f * a1 + dmin * (float)mn1;
+#pragma unroll
+            for (int n = 0; n < NC; n++)
+                acc[r][n] += (a0 * slo[r][n] + a1 * shi[r][n]) - (b0 * xlo[n] + b1 * xhi[n]);
+        }
+    }
+};
+
+template <int NC, int R, int TS>
+struct Compute<Q6_K, NC, R, TS> {
+    // Unit (n, r): the 6-bit q of weight l is nibble r >> 1 of ql byte l with
+    // bits 2r, 2r + 1 of qh byte l on top.  v_bfi makes fp16 1024 + q, one
+    // packed fp16 add makes it q - 32 (exact), and the two 16-weight halves
+    // take their own int8 scale: acc += d s0 sum_0..15 + d s1 sum_16..31.
+    __device__ __forceinline__ static void run(const Unit<Q6_K, R> &w, const uint32_t *xp, uint32_t ss, uint32_t cs,
+                                               const float *, uint32_t, uint32_t u, float (&acc)[R][NC],
+                                               const u32x4 *) {
+        const uint32_t rr = u & 3, shq = 4 * (rr >> 1), shh = 2 * rr;
+        const half2v bias = {(_Float16)-1056.0f, (_Float16)-1056.0f};
+        float s[2][R][NC];
+#pragma unroll
+        for (int p = 0; p < 2; p++)
+#pragma unroll
+            for (int r = 0; r < R; r++)
+#pragma unroll
+                for (int n = 0; n < NC; n++) s[p][r][n] = 0;
+#pragma unroll
+        for (int sl = 0; sl < 4; sl++) {  // code dwords 2 sl, 2 sl + 1 (weights 8 sl ..)
+            u32x4 xv[NC];
+#pragma unroll
+            for (int n = 0; n < NC; n++) xv[n] = *(const u32x4 *)(xp + n * cs + sl * ss);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const int i = 2 * sl + h;
+                    const uint32_t v = i < 4 ? w.q0[r][i] : w.q1[r][i - 4];
+                    const uint32_t hq = i < 4 ? w.h0[r][i] : w.h1[r][i - 4];
+                    const uint32_t q = ((v >> shq) & 0x0F0F0F0Fu) | (((hq >> shh) & 0x03030303u) << 4);
+                    const uint32_t p02 = __builtin_bit_cast(
+                        uint32_t, __builtin_bit_cast(half2v, bfi(0x003F003Fu, q, MAGIC2)) + bias);
+                    const uint32_t p13 = __builtin_bit_cast(
+                        uint32_t, __builtin_bit_cast(half2v, bfi(0x003F003Fu, q >> 8, MAGIC2)) + bias);
+#pragma unroll
+                    for (int n = 0; n < NC; n++) {
+                        s[sl >> 1][r][n] = dot2(p02, xv[n][2 * h], s[sl >> 1][r][n]);
+                        s[sl >> 1][r][n] = dot2(p13, xv[n][2 * h + 1], s[sl >> 1][r][n]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const float d = h2f(w.d[r]);
+            const float d0 = d * (float)(int8_t)(w.sc[r] & 0xFF), d1 = d * (float)(int8_t)(w.sc[r] >> 8);
+#pragma unroll
+            for (int n = 0; n < NC; n++) acc[r][n] += d0 * s[0][r][n] + d1 * s[1][r][n];
+        }
+    }
+};
+
+template <int NC, int R, int TS>
+struct Compute<IQ4_XS, NC, R, TS> {
+    // Two IQ4_NL-shaped sub-blocks (16 code bytes each) with their own
+    // 6-bit scales: dl = d (ls - 32), ls = nibble of scales_l byte g |
+    // 2 bits of scales_h << 4.
+    __device__ __forceinline__ static void run(const Unit<IQ4_XS, R> &w, const uint32_t *xp, uint32_t ss, uint32_t cs,
+                                               const float *xsp, uint32_t xcs, uint32_t u,
+                                               float (&acc)[R][NC], const u32x4 *) {
+        const uint32_t g = u & 3;
+        float xsum[2][NC], s[2][R][NC];
+#pragma unroll
+        for (int n = 0; n < NC; n++) {
+            const float2 t = *(const float2 *)(xsp + n * xcs);
+            xsum[0][n] = t.x;
+            xsum[1][n] = t.y;
+        }
+#pragma unroll
+        for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+            for (int r = 0; r < R; r++)
+#pragma unroll
+                for (int n = 0; n < NC; n++) s[sb][r][n] = 0;
+#pragma unroll
+        for (int sb = 0; sb < 2; sb++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {  // code dword i: weights 4i.. (low), 16 + 4i.. (high)
+                u32x4 xl[NC], xh[NC];
+#pragma unroll
+                for (int n = 0; n < NC; n++) {
+                    xl[n] = *(const u32x4 *)(xp + n * cs + (4 * sb + (i >> 1)) * ss);
+                    xh[n] = *(const u32x4 *)(xp + n * cs + (4 * sb + 2 + (i >> 1)) * ss);
+                }
+                const int e = 2 * (i & 1);
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const uint32_t v = sb == 0 ? w.q0[r][i] : w.q1[r][i];
+                    const uint32_t bl = Compute<IQ4_NL, NC, R, TS>::levels(v & 0x0F0F0F0Fu);
+                    const uint32_t bh = Compute<IQ4_NL, NC, R, TS>::levels((v >> 4) & 0x0F0F0F0Fu);
+                    const uint32_t l01 = perm(0x64646464u, bl, 0x04010400u), l23 = perm(0x64646464u, bl, 0x04030402u);
+                    const uint32_t h01 = perm(0x64646464u, bh, 0x04010400u), h23 = perm(0x64646464u, bh, 0x04030402u);
+#pragma unroll
+                    for (int n = 0; n < NC; n++) {
+                        s[sb][r][n] = dot2(l01, xl[n][e], s[sb][r][n]);
+                        s[sb][r][n] = dot2(l23, xl[n][e + 1], s[sb][r][n]);
+                        s[sb][r][n] = dot2(h01, xh[n][e], s[sb][r][n]);
+                        s[sb][r][n] = dot2(h23, xh[n][e + 1], s[sb][r][n]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const float d = h2f(w.hdr[r].x & 0xFFFF);
+            const uint32_t sh = w.hdr[r].x >> 16, sl = byte_of(w.hdr[r].y, g);
+            const float dl0 = d * (float)((int)((sl & 0xF) | (((sh >> (4 * g)) & 3) << 4)) - 32);
+            const float dl1 = d * (float)((int)((sl >> 4) | (((sh >> (4 * g + 2)) & 3) << 4)) - 32);
+#pragma unroll
+            for (int n = 0; n < NC; n++)
+                acc[r][n] += dl0 * (s[0][r][n] - 1152.0f * xsum[0][n]) + dl1 * (s[1][r][n] - 1152.0f * xsum[1][n]);
         }
     }
 };

@@ -74,7 +74,8 @@ namespace {
 using namespace okf;
 
 bool supported(int32_t t) {
-    return t == Q8_0 || t == Q4_K || t == IQ2_XXS || t == Q2_0 || t == Q4_0 || t == IQ4_NL;
+    return t == Q8_0 || t == Q4_K || t == IQ2_XXS || t == Q2_0 || t == Q4_0 || t == IQ4_NL || t == Q5_K ||
+           t == Q6_K || t == IQ4_XS;
 }
 
 int hip_fail(okf_ctx *c, hipError_t e) {
@@ -145,7 +146,8 @@ void launch_gemv_s(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32
     // two rows per slot (each staged activation read serves both) where
     // measured faster: IQ2_XXS with 2..5 columns, Q4_K and Q2_0 with 5; a
     // three-deep weight ring for the Q4_K matvec (its rows run 5+ steps)
-    constexpr int R = ((F == IQ2_XXS && NC >= 2) || (NC == 5 && F != Q8_0)) ? 2 : 1, D = (F == Q4_K && NC == 1) ? 3 : 2, WAVES = 4;
+    constexpr int R = ((F == IQ2_XXS && NC >= 2) || (NC == 5 && F != Q8_0 && F != Q5_K && F != Q6_K && F != IQ4_XS)) ? 2 : 1,
+                  D = (F == Q4_K && NC == 1) ? 3 : 2, WAVES = 4;
     const void *fn = (const void *)gemv_kernel<F, NC, R, D, S, SILU>;
     static bool attr = false;  // one attribute call per instantiation
     if (!attr) {
@@ -263,8 +265,9 @@ bool launch_gemv_wide(okf_ctx *c, const GemvCall &call, uint64_t rb, uint32_t K)
 
 template <int F, int NC, bool SILU = false>
 void launch_gemv_nc(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32_t K) {
-    // (Q4_K and Q8_0 units are too large for a deep ring at N > 1)
-    if constexpr (!SILU && !((F == Q4_K || F == Q8_0) && NC > 1))
+    // (Q4_K and Q8_0 units are too large for a deep ring at N > 1; the
+    // formats added after the measurements take the many-workgroup kernel)
+    if constexpr (!SILU && !((F == Q4_K || F == Q8_0) && NC > 1) && F != Q5_K && F != Q6_K && F != IQ4_XS)
         if (n == 1 && launch_gemv_wide<F, NC>(c, calls[0], rb, K)) return;
     constexpr uint32_t UW = unit_weights<F>();
     const size_t tab = F == IQ2_XXS ? 384 * 16 : 0;
@@ -393,6 +396,9 @@ void launch_embed(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_
     case Q4_K: fn<Q4_K>(__VA_ARGS__); break;                \
     case Q4_0: fn<Q4_0>(__VA_ARGS__); break;                \
     case IQ4_NL: fn<IQ4_NL>(__VA_ARGS__); break;            \
+    case Q5_K: fn<Q5_K>(__VA_ARGS__); break;                \
+    case Q6_K: fn<Q6_K>(__VA_ARGS__); break;                \
+    case IQ4_XS: fn<IQ4_XS>(__VA_ARGS__); break;            \
     default: fn<IQ2_XXS>(__VA_ARGS__); break;               \
     }
 
@@ -423,6 +429,9 @@ int run_gemm(okf_ctx *c, const okf_weight *w, const float *X, uint32_t N, float 
         case Q4_K: st = launch_gemm<Q4_K>(c, W, rb, w->K, w->M, X, N, Y); break;
         case Q4_0: st = launch_gemm<Q4_0>(c, W, rb, w->K, w->M, X, N, Y); break;
         case IQ4_NL: st = launch_gemm<IQ4_NL>(c, W, rb, w->K, w->M, X, N, Y); break;
+        case Q5_K: st = launch_gemm<Q5_K>(c, W, rb, w->K, w->M, X, N, Y); break;
+        case Q6_K: st = launch_gemm<Q6_K>(c, W, rb, w->K, w->M, X, N, Y); break;
+        case IQ4_XS: st = launch_gemm<IQ4_XS>(c, W, rb, w->K, w->M, X, N, Y); break;
         default: st = launch_gemm<IQ2_XXS>(c, W, rb, w->K, w->M, X, N, Y); break;
         }
         if (st) return st;

@@ -25,7 +25,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from .formats import Q8_0, Q2_0, Q4_K, IQ2_XXS, Q4_0, IQ4_NL, row_bytes
+from .formats import Q8_0, Q2_0, Q4_K, IQ2_XXS, Q4_0, IQ4_NL, Q5_K, Q6_K, IQ4_XS, row_bytes
 
 _A = 6364136223846793005
 _C = 1442695040888963407
@@ -137,7 +137,46 @@ def iq2_xxs(M: int, K: int, seed: int, d_range=(1e-3, 1e-2)) -> np.ndarray:
     return blk.reshape(-1)
 
 
-GENERATORS = {Q8_0: q8_0, Q2_0: q2_0, Q4_K: q4_k, IQ2_XXS: iq2_xxs, Q4_0: nibble32, IQ4_NL: nibble32}
+def q5_k(M: int, K: int, seed: int, d_range=(1e-3, 1e-2)) -> np.ndarray:
+    """M rows of Q5_K: d, dmin ~ U(d_range) fp16; scales[12], qh[32], qs[128]
+    uniform bytes."""
+    nb = M * (K // 256)
+    g = LCG(seed)
+    d = g.f16(*d_range, nb)
+    dmin = g.f16(*d_range, nb)
+    blk = np.empty((nb, 176), np.uint8)
+    blk[:, 0:2] = _f16_bytes(d)
+    blk[:, 2:4] = _f16_bytes(dmin)
+    blk[:, 4:] = g.bytes(nb * 172).reshape(nb, 172)
+    return blk.reshape(-1)
+
+
+def q6_k(M: int, K: int, seed: int, d_range=(1e-4, 1e-3)) -> np.ndarray:
+    """M rows of Q6_K: ql[128], qh[64], int8 scales[16] uniform bytes; d at
+    byte 208 ~ U(d_range) fp16 (scales reach +-128, so d is smaller)."""
+    nb = M * (K // 256)
+    g = LCG(seed)
+    d = g.f16(*d_range, nb)
+    blk = np.empty((nb, 210), np.uint8)
+    blk[:, :208] = g.bytes(nb * 208).reshape(nb, 208)
+    blk[:, 208:] = _f16_bytes(d)
+    return blk.reshape(-1)
+
+
+def iq4_xs(M: int, K: int, seed: int, d_range=(1e-4, 1e-3)) -> np.ndarray:
+    """M rows of IQ4_XS: d ~ U(d_range) fp16; scales_h, scales_l[4] and
+    qs[128] uniform bytes."""
+    nb = M * (K // 256)
+    g = LCG(seed)
+    d = g.f16(*d_range, nb)
+    blk = np.empty((nb, 136), np.uint8)
+    blk[:, :2] = _f16_bytes(d)
+    blk[:, 2:] = g.bytes(nb * 134).reshape(nb, 134)
+    return blk.reshape(-1)
+
+
+GENERATORS = {Q8_0: q8_0, Q2_0: q2_0, Q4_K: q4_k, IQ2_XXS: iq2_xxs, Q4_0: nibble32, IQ4_NL: nibble32,
+              Q5_K: q5_k, Q6_K: q6_k, IQ4_XS: iq4_xs}
 
 
 def weights(ggml_type: int, M: int, K: int, seed: int) -> np.ndarray:

@@ -1,7 +1,7 @@
 /*
  * okf_quant.h -- C ABI of the MI355X (gfx950) quantized weight x activation
  * path: fused dequantize-and-dot for GGUF Q8_0, Q4_K, IQ2_XXS and the Bonsai
- * ternary Q2_0 blocks, plus Q4_0 and IQ4_NL.
+ * ternary Q2_0 blocks, plus Q4_0, IQ4_NL, Q5_K, Q6_K and IQ4_XS.
  *
  * This ABI is the drop-in boundary for the reference's GPU dispatch surface
  * (LLM/Base/MetalEnc.swift) and the weight reference it takes
@@ -49,6 +49,9 @@ enum {
     OKF_TYPE_Q8_0 = 8,
     OKF_TYPE_IQ4_NL = 20,
     OKF_TYPE_Q4_K = 12,
+    OKF_TYPE_Q5_K = 13,
+    OKF_TYPE_Q6_K = 14,
+    OKF_TYPE_IQ4_XS = 23,
     OKF_TYPE_IQ2_XXS = 16,
     OKF_TYPE_Q2_0 = 42
 };

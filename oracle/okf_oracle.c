@@ -66,6 +66,9 @@ static int block_geom(int32_t type, uint32_t *elems, uint32_t *bytes) {
     case OKF_REF_IQ4_NL: *elems = 32; *bytes = 18; return 0;
     case OKF_REF_Q2_0: *elems = 128; *bytes = 34; return 0;
     case OKF_REF_Q4_K: *elems = 256; *bytes = 144; return 0;
+    case OKF_REF_Q5_K: *elems = 256; *bytes = 176; return 0;
+    case OKF_REF_Q6_K: *elems = 256; *bytes = 210; return 0;
+    case OKF_REF_IQ4_XS: *elems = 256; *bytes = 136; return 0;
     case OKF_REF_IQ2_XXS: *elems = 256; *bytes = 66; return 0;
     default: return -1;
     }
@@ -166,6 +169,73 @@ static void dq_q4_k_block(const uint8_t *b, float *out) {
     }
 }
 
+/* KQuant.q5K, LLM/Quantize/KQuants.swift:127-155: as q4K with a fifth bit
+ * from qh[l] (bytes 16..47), bit 2 it for the low nibble of code group it
+ * and bit 2 it + 1 for its high nibble. */
+static void dq_q5_k_block(const uint8_t *b, float *out) {
+    float d = ldh(b), dmin = ldh(b + 2);
+    int y = 0, qoff = 48, isc = 0;
+    uint8_t u1 = 1, u2 = 2;
+    for (int it = 0; it < 4; it++) {
+        float s1, m1, s2, m2;
+        scale_min(b, isc, &s1, &m1);
+        scale_min(b, isc + 1, &s2, &m2);
+        float d1 = d * s1, o1 = dmin * m1;
+        float d2 = d * s2, o2 = dmin * m2;
+        for (int l = 0; l < 32; l++) {
+            uint8_t q = b[qoff + l], h = b[16 + l];
+            float lo = (float)((q & 0xF) + ((h & u1) ? 16 : 0));
+            float hi = (float)((q >> 4) + ((h & u2) ? 16 : 0));
+            out[y + l] = d1 * lo - o1;
+            out[y + 32 + l] = d2 * hi - o2;
+        }
+        y += 64;
+        qoff += 32;
+        isc += 2;
+        u1 <<= 2;
+        u2 <<= 2;
+    }
+}
+
+/* KQuant.q6K, LLM/Quantize/KQuants.swift:157-176: ql[128], qh[64],
+ * int8 scales[16], d at 208; weight n*128 + r*32 + l has the low nibble
+ * (r < 2) or high nibble (r >= 2) of ql[n*64 + l] (r even) or
+ * ql[n*64 + 32 + l] (r odd), and bits 2r.. of qh[n*32 + l] on top;
+ * w = d * s * (q - 32) with s = scales[n*8 + 2r + l/16]. */
+static void dq_q6_k_block(const uint8_t *b, float *out) {
+    float d = ldh(b + 208);
+    for (int n = 0; n < 2; n++)
+        for (int l = 0; l < 32; l++) {
+            int h = b[128 + n * 32 + l], a = b[n * 64 + l], c = b[n * 64 + l + 32];
+            for (int r = 0; r < 4; r++) {
+                int byte = (r % 2) == 0 ? a : c;
+                int nib = r < 2 ? (byte & 0xF) : (byte >> 4);
+                int q = nib | (((h >> (2 * r)) & 3) << 4);
+                int s = (int8_t)b[192 + n * 8 + 2 * r + l / 16];
+                out[n * 128 + r * 32 + l] = d * (float)s * (float)(q - 32);
+            }
+        }
+}
+
+/* IQX.iq4XS, LLM/Quantize/IQ3.swift:118-133: sub-block ib has the 6-bit
+ * scale ls = (scales_l nibble ib) | (2 bits ib of scales_h) << 4;
+ * dl = d * (ls - 32); w = dl * nl4[nibble], nl4 = the IQ4_NL levels
+ * (IQ3Grid.swift:530). */
+static void dq_iq4_xs_block(const uint8_t *b, float *out) {
+    float d = ldh(b);
+    uint16_t sh = ld16(b + 2);
+    for (int ib = 0; ib < 8; ib++) {
+        uint8_t sl = b[4 + ib / 2];
+        int ls = ((sl >> (4 * (ib % 2))) & 0xF) | (((sh >> (2 * ib)) & 3) << 4);
+        float dl = d * (float)(ls - 32);
+        for (int j = 0; j < 16; j++) {
+            uint8_t q = b[8 + ib * 16 + j];
+            out[ib * 32 + j] = dl * iq4nl_values[q & 0xF];
+            out[ib * 32 + 16 + j] = dl * iq4nl_values[q >> 4];
+        }
+    }
+}
+
 /* IQ2XXS.dequant, LLM/Quantize/IQ2XXS.swift:34-54 */
 static void dq_iq2_xxs_block(const uint8_t *b, float *out) {
     float d = ldh(b);
@@ -190,6 +260,9 @@ typedef void (*sb_decode_fn)(const uint8_t *, float *);
 static sb_decode_fn sb_decoder(int32_t type) {
     switch (type) {
     case OKF_REF_Q4_K: return dq_q4_k_block;
+    case OKF_REF_Q5_K: return dq_q5_k_block;
+    case OKF_REF_Q6_K: return dq_q6_k_block;
+    case OKF_REF_IQ4_XS: return dq_iq4_xs_block;
     case OKF_REF_IQ2_XXS: return dq_iq2_xxs_block;
     default: return NULL;
     }
@@ -285,7 +358,8 @@ static float row_q2_0(const job_t *j, uint32_t m) {
 static float row_superblock(const job_t *j, uint32_t m) {
     const uint8_t *p = j->w + (uint64_t)m * j->row_bytes;
     sb_decode_fn dec = sb_decoder(j->type);
-    uint32_t bytes = j->type == OKF_REF_Q4_K ? 144 : 66;
+    uint32_t elems, bytes;
+    block_geom(j->type, &elems, &bytes);
     float w[256];
     float acc = 0;
     for (uint32_t k = 0; k < j->K; k += 256, p += bytes) {

@@ -34,6 +34,9 @@ enum {
     OKF_REF_Q8_0 = 8,
     OKF_REF_IQ4_NL = 20,
     OKF_REF_Q4_K = 12,
+    OKF_REF_Q5_K = 13,
+    OKF_REF_Q6_K = 14,
+    OKF_REF_IQ4_XS = 23,
     OKF_REF_IQ2_XXS = 16,
     OKF_REF_Q2_0 = 42,
 };

@@ -14,7 +14,7 @@ import pytest
 
 import oracle
 from chatokf_amd import synth
-from chatokf_amd.formats import Q8_0, Q2_0, Q4_K, IQ2_XXS, Q4_0, IQ4_NL
+from chatokf_amd.formats import Q8_0, Q2_0, Q4_K, IQ2_XXS, Q4_0, IQ4_NL, Q5_K, Q6_K, IQ4_XS
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 GOLD = json.load(open(os.path.join(ROOT, "tests", "golden", "iq2xxs_tables.json")))
@@ -200,6 +200,50 @@ def np_dequant(t, w, M, K):
                 s = np.where(sg & (1 << j), np.float32(-1), np.float32(1))
                 out[..., l, j] = db * g * s
         return out.reshape(M, K)
+    if t == Q5_K:
+        b = w.reshape(M, K // 256, 176)
+        d = b[:, :, 0:2].copy().view(np.float16).astype(np.float32)[..., 0]
+        dm = b[:, :, 2:4].copy().view(np.float16).astype(np.float32)[..., 0]
+        s = b[:, :, 4:16].astype(np.uint32)
+        sc = np.concatenate([s[..., 0:4] & 63, (s[..., 8:12] & 15) | ((s[..., 0:4] >> 6) << 4)], -1)
+        mn = np.concatenate([s[..., 4:8] & 63, (s[..., 8:12] >> 4) | ((s[..., 4:8] >> 6) << 4)], -1)
+        qh = b[:, :, 16:48]
+        qs = b[:, :, 48:].reshape(M, K // 256, 4, 32)
+        q = np.empty((M, K // 256, 8, 32), np.float32)
+        for g in range(4):  # group g: sub-blocks 2g (low nibbles) and 2g + 1 (high)
+            q[:, :, 2 * g] = (qs[:, :, g] & 15) + 16 * ((qh >> (2 * g)) & 1)
+            q[:, :, 2 * g + 1] = (qs[:, :, g] >> 4) + 16 * ((qh >> (2 * g + 1)) & 1)
+        d1 = d[..., None] * sc.astype(np.float32)
+        o1 = dm[..., None] * mn.astype(np.float32)
+        return (d1[..., None] * q - o1[..., None]).reshape(M, K)
+    if t == Q6_K:
+        b = w.reshape(M, K // 256, 210)
+        ql, qh = b[:, :, 0:128].astype(np.int32), b[:, :, 128:192].astype(np.int32)
+        sc = b[:, :, 192:208].view(np.int8).astype(np.float32)
+        d = b[:, :, 208:210].copy().view(np.float16).astype(np.float32)[..., 0]
+        out = np.empty((M, K // 256, 2, 4, 32), np.float32)
+        for n in range(2):
+            lo, hi = ql[:, :, 64 * n:64 * n + 32], ql[:, :, 64 * n + 32:64 * n + 64]
+            h = qh[:, :, 32 * n:32 * n + 32]
+            quads = [(lo & 15), (hi & 15), (lo >> 4), (hi >> 4)]
+            for r in range(4):
+                q = quads[r] | (((h >> (2 * r)) & 3) << 4)
+                s = np.repeat(sc[:, :, 8 * n + 2 * r:8 * n + 2 * r + 2], 16, axis=-1)
+                out[:, :, n, r] = d[..., None] * s * (q - 32).astype(np.float32)
+        return out.reshape(M, K)
+    if t == IQ4_XS:
+        b = w.reshape(M, K // 256, 136)
+        d = b[:, :, 0:2].copy().view(np.float16).astype(np.float32)[..., 0]
+        sh = b[:, :, 2:4].copy().view(np.uint16)[..., 0].astype(np.int32)
+        sl = b[:, :, 4:8].astype(np.int32)
+        qs = b[:, :, 8:].reshape(M, K // 256, 8, 16)
+        out = np.empty((M, K // 256, 8, 32), np.float32)
+        for ib in range(8):
+            ls = ((sl[..., ib // 2] >> (4 * (ib % 2))) & 15) | (((sh >> (2 * ib)) & 3) << 4)
+            dl = d * (ls - 32).astype(np.float32)
+            out[:, :, ib, :16] = dl[..., None] * IQ4NL_TABLE[qs[:, :, ib] & 15]
+            out[:, :, ib, 16:] = dl[..., None] * IQ4NL_TABLE[qs[:, :, ib] >> 4]
+        return out.reshape(M, K)
     if t in (Q4_0, IQ4_NL):
         b = w.reshape(M, K // 32, 18)
         d = b[:, :, :2].copy().view(np.float16).astype(np.float32)
@@ -215,7 +259,7 @@ IQ4NL_TABLE = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38,
                        np.float32)
 
 SMALL = [(Q8_0, 64, 256), (Q2_0, 64, 512), (Q4_K, 32, 512), (IQ2_XXS, 32, 512), (Q4_0, 64, 256),
-         (IQ4_NL, 64, 256)]
+         (IQ4_NL, 64, 256), (Q5_K, 32, 512), (Q6_K, 32, 512), (IQ4_XS, 32, 512)]
 
 
 @pytest.mark.parametrize("t,M,K", SMALL)
@@ -345,6 +389,41 @@ def test_q4_0_and_iq4_nl_known_answer():
     w = oracle.dequant(IQ4_NL, blk, 32)
     assert np.array_equal(w[:16], IQ4NL_TABLE)
     assert np.array_equal(w[16:], IQ4NL_TABLE[::-1])
+
+
+def test_q5_k_q6_k_iq4_xs_known_answer():
+    # Q5_K, d = 1, dmin = 0, sub-block 0 scale 1: w[l] = (nibble | qh bit 0 << 4)
+    blk = np.zeros(176, np.uint8)
+    blk[0:2] = _f16(1.0)
+    blk[4] = 1
+    blk[48:80] = np.arange(32) & 15
+    blk[16 + 16:16 + 32] = 1  # qh bit 0 for l >= 16
+    w = oracle.dequant(Q5_K, blk, 256)
+    assert np.array_equal(w[:32], np.arange(32, dtype=np.float32))
+    assert np.array_equal(w[32:], np.zeros(224, np.float32))  # other scales 0
+    # Q6_K, d = 1: zero codes give -32 * scale, and each 16 weights of
+    # (n, r) take their own scale scales[n*8 + 2r + l/16]
+    blk = np.zeros(210, np.uint8)
+    blk[192:208] = np.arange(1, 17)
+    blk[208:210] = _f16(1.0)
+    w = oracle.dequant(Q6_K, blk, 256)
+    assert np.array_equal(w, -32 * np.repeat(np.arange(1, 17), 16).astype(np.float32))
+    blk[0:192] = 0xFF  # every code 63: w = scale * 31
+    w = oracle.dequant(Q6_K, blk, 256)
+    assert np.array_equal(w, 31 * np.repeat(np.arange(1, 17), 16).astype(np.float32))
+    # IQ4_XS, d = 1: ls = 33 everywhere (low nibbles 1, high bits 2) gives
+    # dl = 1, so the weights are the levels; ls = 0 gives dl = -32
+    blk = np.zeros(136, np.uint8)
+    blk[0:2] = _f16(1.0)
+    blk[2:4] = np.array([0xAAAA], np.uint16).view(np.uint8)
+    blk[4:8] = 0x11
+    blk[8:136] = np.tile(np.array([j | ((15 - j) << 4) for j in range(16)], np.uint8), 8)
+    w = oracle.dequant(IQ4_XS, blk, 256).reshape(8, 32)
+    assert np.array_equal(w[:, :16], np.tile(IQ4NL_TABLE, (8, 1)))
+    assert np.array_equal(w[:, 16:], np.tile(IQ4NL_TABLE[::-1], (8, 1)))
+    blk[2:8] = 0
+    w = oracle.dequant(IQ4_XS, blk, 256).reshape(8, 32)
+    assert np.array_equal(w[:, :16], np.tile(-32 * IQ4NL_TABLE, (8, 1)))
 
 
 def test_iq4_nl_table_matches_reference_golden():
