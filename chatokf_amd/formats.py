@@ -11,16 +11,25 @@ Q4_K = 12
 Q5_K = 13
 Q6_K = 14
 IQ4_XS = 23
+IQ2_XS = 17
+IQ3_XXS = 18
+IQ1_S = 19
+IQ3_S = 21
+IQ2_S = 22
+IQ1_M = 29
 IQ2_XXS = 16
 Q2_0 = 42
 
 NAMES = {Q8_0: "q8_0", Q4_K: "q4_k", IQ2_XXS: "iq2_xxs", Q2_0: "q2_0", Q4_0: "q4_0", IQ4_NL: "iq4_nl",
-         Q5_K: "q5_k", Q6_K: "q6_k", IQ4_XS: "iq4_xs"}
+         Q5_K: "q5_k", Q6_K: "q6_k", IQ4_XS: "iq4_xs", IQ2_XS: "iq2_xs", IQ2_S: "iq2_s",
+         IQ3_XXS: "iq3_xxs", IQ3_S: "iq3_s", IQ1_S: "iq1_s", IQ1_M: "iq1_m"}
 BY_NAME = {v: k for k, v in NAMES.items()}
 
 # type -> (weights per block, bytes per block)
 BLOCK = {Q8_0: (32, 34), Q2_0: (128, 34), Q4_K: (256, 144), IQ2_XXS: (256, 66), Q4_0: (32, 18),
-         IQ4_NL: (32, 18), Q5_K: (256, 176), Q6_K: (256, 210), IQ4_XS: (256, 136)}
+         IQ4_NL: (32, 18), Q5_K: (256, 176), Q6_K: (256, 210), IQ4_XS: (256, 136),
+         IQ2_XS: (256, 74), IQ2_S: (256, 82), IQ3_XXS: (256, 98), IQ3_S: (256, 110), IQ1_S: (256, 50),
+         IQ1_M: (256, 56)}
 
 
 def block_elems(t: int) -> int:

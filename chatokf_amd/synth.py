@@ -25,7 +25,8 @@ from __future__ import annotations
 
 import numpy as np
 
-from .formats import Q8_0, Q2_0, Q4_K, IQ2_XXS, Q4_0, IQ4_NL, Q5_K, Q6_K, IQ4_XS, row_bytes
+from .formats import (Q8_0, Q2_0, Q4_K, IQ2_XXS, Q4_0, IQ4_NL, Q5_K, Q6_K, IQ4_XS, IQ2_XS, IQ2_S, IQ3_XXS,
+                      IQ3_S, IQ1_S, IQ1_M, row_bytes)
 
 _A = 6364136223846793005
 _C = 1442695040888963407
@@ -175,8 +176,38 @@ def iq4_xs(M: int, K: int, seed: int, d_range=(1e-4, 1e-3)) -> np.ndarray:
     return blk.reshape(-1)
 
 
+def _d_first(nbytes):
+    """256-weight blocks of `nbytes`: fp16 d ~ U(d_range) first, the rest uniform bytes."""
+    def gen(M: int, K: int, seed: int, d_range=(1e-3, 1e-2)) -> np.ndarray:
+        nb = M * (K // 256)
+        g = LCG(seed)
+        d = g.f16(*d_range, nb)
+        blk = np.empty((nb, nbytes), np.uint8)
+        blk[:, :2] = _f16_bytes(d)
+        blk[:, 2:] = g.bytes(nb * (nbytes - 2)).reshape(nb, nbytes - 2)
+        return blk.reshape(-1)
+    gen.__doc__ = f"M rows of {nbytes}-byte superblocks: d ~ U(d_range) fp16, the rest uniform bytes."
+    return gen
+
+
+def iq1_m(M: int, K: int, seed: int, d_range=(1e-3, 1e-2)) -> np.ndarray:
+    """M rows of IQ1_M: qs, qh and the scale fields uniform; the fp16 d ~
+    U(d_range) spread over the top nibbles of the four scale shorts
+    (IQ1M.scale, LLM/Quantize/IQ2XXS.swift:63-72)."""
+    nb = M * (K // 256)
+    g = LCG(seed)
+    d = g.f16(*d_range, nb).view(np.uint16).astype(np.uint16)
+    blk = g.bytes(nb * 56).reshape(nb, 56)
+    sc = blk[:, 48:56].copy().view(np.uint16).reshape(nb, 4) & np.uint16(0x0FFF)
+    for i in range(4):
+        sc[:, i] |= ((d >> np.uint16(4 * i)) & np.uint16(0xF)) << np.uint16(12)
+    blk[:, 48:56] = sc.view(np.uint8).reshape(nb, 8)
+    return blk.reshape(-1)
+
+
 GENERATORS = {Q8_0: q8_0, Q2_0: q2_0, Q4_K: q4_k, IQ2_XXS: iq2_xxs, Q4_0: nibble32, IQ4_NL: nibble32,
-              Q5_K: q5_k, Q6_K: q6_k, IQ4_XS: iq4_xs}
+              Q5_K: q5_k, Q6_K: q6_k, IQ4_XS: iq4_xs, IQ2_XS: _d_first(74), IQ2_S: _d_first(82),
+              IQ3_XXS: _d_first(98), IQ3_S: _d_first(110), IQ1_S: _d_first(50), IQ1_M: iq1_m}
 
 
 def weights(ggml_type: int, M: int, K: int, seed: int) -> np.ndarray:

@@ -15,6 +15,7 @@
 #include <string.h>
 
 #include "iq2xxs_grid.inc"
+#include "iq_grids.inc"
 
 #if defined(__FP_FAST_FMAF) || defined(__FAST_MATH__)
 #error "the oracle must be built without fast-math"
@@ -69,6 +70,12 @@ static int block_geom(int32_t type, uint32_t *elems, uint32_t *bytes) {
     case OKF_REF_Q5_K: *elems = 256; *bytes = 176; return 0;
     case OKF_REF_Q6_K: *elems = 256; *bytes = 210; return 0;
     case OKF_REF_IQ4_XS: *elems = 256; *bytes = 136; return 0;
+    case OKF_REF_IQ2_XS: *elems = 256; *bytes = 74; return 0;
+    case OKF_REF_IQ2_S: *elems = 256; *bytes = 82; return 0;
+    case OKF_REF_IQ3_XXS: *elems = 256; *bytes = 98; return 0;
+    case OKF_REF_IQ3_S: *elems = 256; *bytes = 110; return 0;
+    case OKF_REF_IQ1_S: *elems = 256; *bytes = 50; return 0;
+    case OKF_REF_IQ1_M: *elems = 256; *bytes = 56; return 0;
     case OKF_REF_IQ2_XXS: *elems = 256; *bytes = 66; return 0;
     default: return -1;
     }
@@ -236,6 +243,140 @@ static void dq_iq4_xs_block(const uint8_t *b, float *out) {
     }
 }
 
+/* IQX.sign, LLM/Quantize/IQ3.swift:9-11: bit j of the sign byte negates */
+static inline float iq_sign(uint8_t signs, int j, float v) { return (signs & (1u << j)) ? -v : v; }
+
+/* IQX.iq2XS, LLM/Quantize/IQ3.swift:14-33: { half d; u16 qs[32]; u8 scales[8] } */
+static void dq_iq2_xs_block(const uint8_t *b, float *out) {
+    float d = ldh(b);
+    for (int ib = 0; ib < 8; ib++) {
+        uint8_t sc = b[66 + ib];
+        float db0 = d * (0.5f + (float)(sc & 0xF)) * 0.25f;
+        float db1 = d * (0.5f + (float)(sc >> 4)) * 0.25f;
+        for (int l = 0; l < 4; l++) {
+            uint16_t q = ld16(b + 2 + (ib * 4 + l) * 2);
+            uint64_t entry = okf_ref_iq2xs_grid[q & 511];
+            uint8_t signs = okf_ref_ksigns[q >> 9];
+            float dl = l / 2 == 0 ? db0 : db1;
+            for (int j = 0; j < 8; j++)
+                out[ib * 32 + l * 8 + j] = iq_sign(signs, j, dl * (float)((entry >> (8 * j)) & 0xFF));
+        }
+    }
+}
+
+/* IQX.iq2S, LLM/Quantize/IQ3.swift:36-57:
+ * { half d; u8 qs[32]; u8 signs[32]; u8 qh[8]; u8 scales[8] } (offsets 2, 34, 66, 74) */
+static void dq_iq2_s_block(const uint8_t *b, float *out) {
+    float d = ldh(b);
+    for (int ib = 0; ib < 8; ib++) {
+        uint8_t sc = b[74 + ib];
+        float db0 = d * (0.5f + (float)(sc & 0xF)) * 0.25f;
+        float db1 = d * (0.5f + (float)(sc >> 4)) * 0.25f;
+        uint8_t qh = b[66 + ib];
+        for (int l = 0; l < 4; l++) {
+            int idx = b[2 + ib * 4 + l] | (((int)qh << (8 - 2 * l)) & 0x300);
+            uint64_t entry = okf_ref_iq2s_grid[idx];
+            uint8_t signs = b[34 + ib * 4 + l];
+            float dl = l / 2 == 0 ? db0 : db1;
+            for (int j = 0; j < 8; j++)
+                out[ib * 32 + l * 8 + j] = iq_sign(signs, j, dl * (float)((entry >> (8 * j)) & 0xFF));
+        }
+    }
+}
+
+/* IQX.iq3XXS, LLM/Quantize/IQ3.swift:60-82: { half d; u8 qs[64]; u32 scales_and_signs[8] } */
+static void dq_iq3_xxs_block(const uint8_t *b, float *out) {
+    float d = ldh(b);
+    for (int ib = 0; ib < 8; ib++) {
+        uint32_t aux = ld32(b + 66 + ib * 4);
+        float db = d * (0.5f + (float)(aux >> 28)) * 0.5f;
+        for (int l = 0; l < 4; l++) {
+            uint8_t signs = okf_ref_ksigns[(aux >> (7 * l)) & 127];
+            uint32_t g1 = okf_ref_iq3xxs_grid[b[2 + ib * 8 + 2 * l]];
+            uint32_t g2 = okf_ref_iq3xxs_grid[b[2 + ib * 8 + 2 * l + 1]];
+            int at = ib * 32 + l * 8;
+            for (int j = 0; j < 4; j++) {
+                out[at + j] = iq_sign(signs, j, db * (float)((g1 >> (8 * j)) & 0xFF));
+                out[at + j + 4] = iq_sign(signs, j + 4, db * (float)((g2 >> (8 * j)) & 0xFF));
+            }
+        }
+    }
+}
+
+/* IQX.iq3S, LLM/Quantize/IQ3.swift:85-115:
+ * { half d; u8 qs[64]; u8 qh[8]; u8 signs[32]; u8 scales[4] } (offsets 2, 66, 74, 106) */
+static void dq_iq3_s_block(const uint8_t *b, float *out) {
+    float d = ldh(b);
+    for (int pair = 0; pair < 4; pair++) {
+        uint8_t sc = b[106 + pair];
+        float db1 = d * (float)(1 + 2 * (sc & 0xF));
+        float db2 = d * (float)(1 + 2 * (sc >> 4));
+        for (int half = 0; half < 2; half++) {
+            int ib = pair * 2 + half;
+            uint8_t qh = b[66 + ib];
+            float db = half == 0 ? db1 : db2;
+            for (int l = 0; l < 4; l++) {
+                int base = 2 + ib * 8 + 2 * l;
+                uint32_t g1 = okf_ref_iq3s_grid[b[base] | (((int)qh << (8 - 2 * l)) & 256)];
+                uint32_t g2 = okf_ref_iq3s_grid[b[base + 1] | (((int)qh << (7 - 2 * l)) & 256)];
+                uint8_t signs = b[74 + ib * 4 + l];
+                int at = ib * 32 + l * 8;
+                for (int j = 0; j < 4; j++) {
+                    out[at + j] = iq_sign(signs, j, db * (float)((g1 >> (8 * j)) & 0xFF));
+                    out[at + j + 4] = iq_sign(signs, j + 4, db * (float)((g2 >> (8 * j)) & 0xFF));
+                }
+            }
+        }
+    }
+}
+
+/* IQ1 grid entry -> the 8 ternary digits n (0, 1, 2), digit j at bit
+ * 8 (j % 4) + 4 (j / 4) (IQ1Grid.gpu, LLM/Quantize/IQ1Grid.swift:8) */
+static inline int iq1_digit(uint32_t entry, int j) { return (entry >> (8 * (j % 4) + 4 * (j / 4))) & 0xF; }
+
+/* IQ1.dequant, LLM/Quantize/IQ1.swift:44-66: { half d; u8 qs[32]; u16 qh[8] };
+ * w = dl * (n - 1 + delta), dl = d * (2 ((h >> 12) & 7) + 1), delta = +-1/8 */
+static void dq_iq1_s_block(const uint8_t *b, float *out) {
+    float d = ldh(b);
+    for (int ib = 0; ib < 8; ib++) {
+        uint16_t h = ld16(b + 34 + ib * 2);
+        float dl = d * (float)(2 * ((h >> 12) & 7) + 1);
+        float delta = (h & 0x8000) ? -0.125f : 0.125f;
+        for (int l = 0; l < 4; l++) {
+            int idx = b[2 + ib * 4 + l] | (((h >> (3 * l)) & 7) << 8);
+            uint32_t entry = okf_ref_iq1s_grid[idx];
+            for (int j = 0; j < 8; j++) out[ib * 32 + l * 8 + j] = dl * ((float)iq1_digit(entry, j) - 1 + delta);
+        }
+    }
+}
+
+/* IQ1M.scale + IQ1M.dequant, LLM/Quantize/IQ2XXS.swift:63-98:
+ * { u8 qs[32]; u8 qh[16]; u16 scales[4] }, d reassembled from the top
+ * nibbles of the four scale shorts */
+static void dq_iq1_m_block(const uint8_t *b, float *out) {
+    uint16_t sc[4];
+    for (int i = 0; i < 4; i++) sc[i] = ld16(b + 48 + i * 2);
+    uint16_t bits = (uint16_t)((sc[0] >> 12) | ((sc[1] >> 8) & 0x00f0) | ((sc[2] >> 4) & 0x0f00) | (sc[3] & 0xf000));
+    float d = okf_ref_f16_to_f32(bits);
+    for (int ib = 0; ib < 8; ib++) {
+        uint16_t s = sc[ib / 2];
+        int shift = 6 * (ib % 2);
+        float dl1 = d * (float)(2 * ((s >> shift) & 7) + 1);
+        float dl2 = d * (float)(2 * ((s >> (shift + 3)) & 7) + 1);
+        uint8_t h0 = b[32 + ib * 2], h1 = b[33 + ib * 2];
+        for (int l = 0; l < 4; l++) {
+            uint8_t h = l < 2 ? h0 : h1;
+            int hi = (l % 2) == 0 ? ((int)h << 8) : ((int)h << 4);
+            int idx = b[ib * 4 + l] | (hi & 0x700);
+            int neg = (h & ((l % 2) == 0 ? 0x08 : 0x80)) != 0;
+            float delta = neg ? -0.125f : 0.125f;
+            float dl = l < 2 ? dl1 : dl2;
+            uint32_t entry = okf_ref_iq1s_grid[idx];
+            for (int j = 0; j < 8; j++) out[ib * 32 + l * 8 + j] = dl * ((float)iq1_digit(entry, j) - 1 + delta);
+        }
+    }
+}
+
 /* IQ2XXS.dequant, LLM/Quantize/IQ2XXS.swift:34-54 */
 static void dq_iq2_xxs_block(const uint8_t *b, float *out) {
     float d = ldh(b);
@@ -263,6 +404,12 @@ static sb_decode_fn sb_decoder(int32_t type) {
     case OKF_REF_Q5_K: return dq_q5_k_block;
     case OKF_REF_Q6_K: return dq_q6_k_block;
     case OKF_REF_IQ4_XS: return dq_iq4_xs_block;
+    case OKF_REF_IQ2_XS: return dq_iq2_xs_block;
+    case OKF_REF_IQ2_S: return dq_iq2_s_block;
+    case OKF_REF_IQ3_XXS: return dq_iq3_xxs_block;
+    case OKF_REF_IQ3_S: return dq_iq3_s_block;
+    case OKF_REF_IQ1_S: return dq_iq1_s_block;
+    case OKF_REF_IQ1_M: return dq_iq1_m_block;
     case OKF_REF_IQ2_XXS: return dq_iq2_xxs_block;
     default: return NULL;
     }

@@ -37,6 +37,12 @@ enum {
     OKF_REF_Q5_K = 13,
     OKF_REF_Q6_K = 14,
     OKF_REF_IQ4_XS = 23,
+    OKF_REF_IQ2_XS = 17,
+    OKF_REF_IQ3_XXS = 18,
+    OKF_REF_IQ1_S = 19,
+    OKF_REF_IQ3_S = 21,
+    OKF_REF_IQ2_S = 22,
+    OKF_REF_IQ1_M = 29,
     OKF_REF_IQ2_XXS = 16,
     OKF_REF_Q2_0 = 42,
 };

@@ -14,12 +14,16 @@ import pytest
 
 import oracle
 from chatokf_amd import synth
-from chatokf_amd.formats import Q8_0, Q2_0, Q4_K, IQ2_XXS, Q4_0, IQ4_NL, Q5_K, Q6_K, IQ4_XS
+from chatokf_amd.formats import (Q8_0, Q2_0, Q4_K, IQ2_XXS, Q4_0, IQ4_NL, Q5_K, Q6_K, IQ4_XS, IQ2_XS, IQ2_S,  # noqa: E501
+                                 IQ3_XXS, IQ3_S, IQ1_S, IQ1_M)
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 GOLD = json.load(open(os.path.join(ROOT, "tests", "golden", "iq2xxs_tables.json")))
 GRID = np.array([int(v, 16) for v in GOLD["iq2xxs_grid"]], dtype=np.uint64)
 KSIGNS = np.array(GOLD["ksigns"], dtype=np.uint8)
+IQG = json.load(open(os.path.join(ROOT, "tests", "golden", "iq_grids.json")))
+G = {k: np.array([int(v, 16) for v in IQG[k]], dtype=np.uint64) for k in
+     ("iq1s", "iq2xs", "iq2s", "iq3xxs", "iq3s")}
 
 
 def _f16(v):
@@ -40,6 +44,37 @@ def _inc_grid(path, name):
 ])
 def test_grid_tables_match_reference(path, name):
     assert _inc_grid(os.path.join(ROOT, path), name) == [int(v) for v in GRID]
+
+
+@pytest.mark.parametrize("name", ["iq1s", "iq2xs", "iq2s", "iq3xxs", "iq3s"])
+@pytest.mark.parametrize("path,prefix", [("oracle/iq_grids.inc", "okf_ref_"),
+                                         ("chatokf_amd/csrc/iq_grids.inc", "okf_host_")])
+def test_iq_grids_match_reference(name, path, prefix):
+    """The C tables against the fixture made from the reference's two copies
+    (Swift and IQTables.h, which tests/golden/make_iq_grids.py checks agree)."""
+    text = open(os.path.join(ROOT, path)).read()
+    body = text[text.index(prefix + name + "_grid"):]
+    body = body[body.index("{") + 1: body.index("}")]
+    vals = [int(t, 16) for t in re.findall(r"0x([0-9a-fA-F]+)", body)]
+    assert vals == [int(v) for v in G[name]]
+
+
+def test_iq_grid_invariants():
+    # magnitudes: IQ2_XS / IQ2_S grid bytes are from {8, 25, 43}, IQ3 bytes
+    # take 8 levels (IQ3_XXS 4 + 8i with 62 on top, IQ3_S the odd 1..15), IQ1
+    # digits are ternary (0, 1, 2) in the nibbles 8 (j % 4) + 4 (j / 4)
+    for k in ("iq2xs", "iq2s"):
+        b = set(int(v) >> (8 * j) & 255 for v in G[k] for j in range(8))
+        assert b <= {8, 25, 43}
+        assert len(set(int(v) for v in G[k])) == len(G[k])  # distinct entries
+    for k, levels in (("iq3xxs", {4, 12, 20, 28, 36, 44, 52, 62}), ("iq3s", set(range(1, 16, 2)))):
+        b = set(int(v) >> (8 * j) & 255 for v in G[k] for j in range(4))
+        assert b == levels
+        assert len(set(int(v) for v in G[k])) == len(G[k])
+    dig = set(int(v) >> (8 * (j % 4) + 4 * (j // 4)) & 15 for v in G["iq1s"] for j in range(8))
+    assert dig <= {0, 1, 2}
+    assert all((int(v) & 0xF0F0F0F0) >> 4 <= 0x02020202 for v in G["iq1s"])
+    assert len(set(int(v) for v in G["iq1s"])) == 2048
 
 
 def test_oracle_ksigns_match_reference():
@@ -244,6 +279,8 @@ def np_dequant(t, w, M, K):
             out[:, :, ib, :16] = dl[..., None] * IQ4NL_TABLE[qs[:, :, ib] & 15]
             out[:, :, ib, 16:] = dl[..., None] * IQ4NL_TABLE[qs[:, :, ib] >> 4]
         return out.reshape(M, K)
+    if t in (IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M):
+        return np.stack([_np_iq(t, w.reshape(M, -1)[m]) for m in range(M)])
     if t in (Q4_0, IQ4_NL):
         b = w.reshape(M, K // 32, 18)
         d = b[:, :, :2].copy().view(np.float16).astype(np.float32)
@@ -253,13 +290,86 @@ def np_dequant(t, w, M, K):
     raise ValueError(t)
 
 
+def _g8(entry, nbytes):
+    return [(int(entry) >> (8 * j)) & 255 for j in range(nbytes)]
+
+
+def _np_iq(t, row):
+    """One row of the grid formats, superblock by superblock, written from the
+    ggml block layouts (float32 array arithmetic, the reference's order)."""
+    f32, out = np.float32, []
+    for b in row.reshape(-1, len(row) // (len(row) // {IQ2_XS: 74, IQ2_S: 82, IQ3_XXS: 98, IQ3_S: 110,
+                                                         IQ1_S: 50, IQ1_M: 56}[t])):
+        b = b.astype(np.int64)
+        w = np.zeros(256, np.float32)
+        d = np.frombuffer(bytes(np.uint8(b[:2])), np.float16)[0].astype(f32) if t != IQ1_M else None
+        sgn = lambda s, j: f32(-1) if (int(s) >> j) & 1 else f32(1)  # noqa: E731
+        for ib in range(8):
+            if t in (IQ2_XS, IQ2_S):
+                sc = b[66 + ib] if t == IQ2_XS else b[74 + ib]
+                db = [d * (f32(0.5) + f32(sc & 15)) * f32(0.25), d * (f32(0.5) + f32(sc >> 4)) * f32(0.25)]
+                for l in range(4):
+                    if t == IQ2_XS:
+                        q = b[2 + 2 * (ib * 4 + l)] | (b[3 + 2 * (ib * 4 + l)] << 8)
+                        g, s = _g8(G["iq2xs"][q & 511], 8), KSIGNS[q >> 9]
+                    else:
+                        g = _g8(G["iq2s"][b[2 + ib * 4 + l] | ((b[66 + ib] << (8 - 2 * l)) & 0x300)], 8)
+                        s = b[34 + ib * 4 + l]
+                    for j in range(8):
+                        w[ib * 32 + l * 8 + j] = sgn(s, j) * (db[l // 2] * f32(g[j]))
+            elif t == IQ3_XXS:
+                aux = int(b[66 + 4 * ib]) | int(b[67 + 4 * ib]) << 8 | int(b[68 + 4 * ib]) << 16 | int(b[69 + 4 * ib]) << 24
+                db = d * (f32(0.5) + f32(aux >> 28)) * f32(0.5)
+                for l in range(4):
+                    s = KSIGNS[(aux >> (7 * l)) & 127]
+                    g = _g8(G["iq3xxs"][b[2 + ib * 8 + 2 * l]], 4) + _g8(G["iq3xxs"][b[3 + ib * 8 + 2 * l]], 4)
+                    for j in range(8):
+                        w[ib * 32 + l * 8 + j] = sgn(s, j) * (db * f32(g[j]))
+            elif t == IQ3_S:
+                sc = b[106 + ib // 2] >> (4 * (ib % 2)) & 15
+                db = d * f32(1 + 2 * sc)
+                qh = b[66 + ib]
+                for l in range(4):
+                    g = (_g8(G["iq3s"][b[2 + ib * 8 + 2 * l] | ((qh << (8 - 2 * l)) & 256)], 4)
+                         + _g8(G["iq3s"][b[3 + ib * 8 + 2 * l] | ((qh << (7 - 2 * l)) & 256)], 4))
+                    s = b[74 + ib * 4 + l]
+                    for j in range(8):
+                        w[ib * 32 + l * 8 + j] = sgn(s, j) * (db * f32(g[j]))
+            else:  # IQ1_S / IQ1_M: digits n in {0, 1, 2}, w = dl (n - 1 + delta)
+                if t == IQ1_S:
+                    h = int(b[34 + 2 * ib]) | int(b[35 + 2 * ib]) << 8
+                    dls = [d * f32(2 * ((h >> 12) & 7) + 1)] * 2
+                    hb = [(h >> (3 * l)) & 7 for l in range(4)]
+                    neg = [h >> 15] * 4
+                    qs = b[2 + ib * 4: 6 + ib * 4]
+                else:
+                    sc = [int(b[48 + 2 * i]) | int(b[49 + 2 * i]) << 8 for i in range(4)]
+                    bits = (sc[0] >> 12) | ((sc[1] >> 8) & 0xF0) | ((sc[2] >> 4) & 0xF00) | (sc[3] & 0xF000)
+                    dm = np.array([bits], np.uint16).view(np.float16)[0].astype(f32)
+                    s = sc[ib // 2] >> (6 * (ib % 2))
+                    dls = [dm * f32(2 * (s & 7) + 1), dm * f32(2 * ((s >> 3) & 7) + 1)]
+                    h = [int(b[32 + 2 * ib]), int(b[33 + 2 * ib])]
+                    hb = [h[l // 2] & 7 if l % 2 == 0 else (h[l // 2] >> 4) & 7 for l in range(4)]
+                    neg = [(h[l // 2] >> (3 if l % 2 == 0 else 7)) & 1 for l in range(4)]
+                    qs = b[ib * 4: ib * 4 + 4]
+                for l in range(4):
+                    e = int(G["iq1s"][int(qs[l]) | (hb[l] << 8)])
+                    delta = f32(-0.125) if neg[l] else f32(0.125)
+                    for j in range(8):
+                        n = (e >> (8 * (j % 4) + 4 * (j // 4))) & 15
+                        w[ib * 32 + l * 8 + j] = dls[l // 2] * (f32(n) - f32(1) + delta)
+        out.append(w)
+    return np.concatenate(out)
+
+
 # IQ4_NL's 16 non-linear levels, as published with the format (ggml's
 # kvalues_iq4nl); the golden test checks them against the reference's copy.
 IQ4NL_TABLE = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113],
                        np.float32)
 
 SMALL = [(Q8_0, 64, 256), (Q2_0, 64, 512), (Q4_K, 32, 512), (IQ2_XXS, 32, 512), (Q4_0, 64, 256),
-         (IQ4_NL, 64, 256), (Q5_K, 32, 512), (Q6_K, 32, 512), (IQ4_XS, 32, 512)]
+         (IQ4_NL, 64, 256), (Q5_K, 32, 512), (Q6_K, 32, 512), (IQ4_XS, 32, 512), (IQ2_XS, 8, 512),
+         (IQ2_S, 8, 512), (IQ3_XXS, 8, 512), (IQ3_S, 8, 512), (IQ1_S, 8, 512), (IQ1_M, 8, 512)]
 
 
 @pytest.mark.parametrize("t,M,K", SMALL)
@@ -424,6 +534,61 @@ def test_q5_k_q6_k_iq4_xs_known_answer():
     blk[2:8] = 0
     w = oracle.dequant(IQ4_XS, blk, 256).reshape(8, 32)
     assert np.array_equal(w[:, :16], np.tile(-32 * IQ4NL_TABLE, (8, 1)))
+
+
+def test_grid_formats_known_answer():
+    f32 = np.float32
+    # IQ2_XS, d = 1, scales 0 -> db = 1/8; index 0 (all 8s) with sign index 0
+    # -> 1.0; index 1 (byte 0 is 43) with sign index 127 (all eight negated)
+    blk = np.zeros(74, np.uint8)
+    blk[0:2] = _f16(1.0)
+    blk[2:4] = np.array([1 | (127 << 9)], np.uint16).view(np.uint8)  # group 0: index 1, signs 127
+    blk[66] = 0x20  # sub-block 0: low scale 0 (groups 0, 1), high scale 2 (groups 2, 3)
+    w = oracle.dequant(IQ2_XS, blk, 256)
+    assert np.array_equal(w[:8], -f32(0.125) * np.array([43] + [8] * 7, f32))  # byte j = weight j
+    assert np.array_equal(w[8:16], np.ones(8, f32))
+    assert np.array_equal(w[16:32], np.full(16, f32(2.5 * 0.25 * 8)))  # (0.5 + 2) / 4 * 8
+    # IQ2_S: the grid index takes bits 2l.. of qh as bits 8, 9; signs are bytes
+    blk = np.zeros(82, np.uint8)
+    blk[0:2] = _f16(1.0)
+    blk[2] = 1  # group 0 low index 1 ...
+    blk[66] = 0b01  # ... plus qh bits 0-1 = 1 -> index 257
+    blk[34] = 0x81  # signs of group 0: weights 0 and 7
+    w = oracle.dequant(IQ2_S, blk, 256)
+    g = _g8(G["iq2s"][257], 8)
+    assert np.array_equal(w[:8], np.array([(-1 if j in (0, 7) else 1) * 0.125 * g[j] for j in range(8)], f32))
+    # IQ3_XXS, d = 1, aux = 0 -> db = 1/4; index 0 (all 4s) -> 1.0; aux scale
+    # 15 -> db = 15.5 / 2
+    blk = np.zeros(98, np.uint8)
+    blk[0:2] = _f16(1.0)
+    blk[66 + 4:70 + 4] = np.array([15 << 28], np.uint32).view(np.uint8)
+    w = oracle.dequant(IQ3_XXS, blk, 256)
+    assert np.array_equal(w[:32], np.ones(32, f32))
+    assert np.array_equal(w[32:64], np.full(32, f32(15.5 * 0.5 * 4)))
+    # IQ3_S, d = 1, scale nibble 0 -> db = 1; index 0 (all 1s); sign byte
+    # 0xFF negates its group; qh bit 0 lifts the first index of group 0 to 256
+    blk = np.zeros(110, np.uint8)
+    blk[0:2] = _f16(1.0)
+    blk[74 + 1] = 0xFF
+    w = oracle.dequant(IQ3_S, blk, 256)
+    assert np.array_equal(w[:8], np.ones(8, f32)) and np.array_equal(w[8:16], -np.ones(8, f32))
+    blk[66] = 1
+    w = oracle.dequant(IQ3_S, blk, 256)
+    assert np.array_equal(w[:4], np.array(_g8(G["iq3s"][256], 4), f32))
+    # IQ1_S, d = 1: grid 0 (all digits 0) -> -1 + 1/8; h = 0x8000 | 7 << 12 ->
+    # dl = 15, delta = -1/8; index 1 has digit 2 at j = 0 -> dl (1 + delta)
+    blk = np.zeros(50, np.uint8)
+    blk[0:2] = _f16(1.0)
+    blk[36:38] = np.array([0x8000 | (7 << 12)], np.uint16).view(np.uint8)  # sub-block 1
+    blk[2 + 4] = 1  # sub-block 1, group 0: index 1
+    w = oracle.dequant(IQ1_S, blk, 256)
+    assert np.array_equal(w[:32], np.full(32, f32(-0.875)))
+    assert w[32] == f32(15 * 0.875) and np.array_equal(w[33:64], np.full(31, f32(-15 * 1.125)))
+    # IQ1_M: d = 1.0 (0x3C00) spread over the top nibbles of the scale shorts
+    blk = np.zeros(56, np.uint8)
+    blk[48:56] = np.array([0x0000, 0x0000, 0xC000, 0x3000], np.uint16).view(np.uint8)
+    w = oracle.dequant(IQ1_M, blk, 256)
+    assert np.array_equal(w, np.full(256, f32(-0.875)))
 
 
 def test_iq4_nl_table_matches_reference_golden():
