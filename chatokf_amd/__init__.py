@@ -15,7 +15,8 @@ import contextlib
 import ctypes
 import os
 
-from .formats import Q8_0, Q4_K, IQ2_XXS, Q2_0, Q4_0, IQ4_NL, Q5_K, Q6_K, IQ4_XS, NAMES, BY_NAME, block_elems, row_bytes
+from .formats import (Q8_0, Q4_K, IQ2_XXS, Q2_0, Q4_0, IQ4_NL, Q5_K, Q6_K, IQ4_XS, IQ2_XS, IQ2_S, IQ3_XXS,  # noqa
+                      IQ3_S, IQ1_S, IQ1_M, NAMES, BY_NAME, block_elems, row_bytes)
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("OKF_LIB") or os.path.join(HERE, "libokf_quant.so")
@@ -360,6 +361,7 @@ class GGUF:
 
 
 __all__ = [
-    "Q8_0", "Q4_K", "IQ2_XXS", "Q2_0", "Q4_0", "IQ4_NL", "Q5_K", "Q6_K", "IQ4_XS", "NAMES", "BY_NAME", "block_elems", "row_bytes",
+    "Q8_0", "Q4_K", "IQ2_XXS", "Q2_0", "Q4_0", "IQ4_NL", "Q5_K", "Q6_K", "IQ4_XS", "IQ2_XS", "IQ2_S", "IQ3_XXS", "IQ3_S",
+    "IQ1_S", "IQ1_M", "NAMES", "BY_NAME", "block_elems", "row_bytes",
     "QuantTensor", "Enc", "OkfError", "OkfWeight", "OkfGGUFTensor", "GGUF", "lib", "EXPORTS", "LIB_PATH",
 ]

@@ -5,14 +5,25 @@
 
 namespace okf {
 
-enum Fmt : int { Q4_0 = 2, Q8_0 = 8, Q4_K = 12, Q5_K = 13, Q6_K = 14, IQ2_XXS = 16, IQ4_NL = 20, IQ4_XS = 23,
-                 Q2_0 = 42 };
+enum Fmt : int {
+    Q4_0 = 2, Q8_0 = 8, Q4_K = 12, Q5_K = 13, Q6_K = 14, IQ2_XXS = 16, IQ2_XS = 17, IQ3_XXS = 18, IQ1_S = 19,
+    IQ4_NL = 20, IQ3_S = 21, IQ2_S = 22, IQ4_XS = 23, IQ1_M = 29, Q2_0 = 42
+};
+
+// The grid formats past IQ2_XXS: decoded through tables in device memory
+// (one buffer, byte offsets below) by a generic fp32 matvec.
+__host__ __device__ constexpr bool grid_fmt(int f) {
+    return f == IQ2_XS || f == IQ2_S || f == IQ3_XXS || f == IQ3_S || f == IQ1_S || f == IQ1_M;
+}
+constexpr uint32_t GT_IQ2XS = 0, GT_IQ2S = 4096, GT_IQ3XXS = 12288, GT_IQ3S = 13312, GT_IQ1S = 15360,
+                   GT_BYTES = 23552;
 
 // Bytes of one 256-weight span (Q8_0: 8 blocks, Q2_0: 2 blocks), matching the
 // reference's IQArgs.blk (LLM/Base/MetalEnc.swift:162-167).
 __host__ __device__ constexpr uint32_t block_bytes(int f) {
     return f == Q8_0 ? 34 : f == Q2_0 ? 34 : f == Q4_K ? 144 : (f == Q4_0 || f == IQ4_NL) ? 18
-         : f == Q5_K ? 176 : f == Q6_K ? 210 : f == IQ4_XS ? 136 : 66;
+         : f == Q5_K ? 176 : f == Q6_K ? 210 : f == IQ4_XS ? 136 : f == IQ2_XS ? 74 : f == IQ2_S ? 82
+         : f == IQ3_XXS ? 98 : f == IQ3_S ? 110 : f == IQ1_S ? 50 : f == IQ1_M ? 56 : 66;
 }
 __host__ __device__ constexpr uint32_t block_elems(int f) {
     return (f == Q8_0 || f == Q4_0 || f == IQ4_NL) ? 32 : f == Q2_0 ? 128 : 256;

@@ -207,9 +207,129 @@ __device__ __forceinline__ void decode_unit_iq4_xs(const uint8_t *row, uint32_t 
     }
 }
 
+// IQX.sign (LLM/Quantize/IQ3.swift:9-11): bit j of the sign byte negates.
+__device__ __forceinline__ float iq_sign(uint32_t signs, int j, float v) { return (signs >> j) & 1 ? -v : v; }
+
+// IQX.iq2XS / IQX.iq2S (LLM/Quantize/IQ3.swift:14-57), sub-block ib = u & 7:
+// db = d * (0.5 + nibble) * 0.25 (low nibble for groups 0, 1, high for 2, 3);
+// w = sign(db * grid byte j).
+template <bool S>
+__device__ __forceinline__ void decode_unit_iq2_xs_s(const uint8_t *row, uint32_t u, float *w,
+                                                     const uint8_t *gt) {
+    const uint8_t *b = row + (uint64_t)(u >> 3) * (S ? 82 : 74);
+    const uint32_t ib = u & 7;
+    const float d = h2f(ldu<uint16_t>(b));
+    const uint32_t sc = b[(S ? 74 : 66) + ib];
+    const float db0 = d * (0.5f + (float)(sc & 0xF)) * 0.25f, db1 = d * (0.5f + (float)(sc >> 4)) * 0.25f;
+    const uint64_t *grid = (const uint64_t *)(gt + (S ? GT_IQ2S : GT_IQ2XS));
+#pragma unroll
+    for (int l = 0; l < 4; l++) {
+        uint64_t e;
+        uint32_t signs;
+        if constexpr (S) {
+            const uint32_t qh = b[66 + ib];
+            e = grid[b[2 + ib * 4 + l] | ((qh << (8 - 2 * l)) & 0x300)];
+            signs = b[34 + ib * 4 + l];
+        } else {
+            const uint32_t q = ldu<uint16_t>(b + 2 + (ib * 4 + l) * 2);
+            e = grid[q & 511];
+            signs = iq2_signs(q >> 9);
+        }
+        const float dl = l < 2 ? db0 : db1;
+#pragma unroll
+        for (int j = 0; j < 8; j++) w[l * 8 + j] = iq_sign(signs, j, dl * (float)((e >> (8 * j)) & 0xFF));
+    }
+}
+
+// IQX.iq3XXS / IQX.iq3S (LLM/Quantize/IQ3.swift:60-115), sub-block ib = u & 7.
+template <bool S>
+__device__ __forceinline__ void decode_unit_iq3(const uint8_t *row, uint32_t u, float *w, const uint8_t *gt) {
+    const uint8_t *b = row + (uint64_t)(u >> 3) * (S ? 110 : 98);
+    const uint32_t ib = u & 7;
+    const float d = h2f(ldu<uint16_t>(b));
+    const uint32_t *grid = (const uint32_t *)(gt + (S ? GT_IQ3S : GT_IQ3XXS));
+    float db;
+    uint32_t aux = 0, qh = 0;
+    if constexpr (S) {
+        const uint32_t sc = (b[106 + ib / 2] >> (4 * (ib & 1))) & 0xF;
+        db = d * (float)(1 + 2 * sc);
+        qh = b[66 + ib];
+    } else {
+        aux = ldu<uint32_t>(b + 66 + ib * 4);
+        db = d * (0.5f + (float)(aux >> 28)) * 0.5f;
+    }
+#pragma unroll
+    for (int l = 0; l < 4; l++) {
+        const uint32_t i1 = b[2 + ib * 8 + 2 * l], i2 = b[3 + ib * 8 + 2 * l];
+        uint32_t g1, g2, signs;
+        if constexpr (S) {
+            g1 = grid[i1 | ((qh << (8 - 2 * l)) & 256)];
+            g2 = grid[i2 | ((qh << (7 - 2 * l)) & 256)];
+            signs = b[74 + ib * 4 + l];
+        } else {
+            g1 = grid[i1];
+            g2 = grid[i2];
+            signs = iq2_signs((aux >> (7 * l)) & 127);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            w[l * 8 + j] = iq_sign(signs, j, db * (float)((g1 >> (8 * j)) & 0xFF));
+            w[l * 8 + j + 4] = iq_sign(signs, j + 4, db * (float)((g2 >> (8 * j)) & 0xFF));
+        }
+    }
+}
+
+// IQ1.dequant (LLM/Quantize/IQ1.swift:44-66) and IQ1M.dequant
+// (LLM/Quantize/IQ2XXS.swift:63-98), sub-block ib = u & 7: w = dl (n - 1 +
+// delta) with the grid's ternary digit n at bit 8 (j % 4) + 4 (j / 4).
+template <bool M>
+__device__ __forceinline__ void decode_unit_iq1(const uint8_t *row, uint32_t u, float *w, const uint8_t *gt) {
+    const uint8_t *b = row + (uint64_t)(u >> 3) * (M ? 56 : 50);
+    const uint32_t ib = u & 7;
+    const uint32_t *grid = (const uint32_t *)(gt + GT_IQ1S);
+    float dls[2];
+    uint32_t hb[4], neg[4];
+    const uint8_t *qs;
+    if constexpr (M) {
+        uint32_t sc[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) sc[i] = ldu<uint16_t>(b + 48 + i * 2);
+        const uint32_t bits = (sc[0] >> 12) | ((sc[1] >> 8) & 0x00f0) | ((sc[2] >> 4) & 0x0f00) | (sc[3] & 0xf000);
+        const float d = h2f((uint16_t)bits);
+        const uint32_t s = sc[ib / 2] >> (6 * (ib & 1));
+        dls[0] = d * (float)(2 * (s & 7) + 1);
+        dls[1] = d * (float)(2 * ((s >> 3) & 7) + 1);
+        const uint32_t h0 = b[32 + ib * 2], h1 = b[33 + ib * 2];
+        hb[0] = h0 & 7; hb[1] = (h0 >> 4) & 7; hb[2] = h1 & 7; hb[3] = (h1 >> 4) & 7;
+        neg[0] = (h0 >> 3) & 1; neg[1] = h0 >> 7; neg[2] = (h1 >> 3) & 1; neg[3] = h1 >> 7;
+        qs = b + ib * 4;
+    } else {
+        const float d = h2f(ldu<uint16_t>(b));
+        const uint32_t h = ldu<uint16_t>(b + 34 + ib * 2);
+        dls[0] = dls[1] = d * (float)(2 * ((h >> 12) & 7) + 1);
+#pragma unroll
+        for (int l = 0; l < 4; l++) {
+            hb[l] = (h >> (3 * l)) & 7;
+            neg[l] = h >> 15;
+        }
+        qs = b + 2 + ib * 4;
+    }
+#pragma unroll
+    for (int l = 0; l < 4; l++) {
+        const uint32_t e = grid[qs[l] | (hb[l] << 8)];
+        const float delta = neg[l] ? -0.125f : 0.125f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint32_t n = (e >> (8 * (j % 4) + 4 * (j / 4))) & 0xF;
+            w[l * 8 + j] = dls[l / 2] * ((float)n - 1.0f + delta);
+        }
+    }
+}
+
+// gt: the grid tables of the grid formats (GT_* offsets), in device memory
 template <int F>
 __device__ __forceinline__ void decode_unit(const uint8_t *row, uint32_t u, float *w,
-                                            const uint2 *grid) {
+                                            const uint2 *grid, const uint8_t *gt = nullptr) {
     if constexpr (F == Q8_0) decode_unit_q8_0(row, u, w);
     else if constexpr (F == Q2_0) decode_unit_q2_0(row, u, w);
     else if constexpr (F == Q4_K) decode_unit_q4_k(row, u, w);
@@ -218,6 +338,9 @@ __device__ __forceinline__ void decode_unit(const uint8_t *row, uint32_t u, floa
     else if constexpr (F == Q5_K) decode_unit_q5_k(row, u, w);
     else if constexpr (F == Q6_K) decode_unit_q6_k(row, u, w);
     else if constexpr (F == IQ4_XS) decode_unit_iq4_xs(row, u, w);
+    else if constexpr (F == IQ2_XS || F == IQ2_S) decode_unit_iq2_xs_s<F == IQ2_S>(row, u, w, gt);
+    else if constexpr (F == IQ3_XXS || F == IQ3_S) decode_unit_iq3<F == IQ3_S>(row, u, w, gt);
+    else if constexpr (F == IQ1_S || F == IQ1_M) decode_unit_iq1<F == IQ1_M>(row, u, w, gt);
     else decode_unit_iq2_xxs(row, u, w, grid);
 }
 

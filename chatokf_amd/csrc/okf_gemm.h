@@ -38,7 +38,8 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t *__restric
                                                         uint64_t row_bytes, uint32_t K, uint32_t M,
                                                         const float *__restrict__ X, uint32_t N,
                                                         float *__restrict__ Y,
-                                                        const uint2 *__restrict__ grid_g) {
+                                                        const uint2 *__restrict__ grid_g,
+                                                        const uint8_t *__restrict__ gt) {
     __shared__ __attribute__((aligned(16))) _Float16 As[GB_M * G_LDS_STRIDE];
     __shared__ __attribute__((aligned(16))) _Float16 Bs[GB_N * G_LDS_STRIDE];
     __shared__ uint2 grid[F == IQ2_XXS ? 256 : 1];
@@ -65,7 +66,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t *__restric
         _Float16 *bd = Bs + lr * G_LDS_STRIDE + lh * 32;
         if (u < units) {
             float w[32];
-            decode_unit<F>(wrow, u, w, grid);
+            decode_unit<F>(wrow, u, w, grid, gt);
             store_half32(ad, w);
             float x[32];
             const float4 *xp = (const float4 *)(xrow + u * 32);
@@ -125,7 +126,8 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t *__restric
 template <int F>
 __global__ __launch_bounds__(256) void dequant_row_kernel(const uint8_t *__restrict__ row,
                                                           uint32_t units, float *__restrict__ out,
-                                                          const uint2 *__restrict__ grid_g) {
+                                                          const uint2 *__restrict__ grid_g,
+                                                          const uint8_t *__restrict__ gt) {
     __shared__ uint2 grid[F == IQ2_XXS ? 256 : 1];
     if constexpr (F == IQ2_XXS) {
         grid[threadIdx.x] = grid_g[threadIdx.x];
@@ -134,7 +136,7 @@ __global__ __launch_bounds__(256) void dequant_row_kernel(const uint8_t *__restr
     const uint32_t u = blockIdx.x * 256 + threadIdx.x;
     if (u >= units) return;
     float w[32];
-    decode_unit<F>(row, u, w, grid);
+    decode_unit<F>(row, u, w, grid, gt);
     float4 *o = (float4 *)(out + (uint64_t)u * 32);
 #pragma unroll
     for (int i = 0; i < 8; i++) o[i] = make_float4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
@@ -150,7 +152,8 @@ __global__ __launch_bounds__(256) void embed_batch_kernel(const uint8_t *__restr
                                                           const int32_t *__restrict__ ids,
                                                           uint32_t units_per_row, uint32_t units,
                                                           float *__restrict__ out,
-                                                          const uint2 *__restrict__ grid_g) {
+                                                          const uint2 *__restrict__ grid_g,
+                                                          const uint8_t *__restrict__ gt) {
     __shared__ uint2 grid[F == IQ2_XXS ? 256 : 1];
     if constexpr (F == IQ2_XXS) {
         grid[threadIdx.x] = grid_g[threadIdx.x];
@@ -162,7 +165,7 @@ __global__ __launch_bounds__(256) void embed_batch_kernel(const uint8_t *__restr
     const int32_t id = ids[n];
     const uint32_t row = id < 0 ? 0u : min((uint32_t)id, M - 1);
     float w[32];
-    decode_unit<F>(W + (uint64_t)row * row_bytes, u, w, grid);
+    decode_unit<F>(W + (uint64_t)row * row_bytes, u, w, grid, gt);
     float4 *o = (float4 *)(out + ((uint64_t)n * units_per_row + u) * 32);
 #pragma unroll
     for (int i = 0; i < 8; i++) o[i] = make_float4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);

@@ -33,7 +33,7 @@ namespace okf {
 // any K that is a whole number of blocks works).
 template <int F>
 __host__ __device__ constexpr uint32_t unit_weights() {
-    return (F == Q8_0 || F == Q4_0 || F == IQ4_NL || F == Q6_K) ? 32 : 64;
+    return (F == Q8_0 || F == Q4_0 || F == IQ4_NL || F == Q6_K || grid_fmt(F)) ? 32 : 64;
 }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -64,8 +64,12 @@ constexpr uint32_t ONES2 = 0x3C003C00u;   // two fp16 1.0
 
 // ---------------------------------------------------------------- units --
 // Raw bytes of one unit for R rows (native vector types keep them in VGPRs).
+// The grid formats (grid_fmt) keep only the row: their compute decodes a
+// 32-weight sub-block with the bit-exact decoder.
 template <int F, int R>
-struct Unit;
+struct Unit {
+    const uint8_t *row[R];
+};
 template <int R>
 struct Unit<Q4_K, R> {  // 16-byte header + 32 code bytes of group g
     u32x4 hdr[R], q0[R], q1[R];
@@ -153,6 +157,8 @@ __device__ __forceinline__ void load_unit(const uint8_t *const rows[R], uint32_t
             w.hdr[r] = ldu<uint2>(b);
             w.q0[r] = ldu<u32x4>(b + 8 + g * 32);
             w.q1[r] = ldu<u32x4>(b + 24 + g * 32);
+        } else if constexpr (grid_fmt(F)) {
+            w.row[r] = rows[r];
         } else if constexpr (F == Q4_0 || F == IQ4_NL) {
             const uint8_t *b = rows[r] + (uint64_t)u * 18;
             w.d[r] = ldu<uint16_t>(b);
@@ -234,7 +240,38 @@ __device__ __forceinline__ uint32_t xs_index(uint32_t u, uint32_t p) {
 // acc[r][n] += unit contribution; xp = this lane's pairs of column 0 in
 // LDS (slot s at xp[s * 64]), cs = uint32 stride between columns.
 template <int F, int NC, int R, int TS = 1>
-struct Compute;
+struct Compute {
+    // The grid formats (IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M): the
+    // 32-weight sub-block is decoded to fp32 with the bit-exact decoder
+    // (grid tables from device memory, tab) and multiplied into the staged
+    // fp16 activations (natural order) in fp32.
+    static_assert(grid_fmt(F), "no matvec compute for this format");
+    __device__ __forceinline__ static void run(const Unit<F, R> &w, const uint32_t *xp, uint32_t ss, uint32_t cs,
+                                               const float *, uint32_t, uint32_t u, float (&acc)[R][NC],
+                                               const u32x4 *tab) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            float wv[32];
+            decode_unit<F>(w.row[r], u, wv, nullptr, (const uint8_t *)tab);
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+#pragma unroll
+                for (int n = 0; n < NC; n++) {
+                    const u32x4 xv = *(const u32x4 *)(xp + n * cs + s * ss);
+                    float a = 0;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        // (the element is copied out first: a bit_cast of a vector
+                        // element expression reads the vector's first element)
+                        const uint32_t xe = xv[e];
+                        a += wv[8 * s + 2 * e] * h2f(xe & 0xFFFF) + wv[8 * s + 2 * e + 1] * h2f(xe >> 16);
+                    }
+                    acc[r][n] += a;
+                }
+            }
+        }
+    }
+};
 
 template <int NC, int R, int TS>
 struct Compute<Q4_K, NC, R, TS> {
@@ -920,7 +957,7 @@ __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ W, uint64_
                 const uint32_t u = i + L * (part + S * (t + j));
                 if (u < cn)
                     Compute<F, NC, R>::run(buf[j], xs + xs_index<F, L>(u, 0), 4 * L, cs,
-                                           xsum + u * (UW / 32), xcs, c0 + u, acc, tab);
+                                           xsum + u * (UW / 32), xcs, c0 + u, acc, grid_fmt(F) ? tab_g : tab);
                 load_unit<F, R>(rows, c0 + min(u + L * S * D, last), buf[j]);
             }
         }
@@ -929,7 +966,7 @@ __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ W, uint64_
             const uint32_t u = i + L * (part + S * (t + j));
             if (u < cn)
                 Compute<F, NC, R>::run(buf[j], xs + xs_index<F, L>(u, 0), 4 * L, cs,
-                                       xsum + u * (UW / 32), xcs, c0 + u, acc, tab);
+                                       xsum + u * (UW / 32), xcs, c0 + u, acc, grid_fmt(F) ? tab_g : tab);
         }
     }
     // reduce: over the slot's lanes, then (S > 1) over the parts in LDS

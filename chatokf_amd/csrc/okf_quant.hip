@@ -26,6 +26,7 @@
 #include "okf_norm.h"
 
 #include "iq2xxs_grid.inc"
+#include "iq_grids.inc"
 
 // one matvec y = W x of a launch group (with X2: x = silu(X) * X2)
 struct GemvCall {
@@ -44,6 +45,7 @@ struct okf_ctx {
     int device = -1;
     hipStream_t stream = nullptr;
     uint2 *grid = nullptr;  // 256 IQ2_XXS grid entries in device memory
+    uint8_t *grids = nullptr;  // the grids of IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S / IQ1_M (GT_* offsets)
     okf::u32x4 *tab = nullptr;   // IQ2_XXS fp16 grid (256 x 8 halves) + sign masks (128)
     size_t max_lds = 65536;  // dynamic LDS a workgroup may use
     // matvec tuning (defaults chosen per shape; OKF_GEMV_* environment
@@ -75,7 +77,7 @@ using namespace okf;
 
 bool supported(int32_t t) {
     return t == Q8_0 || t == Q4_K || t == IQ2_XXS || t == Q2_0 || t == Q4_0 || t == IQ4_NL || t == Q5_K ||
-           t == Q6_K || t == IQ4_XS;
+           t == Q6_K || t == IQ4_XS || grid_fmt(t);
 }
 
 int hip_fail(okf_ctx *c, hipError_t e) {
@@ -146,7 +148,7 @@ void launch_gemv_s(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32
     // two rows per slot (each staged activation read serves both) where
     // measured faster: IQ2_XXS with 2..5 columns, Q4_K and Q2_0 with 5; a
     // three-deep weight ring for the Q4_K matvec (its rows run 5+ steps)
-    constexpr int R = ((F == IQ2_XXS && NC >= 2) || (NC == 5 && F != Q8_0 && F != Q5_K && F != Q6_K && F != IQ4_XS)) ? 2 : 1,
+    constexpr int R = ((F == IQ2_XXS && NC >= 2) || (NC == 5 && F != Q8_0 && F != Q5_K && F != Q6_K && F != IQ4_XS && !grid_fmt(F))) ? 2 : 1,
                   D = (F == Q4_K && NC == 1) ? 3 : 2, WAVES = 4;
     const void *fn = (const void *)gemv_kernel<F, NC, R, D, S, SILU>;
     static bool attr = false;  // one attribute call per instantiation
@@ -167,8 +169,11 @@ void launch_gemv_s(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32
         g.end[i] = total;
     }
     g.n = (uint32_t)n;
+    // the tables the compute reads: IQ2_XXS's LDS rows (copied from c->tab),
+    // or the grid formats' device-memory grids
+    const u32x4 *tabs = grid_fmt(F) ? (const u32x4 *)c->grids : c->tab;
     hipLaunchKernelGGL((gemv_kernel<F, NC, R, D, S, SILU>), dim3(total), dim3(64 * WAVES), lds, c->stream,
-                       g, rb, K, c->tab, cunits);
+                       g, rb, K, tabs, cunits);
 }
 
 // Launch geometry: 256-thread workgroups of four wavefronts, each four row
@@ -267,7 +272,8 @@ template <int F, int NC, bool SILU = false>
 void launch_gemv_nc(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32_t K) {
     // (Q4_K and Q8_0 units are too large for a deep ring at N > 1; the
     // formats added after the measurements take the many-workgroup kernel)
-    if constexpr (!SILU && !((F == Q4_K || F == Q8_0) && NC > 1) && F != Q5_K && F != Q6_K && F != IQ4_XS)
+    if constexpr (!SILU && !((F == Q4_K || F == Q8_0) && NC > 1) && F != Q5_K && F != Q6_K && F != IQ4_XS &&
+                  !grid_fmt(F))
         if (n == 1 && launch_gemv_wide<F, NC>(c, calls[0], rb, K)) return;
     constexpr uint32_t UW = unit_weights<F>();
     const size_t tab = F == IQ2_XXS ? 384 * 16 : 0;
@@ -370,7 +376,7 @@ int launch_gemm(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t 
     }
     dim3 grid((N + GB_N - 1) / GB_N, (M + GB_M - 1) / GB_M);
     hipLaunchKernelGGL((gemm_mfma_kernel<F>), grid, dim3(256), 0, c->stream, W, rb, K, M, X, N, Y,
-                       c->grid);
+                       c->grid, c->grids);
     return OKF_OK;
 }
 
@@ -378,7 +384,7 @@ template <int F>
 void launch_dequant(okf_ctx *c, const uint8_t *row, uint32_t n, float *out) {
     const uint32_t units = n / 32;
     hipLaunchKernelGGL((dequant_row_kernel<F>), dim3((units + 255) / 256), dim3(256), 0, c->stream,
-                       row, units, out, c->grid);
+                       row, units, out, c->grid, c->grids);
 }
 
 template <int F>
@@ -386,7 +392,7 @@ void launch_embed(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_
                   const int32_t *ids, uint32_t N, float *out) {
     const uint32_t upr = K / 32, units = N * upr;
     hipLaunchKernelGGL((embed_batch_kernel<F>), dim3((units + 255) / 256), dim3(256), 0, c->stream, W,
-                       rb, M, ids, upr, units, out, c->grid);
+                       rb, M, ids, upr, units, out, c->grid, c->grids);
 }
 
 #define OKF_DISPATCH(type, fn, ...)                         \
@@ -399,6 +405,12 @@ void launch_embed(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_
     case Q5_K: fn<Q5_K>(__VA_ARGS__); break;                \
     case Q6_K: fn<Q6_K>(__VA_ARGS__); break;                \
     case IQ4_XS: fn<IQ4_XS>(__VA_ARGS__); break;            \
+    case IQ2_XS: fn<IQ2_XS>(__VA_ARGS__); break;            \
+    case IQ2_S: fn<IQ2_S>(__VA_ARGS__); break;              \
+    case IQ3_XXS: fn<IQ3_XXS>(__VA_ARGS__); break;          \
+    case IQ3_S: fn<IQ3_S>(__VA_ARGS__); break;              \
+    case IQ1_S: fn<IQ1_S>(__VA_ARGS__); break;              \
+    case IQ1_M: fn<IQ1_M>(__VA_ARGS__); break;              \
     default: fn<IQ2_XXS>(__VA_ARGS__); break;               \
     }
 
@@ -432,6 +444,12 @@ int run_gemm(okf_ctx *c, const okf_weight *w, const float *X, uint32_t N, float 
         case Q5_K: st = launch_gemm<Q5_K>(c, W, rb, w->K, w->M, X, N, Y); break;
         case Q6_K: st = launch_gemm<Q6_K>(c, W, rb, w->K, w->M, X, N, Y); break;
         case IQ4_XS: st = launch_gemm<IQ4_XS>(c, W, rb, w->K, w->M, X, N, Y); break;
+        case IQ2_XS: st = launch_gemm<IQ2_XS>(c, W, rb, w->K, w->M, X, N, Y); break;
+        case IQ2_S: st = launch_gemm<IQ2_S>(c, W, rb, w->K, w->M, X, N, Y); break;
+        case IQ3_XXS: st = launch_gemm<IQ3_XXS>(c, W, rb, w->K, w->M, X, N, Y); break;
+        case IQ3_S: st = launch_gemm<IQ3_S>(c, W, rb, w->K, w->M, X, N, Y); break;
+        case IQ1_S: st = launch_gemm<IQ1_S>(c, W, rb, w->K, w->M, X, N, Y); break;
+        case IQ1_M: st = launch_gemm<IQ1_M>(c, W, rb, w->K, w->M, X, N, Y); break;
         default: st = launch_gemm<IQ2_XXS>(c, W, rb, w->K, w->M, X, N, Y); break;
         }
         if (st) return st;
@@ -479,12 +497,30 @@ int okf_ctx_create(int device, okf_ctx **out) {
         if (e == hipSuccess)
             e = hipMemcpy(c->grid, okf_iq2xxs_grid_host, sizeof(okf_iq2xxs_grid_host),
                           hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMalloc((void **)&c->grids, GT_BYTES);
+        if (e == hipSuccess) {
+            static_assert(sizeof(okf_host_iq2xs_grid) == GT_IQ2S - GT_IQ2XS &&
+                              sizeof(okf_host_iq2s_grid) == GT_IQ3XXS - GT_IQ2S &&
+                              sizeof(okf_host_iq3xxs_grid) == GT_IQ3S - GT_IQ3XXS &&
+                              sizeof(okf_host_iq3s_grid) == GT_IQ1S - GT_IQ3S &&
+                              sizeof(okf_host_iq1s_grid) == GT_BYTES - GT_IQ1S,
+                          "grid table layout");
+            const struct { const void *p; size_t n, off; } parts[] = {
+                {okf_host_iq2xs_grid, sizeof(okf_host_iq2xs_grid), GT_IQ2XS},
+                {okf_host_iq2s_grid, sizeof(okf_host_iq2s_grid), GT_IQ2S},
+                {okf_host_iq3xxs_grid, sizeof(okf_host_iq3xxs_grid), GT_IQ3XXS},
+                {okf_host_iq3s_grid, sizeof(okf_host_iq3s_grid), GT_IQ3S},
+                {okf_host_iq1s_grid, sizeof(okf_host_iq1s_grid), GT_IQ1S}};
+            for (const auto &q : parts)
+                if (e == hipSuccess) e = hipMemcpy(c->grids + q.off, q.p, q.n, hipMemcpyHostToDevice);
+        }
         uint32_t tabh[384 * 4];
         build_iq2_tables(tabh);
         if (e == hipSuccess) e = hipMalloc((void **)&c->tab, sizeof(tabh));
         if (e == hipSuccess) e = hipMemcpy(c->tab, tabh, sizeof(tabh), hipMemcpyHostToDevice);
         if (e != hipSuccess) {
             if (c->grid) (void)hipFree(c->grid);
+            if (c->grids) (void)hipFree(c->grids);
             if (c->tab) (void)hipFree(c->tab);
             if (c->stream) (void)hipStreamDestroy(c->stream);
             delete c;
@@ -514,6 +550,7 @@ int okf_ctx_destroy(okf_ctx *c) {
         (void)hipSetDevice(c->device);
         if (hipStreamSynchronize(c->stream) != hipSuccess) st = OKF_E_HIP;
         (void)hipFree(c->grid);
+        (void)hipFree(c->grids);
         (void)hipFree(c->tab);
         if (c->xh) (void)hipFree(c->xh);
         if (c->part) (void)hipFree(c->part);

@@ -1,7 +1,8 @@
 /*
  * okf_quant.h -- C ABI of the MI355X (gfx950) quantized weight x activation
  * path: fused dequantize-and-dot for GGUF Q8_0, Q4_K, IQ2_XXS and the Bonsai
- * ternary Q2_0 blocks, plus Q4_0, IQ4_NL, Q5_K, Q6_K and IQ4_XS.
+ * ternary Q2_0 blocks, plus Q4_0, IQ4_NL, Q5_K, Q6_K, IQ4_XS, IQ2_XS, IQ2_S,
+ * IQ3_XXS, IQ3_S, IQ1_S and IQ1_M.
  *
  * This ABI is the drop-in boundary for the reference's GPU dispatch surface
  * (LLM/Base/MetalEnc.swift) and the weight reference it takes
@@ -52,6 +53,12 @@ enum {
     OKF_TYPE_Q5_K = 13,
     OKF_TYPE_Q6_K = 14,
     OKF_TYPE_IQ4_XS = 23,
+    OKF_TYPE_IQ2_XS = 17,
+    OKF_TYPE_IQ3_XXS = 18,
+    OKF_TYPE_IQ1_S = 19,
+    OKF_TYPE_IQ3_S = 21,
+    OKF_TYPE_IQ2_S = 22,
+    OKF_TYPE_IQ1_M = 29,
     OKF_TYPE_IQ2_XXS = 16,
     OKF_TYPE_Q2_0 = 42
 };
