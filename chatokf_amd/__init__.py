@@ -16,7 +16,7 @@ import ctypes
 import os
 
 from .formats import (Q8_0, Q4_K, IQ2_XXS, Q2_0, Q4_0, IQ4_NL, Q5_K, Q6_K, IQ4_XS, IQ2_XS, IQ2_S, IQ3_XXS,  # noqa
-                      IQ3_S, IQ1_S, IQ1_M, NAMES, BY_NAME, block_elems, row_bytes)
+                      IQ3_S, IQ1_S, IQ1_M, F32, F16, BF16, Q2_K, Q3_K, NAMES, BY_NAME, block_elems, row_bytes)
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("OKF_LIB") or os.path.join(HERE, "libokf_quant.so")
@@ -362,6 +362,6 @@ class GGUF:
 
 __all__ = [
     "Q8_0", "Q4_K", "IQ2_XXS", "Q2_0", "Q4_0", "IQ4_NL", "Q5_K", "Q6_K", "IQ4_XS", "IQ2_XS", "IQ2_S", "IQ3_XXS", "IQ3_S",
-    "IQ1_S", "IQ1_M", "NAMES", "BY_NAME", "block_elems", "row_bytes",
+    "IQ1_S", "IQ1_M", "F32", "F16", "BF16", "Q2_K", "Q3_K", "NAMES", "BY_NAME", "block_elems", "row_bytes",
     "QuantTensor", "Enc", "OkfError", "OkfWeight", "OkfGGUFTensor", "GGUF", "lib", "EXPORTS", "LIB_PATH",
 ]

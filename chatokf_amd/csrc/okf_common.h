@@ -7,13 +7,17 @@ namespace okf {
 
 enum Fmt : int {
     Q4_0 = 2, Q8_0 = 8, Q4_K = 12, Q5_K = 13, Q6_K = 14, IQ2_XXS = 16, IQ2_XS = 17, IQ3_XXS = 18, IQ1_S = 19,
-    IQ4_NL = 20, IQ3_S = 21, IQ2_S = 22, IQ4_XS = 23, IQ1_M = 29, Q2_0 = 42
+    IQ4_NL = 20, IQ3_S = 21, IQ2_S = 22, IQ4_XS = 23, IQ1_M = 29, Q2_0 = 42,
+    F32 = 0, F16 = 1, BF16 = 30, Q2_K = 10, Q3_K = 11
 };
 
-// The grid formats past IQ2_XXS: decoded through tables in device memory
-// (one buffer, byte offsets below) by a generic fp32 matvec.
+// The grid formats past IQ2_XXS (decoded through tables in device memory:
+// one buffer, byte offsets below), the small K-quants Q2_K / Q3_K and the
+// plain f32 / f16 / bf16 weights take a generic matvec: the bit-exact
+// decoder, then fp32 products.
 __host__ __device__ constexpr bool grid_fmt(int f) {
-    return f == IQ2_XS || f == IQ2_S || f == IQ3_XXS || f == IQ3_S || f == IQ1_S || f == IQ1_M;
+    return f == IQ2_XS || f == IQ2_S || f == IQ3_XXS || f == IQ3_S || f == IQ1_S || f == IQ1_M || f == Q2_K ||
+           f == Q3_K || f == F32 || f == F16 || f == BF16;
 }
 constexpr uint32_t GT_IQ2XS = 0, GT_IQ2S = 4096, GT_IQ3XXS = 12288, GT_IQ3S = 13312, GT_IQ1S = 15360,
                    GT_BYTES = 23552;
@@ -23,10 +27,11 @@ constexpr uint32_t GT_IQ2XS = 0, GT_IQ2S = 4096, GT_IQ3XXS = 12288, GT_IQ3S = 13
 __host__ __device__ constexpr uint32_t block_bytes(int f) {
     return f == Q8_0 ? 34 : f == Q2_0 ? 34 : f == Q4_K ? 144 : (f == Q4_0 || f == IQ4_NL) ? 18
          : f == Q5_K ? 176 : f == Q6_K ? 210 : f == IQ4_XS ? 136 : f == IQ2_XS ? 74 : f == IQ2_S ? 82
-         : f == IQ3_XXS ? 98 : f == IQ3_S ? 110 : f == IQ1_S ? 50 : f == IQ1_M ? 56 : 66;
+         : f == IQ3_XXS ? 98 : f == IQ3_S ? 110 : f == IQ1_S ? 50 : f == IQ1_M ? 56 : f == Q2_K ? 84
+         : f == Q3_K ? 110 : f == F32 ? 128 : (f == F16 || f == BF16) ? 64 : 66;
 }
 __host__ __device__ constexpr uint32_t block_elems(int f) {
-    return (f == Q8_0 || f == Q4_0 || f == IQ4_NL) ? 32 : f == Q2_0 ? 128 : 256;
+    return (f == Q8_0 || f == Q4_0 || f == IQ4_NL || f == F32 || f == F16 || f == BF16) ? 32 : f == Q2_0 ? 128 : 256;
 }
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));

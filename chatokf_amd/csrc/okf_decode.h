@@ -326,6 +326,82 @@ __device__ __forceinline__ void decode_unit_iq1(const uint8_t *row, uint32_t u, 
     }
 }
 
+// KQuant.q2K (LLM/Quantize/KQuants.swift:9-36), 32-weight group j = u & 7 of
+// superblock u >> 3 ({u8 scales[16]; u8 qs[64]; half d, dmin}): n = j / 4,
+// bit field 2 (j % 4) of code bytes 16 + 32 n .., scale bytes 2 j, 2 j + 1
+// (16 weights each); w = (d * (sc & 15)) * q - dmin * (sc >> 4).
+__device__ __forceinline__ void decode_unit_q2_k(const uint8_t *row, uint32_t u, float *w) {
+    const uint8_t *b = row + (uint64_t)(u >> 3) * 84;
+    const uint32_t j = u & 7, n = j >> 2, sh = 2 * (j & 3);
+    const float d = h2f(ldu<uint16_t>(b + 80)), dmin = h2f(ldu<uint16_t>(b + 82));
+    uint32_t q[8];
+    *(uint4 *)&q[0] = ldu<uint4>(b + 16 + 32 * n);
+    *(uint4 *)&q[4] = ldu<uint4>(b + 32 + 32 * n);
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const uint32_t sc = b[2 * j + h];
+        const float dl = d * (float)(sc & 0xF), ml = dmin * (float)(sc >> 4);
+#pragma unroll
+        for (int l = 0; l < 16; l++)
+            w[16 * h + l] = dl * (float)((byte_of(q[(16 * h + l) >> 2], l & 3) >> sh) & 3) - ml;
+    }
+}
+
+// KQuant.q3K (LLM/Quantize/KQuants.swift:38-83), group j = u & 7 ({u8
+// hmask[32]; u8 qs[64]; u8 scales[12]; half d}): scale i = 2 j + h has its
+// low nibble in byte i (i < 8) or the high nibble of byte i - 8 and its top
+// bits at 2 (i / 4) of byte 8 + i % 4 (the reference's aux shuffle);
+// w = (d * (scale - 32)) * (q - (hmask bit n * 4 + j % 4 of byte l ? 0 : 4)).
+__device__ __forceinline__ void decode_unit_q3_k(const uint8_t *row, uint32_t u, float *w) {
+    const uint8_t *b = row + (uint64_t)(u >> 3) * 110;
+    const uint32_t j = u & 7, n = j >> 2, sh = 2 * (j & 3), hb = 4 * n + (j & 3);
+    const float dall = h2f(ldu<uint16_t>(b + 108));
+    uint32_t q[8], hm[8];
+    *(uint4 *)&q[0] = ldu<uint4>(b + 32 + 32 * n);
+    *(uint4 *)&q[4] = ldu<uint4>(b + 48 + 32 * n);
+    *(uint4 *)&hm[0] = ldu<uint4>(b);
+    *(uint4 *)&hm[4] = ldu<uint4>(b + 16);
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const uint32_t i = n * 8 + (j & 3) * 2 + h;
+        const uint32_t lo = (b[96 + (i & 7)] >> (4 * (i >> 3))) & 0xF, hi = (b[104 + (i & 3)] >> (2 * (i >> 2))) & 3;
+        const float dl = dall * (float)((int)(lo | (hi << 4)) - 32);
+#pragma unroll
+        for (int l = 0; l < 16; l++) {
+            const uint32_t at = 16 * h + l;
+            const float bump = (byte_of(hm[at >> 2], at & 3) >> hb) & 1 ? 0.0f : 4.0f;
+            w[at] = dl * ((float)((byte_of(q[at >> 2], at & 3) >> sh) & 3) - bump);
+        }
+    }
+}
+
+// GQ.element (LLM/Gemma/Gemma4Quant.swift:302-316): 32 plain weights.
+template <int F>
+__device__ __forceinline__ void decode_unit_dense(const uint8_t *row, uint32_t u, float *w) {
+    if constexpr (F == F32) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint4 v = ldu<uint4>(row + (uint64_t)u * 128 + 16 * i);
+            w[4 * i] = __builtin_bit_cast(float, v.x);
+            w[4 * i + 1] = __builtin_bit_cast(float, v.y);
+            w[4 * i + 2] = __builtin_bit_cast(float, v.z);
+            w[4 * i + 3] = __builtin_bit_cast(float, v.w);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint4 v = ldu<uint4>(row + (uint64_t)u * 64 + 16 * i);
+            const uint32_t d4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t lo = d4[k] & 0xFFFF, hi = d4[k] >> 16;
+                w[8 * i + 2 * k] = F == F16 ? h2f((uint16_t)lo) : __builtin_bit_cast(float, lo << 16);
+                w[8 * i + 2 * k + 1] = F == F16 ? h2f((uint16_t)hi) : __builtin_bit_cast(float, hi << 16);
+            }
+        }
+    }
+}
+
 // gt: the grid tables of the grid formats (GT_* offsets), in device memory
 template <int F>
 __device__ __forceinline__ void decode_unit(const uint8_t *row, uint32_t u, float *w,
@@ -341,6 +417,9 @@ __device__ __forceinline__ void decode_unit(const uint8_t *row, uint32_t u, floa
     else if constexpr (F == IQ2_XS || F == IQ2_S) decode_unit_iq2_xs_s<F == IQ2_S>(row, u, w, gt);
     else if constexpr (F == IQ3_XXS || F == IQ3_S) decode_unit_iq3<F == IQ3_S>(row, u, w, gt);
     else if constexpr (F == IQ1_S || F == IQ1_M) decode_unit_iq1<F == IQ1_M>(row, u, w, gt);
+    else if constexpr (F == Q2_K) decode_unit_q2_k(row, u, w);
+    else if constexpr (F == Q3_K) decode_unit_q3_k(row, u, w);
+    else if constexpr (F == F32 || F == F16 || F == BF16) decode_unit_dense<F>(row, u, w);
     else decode_unit_iq2_xxs(row, u, w, grid);
 }
 

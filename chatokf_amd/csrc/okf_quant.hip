@@ -411,6 +411,11 @@ void launch_embed(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_
     case IQ3_S: fn<IQ3_S>(__VA_ARGS__); break;              \
     case IQ1_S: fn<IQ1_S>(__VA_ARGS__); break;              \
     case IQ1_M: fn<IQ1_M>(__VA_ARGS__); break;              \
+    case Q2_K: fn<Q2_K>(__VA_ARGS__); break;                \
+    case Q3_K: fn<Q3_K>(__VA_ARGS__); break;                \
+    case F32: fn<F32>(__VA_ARGS__); break;                  \
+    case F16: fn<F16>(__VA_ARGS__); break;                  \
+    case BF16: fn<BF16>(__VA_ARGS__); break;                \
     default: fn<IQ2_XXS>(__VA_ARGS__); break;               \
     }
 
@@ -450,6 +455,11 @@ int run_gemm(okf_ctx *c, const okf_weight *w, const float *X, uint32_t N, float 
         case IQ3_S: st = launch_gemm<IQ3_S>(c, W, rb, w->K, w->M, X, N, Y); break;
         case IQ1_S: st = launch_gemm<IQ1_S>(c, W, rb, w->K, w->M, X, N, Y); break;
         case IQ1_M: st = launch_gemm<IQ1_M>(c, W, rb, w->K, w->M, X, N, Y); break;
+        case Q2_K: st = launch_gemm<Q2_K>(c, W, rb, w->K, w->M, X, N, Y); break;
+        case Q3_K: st = launch_gemm<Q3_K>(c, W, rb, w->K, w->M, X, N, Y); break;
+        case F32: st = launch_gemm<F32>(c, W, rb, w->K, w->M, X, N, Y); break;
+        case F16: st = launch_gemm<F16>(c, W, rb, w->K, w->M, X, N, Y); break;
+        case BF16: st = launch_gemm<BF16>(c, W, rb, w->K, w->M, X, N, Y); break;
         default: st = launch_gemm<IQ2_XXS>(c, W, rb, w->K, w->M, X, N, Y); break;
         }
         if (st) return st;
@@ -570,6 +580,10 @@ int okf_ctx_stream(okf_ctx *c, void **stream) {
 int okf_row_bytes(int32_t type, uint64_t n, uint64_t *out) {
     if (!out) return OKF_E_ARG;
     if (!supported(type)) return OKF_E_TYPE;
+    if (type == F32 || type == F16 || type == BF16) {  // any n, as GGUF.rowByteCount
+        *out = n * (type == F32 ? 4 : 2);
+        return OKF_OK;
+    }
     if (n % block_elems(type)) return OKF_E_SHAPE;
     *out = n / block_elems(type) * block_bytes(type);
     return OKF_OK;

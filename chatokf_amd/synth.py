@@ -26,7 +26,7 @@ from __future__ import annotations
 import numpy as np
 
 from .formats import (Q8_0, Q2_0, Q4_K, IQ2_XXS, Q4_0, IQ4_NL, Q5_K, Q6_K, IQ4_XS, IQ2_XS, IQ2_S, IQ3_XXS,
-                      IQ3_S, IQ1_S, IQ1_M, row_bytes)
+                      IQ3_S, IQ1_S, IQ1_M, F32, F16, BF16, Q2_K, Q3_K, row_bytes)
 
 _A = 6364136223846793005
 _C = 1442695040888963407
@@ -205,9 +205,38 @@ def iq1_m(M: int, K: int, seed: int, d_range=(1e-3, 1e-2)) -> np.ndarray:
     return blk.reshape(-1)
 
 
+def _d_last(nbytes, nd):
+    """256-weight blocks of `nbytes` with `nd` fp16 scales ~ U(d_range) at the
+    end (Q2_K: d, dmin; Q3_K: d), the rest uniform bytes."""
+    def gen(M: int, K: int, seed: int, d_range=(1e-3, 1e-2)) -> np.ndarray:
+        nb = M * (K // 256)
+        g = LCG(seed)
+        blk = np.empty((nb, nbytes), np.uint8)
+        blk[:, :nbytes - 2 * nd] = g.bytes(nb * (nbytes - 2 * nd)).reshape(nb, nbytes - 2 * nd)
+        for i in range(nd):
+            blk[:, nbytes - 2 * (nd - i):nbytes - 2 * (nd - i) + 2] = _f16_bytes(g.f16(*d_range, nb))
+        return blk.reshape(-1)
+    gen.__doc__ = f"M rows of {nbytes}-byte K-quant superblocks: {nd} fp16 scale(s) at the end, the rest uniform."
+    return gen
+
+
+def dense(kind):
+    """M rows of plain weights (f32, f16 or bf16): N(0, 1) / 16 from the LCG."""
+    def gen(M: int, K: int, seed: int) -> np.ndarray:
+        v = (LCG(seed).normal(M * K) / 16).astype(np.float32)
+        if kind == "f32":
+            return v.view(np.uint8)
+        if kind == "f16":
+            return v.astype(np.float16).view(np.uint8)
+        return (v.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8)  # bf16: the upper half
+    return gen
+
+
 GENERATORS = {Q8_0: q8_0, Q2_0: q2_0, Q4_K: q4_k, IQ2_XXS: iq2_xxs, Q4_0: nibble32, IQ4_NL: nibble32,
               Q5_K: q5_k, Q6_K: q6_k, IQ4_XS: iq4_xs, IQ2_XS: _d_first(74), IQ2_S: _d_first(82),
-              IQ3_XXS: _d_first(98), IQ3_S: _d_first(110), IQ1_S: _d_first(50), IQ1_M: iq1_m}
+              IQ3_XXS: _d_first(98), IQ3_S: _d_first(110), IQ1_S: _d_first(50), IQ1_M: iq1_m,
+              Q2_K: _d_last(84, 2), Q3_K: _d_last(110, 1), F32: dense("f32"), F16: dense("f16"),
+              BF16: dense("bf16")}
 
 
 def weights(ggml_type: int, M: int, K: int, seed: int) -> np.ndarray:

@@ -2,7 +2,8 @@
  * okf_quant.h -- C ABI of the MI355X (gfx950) quantized weight x activation
  * path: fused dequantize-and-dot for GGUF Q8_0, Q4_K, IQ2_XXS and the Bonsai
  * ternary Q2_0 blocks, plus Q4_0, IQ4_NL, Q5_K, Q6_K, IQ4_XS, IQ2_XS, IQ2_S,
- * IQ3_XXS, IQ3_S, IQ1_S and IQ1_M.
+ * IQ3_XXS, IQ3_S, IQ1_S, IQ1_M, Q2_K and Q3_K, and plain f32 / f16 / bf16
+ * weights (whose kernels take K a multiple of 32).
  *
  * This ABI is the drop-in boundary for the reference's GPU dispatch surface
  * (LLM/Base/MetalEnc.swift) and the weight reference it takes
@@ -59,6 +60,11 @@ enum {
     OKF_TYPE_IQ3_S = 21,
     OKF_TYPE_IQ2_S = 22,
     OKF_TYPE_IQ1_M = 29,
+    OKF_TYPE_Q2_K = 10,
+    OKF_TYPE_Q3_K = 11,
+    OKF_TYPE_F32 = 0,
+    OKF_TYPE_F16 = 1,
+    OKF_TYPE_BF16 = 30,
     OKF_TYPE_IQ2_XXS = 16,
     OKF_TYPE_Q2_0 = 42
 };
@@ -87,7 +93,8 @@ int okf_ctx_destroy(okf_ctx *ctx);
 /* The hipStream_t the context launches on (for events / interop). */
 int okf_ctx_stream(okf_ctx *ctx, void **stream);
 
-/* GGUF.rowByteCount (LLM/Base/GGUF.swift:160-188) for the four types. */
+/* GGUF.rowByteCount (LLM/Base/GGUF.swift:160-188) for the types above: n a
+ * whole number of blocks, or any n for f32 / f16 / bf16. */
 int okf_row_bytes(int32_t ggml_type, uint64_t n, uint64_t *out);
 
 /* MetalEnc.gemv (MetalEnc.swift:84-93): y[M] = W x[K].

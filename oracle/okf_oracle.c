@@ -76,6 +76,10 @@ static int block_geom(int32_t type, uint32_t *elems, uint32_t *bytes) {
     case OKF_REF_IQ3_S: *elems = 256; *bytes = 110; return 0;
     case OKF_REF_IQ1_S: *elems = 256; *bytes = 50; return 0;
     case OKF_REF_IQ1_M: *elems = 256; *bytes = 56; return 0;
+    case OKF_REF_Q2_K: *elems = 256; *bytes = 84; return 0;
+    case OKF_REF_Q3_K: *elems = 256; *bytes = 110; return 0;
+    case OKF_REF_F32: *elems = 32; *bytes = 128; return 0;
+    case OKF_REF_F16: case OKF_REF_BF16: *elems = 32; *bytes = 64; return 0;
     case OKF_REF_IQ2_XXS: *elems = 256; *bytes = 66; return 0;
     default: return -1;
     }
@@ -174,6 +178,69 @@ static void dq_q4_k_block(const uint8_t *b, float *out) {
         qoff += 32;
         isc += 2;
     }
+}
+
+/* KQuant.q2K, LLM/Quantize/KQuants.swift:9-36:
+ * { u8 scales[16]; u8 qs[64]; half d; half dmin } */
+static void dq_q2_k_block(const uint8_t *b, float *out) {
+    float d = ldh(b + 80), dmin = ldh(b + 82);
+    int y = 0, qoff = 16, isc = 0;
+    for (int n = 0; n < 2; n++) {
+        for (int shift = 0; shift < 8; shift += 2)
+            for (int half = 0; half < 2; half++) {
+                uint8_t sc = b[isc++];
+                float dl = d * (float)(sc & 0xF), ml = dmin * (float)(sc >> 4);
+                for (int l = 0; l < 16; l++) out[y++] = dl * (float)((b[qoff + half * 16 + l] >> shift) & 3) - ml;
+            }
+        qoff += 32;
+    }
+}
+
+/* KQuant.q3K, LLM/Quantize/KQuants.swift:38-83:
+ * { u8 hmask[32]; u8 qs[64]; u8 scales[12]; half d }; the 16 6-bit scales
+ * are unpacked from the 12 bytes as the reference's aux shuffle does */
+static void dq_q3_k_block(const uint8_t *b, float *out) {
+    float dall = ldh(b + 108);
+    uint32_t aux[4] = {ld32(b + 96), ld32(b + 100), ld32(b + 104), 0};
+    const uint32_t km1 = 0x03030303u, km2 = 0x0f0f0f0fu, tmp = aux[2];
+    aux[2] = ((aux[0] >> 4) & km2) | (((tmp >> 4) & km1) << 4);
+    aux[3] = ((aux[1] >> 4) & km2) | (((tmp >> 6) & km1) << 4);
+    aux[0] = (aux[0] & km2) | (((tmp >> 0) & km1) << 4);
+    aux[1] = (aux[1] & km2) | (((tmp >> 2) & km1) << 4);
+    int8_t scales[16];
+    for (int i = 0; i < 4; i++)
+        for (int j = 0; j < 4; j++) scales[i * 4 + j] = (int8_t)((aux[i] >> (8 * j)) & 0xFF);
+    int y = 0, qoff = 32, isc = 0;
+    uint8_t m = 1;
+    for (int n = 0; n < 2; n++) {
+        for (int shift = 0; shift < 8; shift += 2) {
+            for (int half = 0; half < 2; half++) {
+                float dl = dall * (float)((int)scales[isc++] - 32);
+                for (int l = 0; l < 16; l++) {
+                    int at = half * 16 + l;
+                    float bump = (b[at] & m) ? 0.0f : 4.0f;
+                    out[y++] = dl * ((float)((b[qoff + at] >> shift) & 3) - bump);
+                }
+            }
+            m <<= 1;
+        }
+        qoff += 32;
+    }
+}
+
+/* GQ.element, LLM/Gemma/Gemma4Quant.swift:302-316: f32, f16 and bf16 (the
+ * upper half of an f32) weights */
+static float dense_element(int32_t type, const uint8_t *p, uint64_t i) {
+    if (type == OKF_REF_F32) {
+        float v;
+        memcpy(&v, p + i * 4, 4);
+        return v;
+    }
+    if (type == OKF_REF_F16) return okf_ref_f16_to_f32(ld16(p + i * 2));
+    uint32_t bits = (uint32_t)ld16(p + i * 2) << 16;
+    float v;
+    memcpy(&v, &bits, 4);
+    return v;
 }
 
 /* KQuant.q5K, LLM/Quantize/KQuants.swift:127-155: as q4K with a fifth bit
@@ -410,6 +477,8 @@ static sb_decode_fn sb_decoder(int32_t type) {
     case OKF_REF_IQ3_S: return dq_iq3_s_block;
     case OKF_REF_IQ1_S: return dq_iq1_s_block;
     case OKF_REF_IQ1_M: return dq_iq1_m_block;
+    case OKF_REF_Q2_K: return dq_q2_k_block;
+    case OKF_REF_Q3_K: return dq_q3_k_block;
     case OKF_REF_IQ2_XXS: return dq_iq2_xxs_block;
     default: return NULL;
     }
@@ -423,6 +492,9 @@ int okf_ref_dequant(int32_t type, const uint8_t *p, uint64_t n, float *out) {
     case OKF_REF_Q2_0: dq_q2_0(p, n, out); break;
     case OKF_REF_Q4_0: dq_q4_0(p, n, out); break;
     case OKF_REF_IQ4_NL: dq_iq4_nl(p, n, out); break;
+    case OKF_REF_F32: case OKF_REF_F16: case OKF_REF_BF16:
+        for (uint64_t i = 0; i < n; i++) out[i] = dense_element(type, p, i);
+        break;
     default: { /* superBlockGather, Gemma4Quant.swift:351-360 */
         sb_decode_fn dec = sb_decoder(type);
         for (uint64_t b = 0; b < n / 256; b++) dec(p + b * bytes, out + b * 256);
@@ -477,6 +549,15 @@ static float row_nibble32(const job_t *j, uint32_t m) {
         }
         acc += a * d;
     }
+    return acc;
+}
+
+/* GQ.denseMatvec, LLM/Gemma/Gemma4Quant.swift:281-300: acc += w_i * x_i over
+ * the whole row, in order. */
+static float row_dense(const job_t *j, uint32_t m) {
+    const uint8_t *p = j->w + (uint64_t)m * j->row_bytes;
+    float acc = 0;
+    for (uint32_t i = 0; i < j->K; i++) acc += dense_element(j->type, p, i) * j->x[i];
     return acc;
 }
 
@@ -562,6 +643,7 @@ static void *run_slice(void *arg) {
         case OKF_REF_Q8_0: v = row_q8_0(j, m); break;
         case OKF_REF_Q2_0: v = row_q2_0(j, m); break;
         case OKF_REF_Q4_0: case OKF_REF_IQ4_NL: v = row_nibble32(j, m); break;
+        case OKF_REF_F32: case OKF_REF_F16: case OKF_REF_BF16: v = row_dense(j, m); break;
         default: v = row_superblock(j, m); break;
         }
         j->y[m] = v;

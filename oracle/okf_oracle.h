@@ -43,6 +43,11 @@ enum {
     OKF_REF_IQ3_S = 21,
     OKF_REF_IQ2_S = 22,
     OKF_REF_IQ1_M = 29,
+    OKF_REF_F32 = 0,
+    OKF_REF_F16 = 1,
+    OKF_REF_BF16 = 30,
+    OKF_REF_Q2_K = 10,
+    OKF_REF_Q3_K = 11,
     OKF_REF_IQ2_XXS = 16,
     OKF_REF_Q2_0 = 42,
 };

@@ -16,7 +16,7 @@ import pytest
 import oracle
 from chatokf_amd import synth
 from chatokf_amd.formats import (Q8_0, Q2_0, Q4_K, IQ2_XXS, Q4_0, IQ4_NL, Q5_K, Q6_K, IQ4_XS, IQ2_XS, IQ2_S,  # noqa
-                                 IQ3_XXS, IQ3_S, IQ1_S, IQ1_M, NAMES, row_bytes)
+                                 IQ3_XXS, IQ3_S, IQ1_S, IQ1_M, F32, F16, BF16, Q2_K, Q3_K, NAMES, row_bytes)
 
 torch = pytest.importorskip("torch")
 import chatokf_amd as ok  # noqa: E402
@@ -71,7 +71,7 @@ def run_gemm(enc, t, M, K, w, X, tile=False):
 # ------------------------------------------------------------------ dequant
 DQ_CASES = [(Q8_0, 6, 2048), (Q2_0, 6, 6144), (Q4_K, 4, 5120), (IQ2_XXS, 4, 5120), (Q4_0, 6, 4096),
             (IQ4_NL, 6, 4096), (Q5_K, 4, 5120), (Q6_K, 4, 5120), (IQ4_XS, 4, 5120)] + \
-    [(t, 4, 5120) for t in (IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M)]
+    [(t, 4, 5120) for t in (IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M, Q2_K, Q3_K, F32, F16, BF16)]
 
 
 @pytest.mark.parametrize("t,M,K", DQ_CASES, ids=[NAMES[c[0]] for c in DQ_CASES])
@@ -133,7 +133,8 @@ EDGE = [(Q8_0, 1, 32), (Q8_0, 3, 96), (Q8_0, 4099, 2080), (Q2_0, 5, 128), (Q2_0,
         (Q4_0, 1, 32), (Q4_0, 4099, 2080), (Q4_0, 2048, 4096), (IQ4_NL, 3, 96), (IQ4_NL, 4099, 2080),
         (IQ4_NL, 2048, 4096), (Q5_K, 1, 256), (Q5_K, 4101, 2304), (Q6_K, 3, 256), (Q6_K, 4099, 1280),
         (IQ4_XS, 2, 512), (IQ4_XS, 4103, 2304)] + \
-    [(t, M, K) for t in (IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M) for M, K in ((3, 256), (4101, 1280))]
+    [(t, M, K) for t in (IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M, Q2_K, Q3_K) for M, K in ((3, 256), (4101, 1280))] + \
+    [(t, M, K) for t in (F32, F16, BF16) for M, K in ((3, 32), (4101, 1056))]
 
 
 def fp16_bound(t, w, K, M, x):
@@ -183,7 +184,7 @@ def test_gemv_weight_offset(enc):
 
 # ------------------------------------------------------------------ narrow N = 2..5
 @pytest.mark.parametrize("t", [Q8_0, Q2_0, Q4_K, IQ2_XXS, Q4_0, IQ4_NL, Q5_K, Q6_K, IQ4_XS, IQ2_XS, IQ2_S,
-                               IQ3_XXS, IQ3_S, IQ1_S, IQ1_M], ids=lambda t: NAMES[t])
+                               IQ3_XXS, IQ3_S, IQ1_S, IQ1_M, Q2_K, Q3_K, F32, F16, BF16], ids=lambda t: NAMES[t])
 @pytest.mark.parametrize("N", [2, 3, 4, 5])
 def test_narrow_matches_oracle_and_gemv(enc, t, N):
     M, K = 1030, 2048
@@ -309,7 +310,8 @@ def test_silu_mul_matches_oracle(enc):
 
 SILU_CASES = [(Q2_0, 2048, 6144, 1102), (Q8_0, 300, 2048, 81), (Q4_K, 260, 2304, 82), (IQ4_NL, 96, 512, 85),
               (IQ2_XXS, 129, 1536, 83), (Q2_0, 130, 1024, 84), (Q5_K, 100, 768, 86), (Q6_K, 70, 512, 87),
-              (IQ4_XS, 90, 1024, 88), (IQ2_S, 70, 512, 89), (IQ1_M, 50, 768, 90)]
+              (IQ4_XS, 90, 1024, 88), (IQ2_S, 70, 512, 89), (IQ1_M, 50, 768, 90), (Q3_K, 60, 512, 91),
+              (BF16, 40, 1024, 92)]
 
 
 @pytest.mark.parametrize("t,M,K,seed", SILU_CASES)
@@ -370,7 +372,8 @@ def test_parallel_group_matches_single_calls(enc):
 TILE = [(Q8_0, 300, 2048, 37), (Q2_0, 130, 1024, 129), (Q4_K, 260, 2304, 77), (IQ2_XXS, 129, 1536, 6),
         (Q4_K, 1, 256, 64), (Q8_0, 5, 96, 200), (Q4_K, 4224, 256, 512), (Q4_K, 1000, 512, 300),
         (Q4_0, 300, 2048, 37), (IQ4_NL, 130, 1024, 70), (Q5_K, 200, 1024, 40), (Q6_K, 129, 768, 33),
-        (IQ4_XS, 260, 1280, 90)] + [(t, 130, 768, 41) for t in (IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M)]
+        (IQ4_XS, 260, 1280, 90)] + [(t, 130, 768, 41) for t in (IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M, Q2_K, Q3_K, F32,
+                                                                F16, BF16)]
 
 
 @pytest.mark.parametrize("t,M,K,N", TILE)
@@ -432,7 +435,7 @@ def test_injected_fault_launches_nothing(enc):
 
 # ------------------------------------------------------------------ embedding gather
 @pytest.mark.parametrize("t", [Q8_0, Q2_0, Q4_K, IQ2_XXS, Q4_0, IQ4_NL, Q5_K, Q6_K, IQ4_XS, IQ2_XS, IQ2_S,
-                               IQ3_XXS, IQ3_S, IQ1_S, IQ1_M], ids=lambda t: NAMES[t])
+                               IQ3_XXS, IQ3_S, IQ1_S, IQ1_M, Q2_K, Q3_K, F32, F16, BF16], ids=lambda t: NAMES[t])
 def test_embed_batch_bit_exact(enc, t):
     # embedBatch (MetalEnc.swift:1096-1146) vs the oracle's dequant of each row
     M, K = 300, 2048

@@ -15,7 +15,7 @@ import pytest
 import oracle
 from chatokf_amd import synth
 from chatokf_amd.formats import (Q8_0, Q2_0, Q4_K, IQ2_XXS, Q4_0, IQ4_NL, Q5_K, Q6_K, IQ4_XS, IQ2_XS, IQ2_S,  # noqa: E501
-                                 IQ3_XXS, IQ3_S, IQ1_S, IQ1_M)
+                                 IQ3_XXS, IQ3_S, IQ1_S, IQ1_M, F32, F16, BF16, Q2_K, Q3_K)
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 GOLD = json.load(open(os.path.join(ROOT, "tests", "golden", "iq2xxs_tables.json")))
@@ -281,6 +281,46 @@ def np_dequant(t, w, M, K):
         return out.reshape(M, K)
     if t in (IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M):
         return np.stack([_np_iq(t, w.reshape(M, -1)[m]) for m in range(M)])
+    if t == F32:
+        return w.view(np.float32).reshape(M, K).copy()
+    if t == F16:
+        return w.view(np.float16).astype(np.float32).reshape(M, K)
+    if t == BF16:
+        return (w.view(np.uint16).astype(np.uint32) << 16).view(np.float32).reshape(M, K)
+    if t == Q2_K:
+        b = w.reshape(M, K // 256, 84)
+        d = b[:, :, 80:82].copy().view(np.float16).astype(np.float32)
+        dm = b[:, :, 82:84].copy().view(np.float16).astype(np.float32)
+        sc = b[:, :, :16].astype(np.float32)
+        out = np.empty((M, K // 256, 2, 4, 2, 16), np.float32)
+        for n in range(2):
+            for s in range(4):
+                for h in range(2):
+                    i = n * 8 + s * 2 + h
+                    q = (b[:, :, 16 + 32 * n + 16 * h:32 + 32 * n + 16 * h] >> (2 * s)) & 3
+                    dl = d[..., 0] * (b[:, :, i] & 15).astype(np.float32)
+                    ml = dm[..., 0] * (b[:, :, i] >> 4).astype(np.float32)
+                    out[:, :, n, s, h] = dl[..., None] * q.astype(np.float32) - ml[..., None]
+        return out.reshape(M, K)
+    if t == Q3_K:
+        b = w.reshape(M, K // 256, 110).astype(np.int64)
+        d = w.reshape(M, K // 256, 110)[:, :, 108:110].copy().view(np.float16).astype(np.float32)[..., 0]
+        # the 16 6-bit scales: low nibble from byte i (i < 8) or the high
+        # nibble of byte i - 8, top two bits from byte 8 + i % 4 at 2 (i // 4)
+        sc = np.empty((M, K // 256, 16), np.int64)
+        for i in range(16):
+            lo = (b[:, :, 96 + (i % 8)] >> (4 * (i // 8))) & 15
+            hi = (b[:, :, 104 + i % 4] >> (2 * (i // 4))) & 3
+            sc[:, :, i] = (lo | (hi << 4)) - 32
+        out = np.empty((M, K // 256, 2, 4, 2, 16), np.float32)
+        for n in range(2):
+            for s in range(4):
+                for h in range(2):
+                    q = (b[:, :, 32 + 32 * n + 16 * h:48 + 32 * n + 16 * h] >> (2 * s)) & 3
+                    bump = np.where(b[:, :, 16 * h:16 * h + 16] & (1 << (4 * n + s)), 0, 4).astype(np.float32)
+                    dl = d * sc[:, :, n * 8 + s * 2 + h].astype(np.float32)
+                    out[:, :, n, s, h] = dl[..., None] * (q.astype(np.float32) - bump)
+        return out.reshape(M, K)
     if t in (Q4_0, IQ4_NL):
         b = w.reshape(M, K // 32, 18)
         d = b[:, :, :2].copy().view(np.float16).astype(np.float32)
@@ -369,7 +409,8 @@ IQ4NL_TABLE = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38,
 
 SMALL = [(Q8_0, 64, 256), (Q2_0, 64, 512), (Q4_K, 32, 512), (IQ2_XXS, 32, 512), (Q4_0, 64, 256),
          (IQ4_NL, 64, 256), (Q5_K, 32, 512), (Q6_K, 32, 512), (IQ4_XS, 32, 512), (IQ2_XS, 8, 512),
-         (IQ2_S, 8, 512), (IQ3_XXS, 8, 512), (IQ3_S, 8, 512), (IQ1_S, 8, 512), (IQ1_M, 8, 512)]
+         (IQ2_S, 8, 512), (IQ3_XXS, 8, 512), (IQ3_S, 8, 512), (IQ1_S, 8, 512), (IQ1_M, 8, 512),
+         (Q2_K, 16, 512), (Q3_K, 16, 512), (F32, 16, 256), (F16, 16, 256), (BF16, 16, 256)]
 
 
 @pytest.mark.parametrize("t,M,K", SMALL)
@@ -589,6 +630,34 @@ def test_grid_formats_known_answer():
     blk[48:56] = np.array([0x0000, 0x0000, 0xC000, 0x3000], np.uint16).view(np.uint8)
     w = oracle.dequant(IQ1_M, blk, 256)
     assert np.array_equal(w, np.full(256, f32(-0.875)))
+
+
+def test_q2_k_q3_k_dense_known_answer():
+    f32 = np.float32
+    # Q2_K, d = 1, dmin = 1/2: scale byte 0x13 -> dl = 3, ml = 1/2; codes
+    # 0..3 in the first byte's four 2-bit fields go to weights 0, 32, 64, 96
+    blk = np.zeros(84, np.uint8)
+    blk[0] = blk[2] = blk[4] = blk[6] = 0x13
+    blk[16] = 0b11100100  # codes 0, 1, 2, 3
+    blk[80:82], blk[82:84] = _f16(1.0), _f16(0.5)
+    w = oracle.dequant(Q2_K, blk, 256)
+    assert [w[0], w[32], w[64], w[96]] == [f32(-0.5), f32(2.5), f32(5.5), f32(8.5)]
+    assert w[1] == f32(-0.5) and w[16] == 0  # weights 16..31 take scale byte 1 = 0
+    # Q3_K, d = 1: scale 32 + 2 (low nibble 2, top bits 2) gives dl = 2;
+    # hmask bit set -> no bump, clear -> code - 4
+    blk = np.zeros(110, np.uint8)
+    blk[96] = 0x02
+    blk[104] = 0b10  # top bits of scale 0
+    blk[32] = 3
+    blk[0] = 1  # hmask bit 0 of weight 0
+    blk[108:110] = _f16(1.0)
+    w = oracle.dequant(Q3_K, blk, 256)
+    assert w[0] == f32(6) and w[1] == f32(-8)  # 2 * 3 and 2 * (0 - 4)
+    # dense: f16 1.5, bf16 0x3FC0 = 1.5, f32 as stored
+    assert oracle.dequant(F16, np.tile(_f16(1.5), 32), 32)[0] == f32(1.5)
+    assert oracle.dequant(BF16, np.tile(np.array([0xC0, 0x3F], np.uint8), 32), 32)[0] == f32(1.5)
+    v = np.arange(32, dtype=np.float32) / 7
+    assert np.array_equal(oracle.dequant(F32, v.view(np.uint8), 32), v)
 
 
 def test_iq4_nl_table_matches_reference_golden():
