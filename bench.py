@@ -281,7 +281,7 @@ def main():
             w_ = torch.rand(n, device="cuda", generator=g) + 0.5
             y_ = torch.empty(rows, n, device="cuda")
             fn, args_ = enc._lib.okf_add_rmsnorm_batch, (r_.data_ptr(), w_.data_ptr(), y_.data_ptr())
-            nbytes = (5 * rows + 1) * n * 4
+            nbytes = (4 * rows + 1) * n * 4  # x, r read; x, y written; w read once
 
             def call(i, xs_=xs_, nr=nr):
                 if fn(enc.h, xs_[i % nr].data_ptr(), *args_, n, rows, ctypes.c_float(1e-6)):
