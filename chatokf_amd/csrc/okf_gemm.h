@@ -408,31 +408,35 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_kernel(const uint8_t *__restr
         }
 }
 
-// Y of the split tiles: workgroup b sums float4 (b % 16) * 256 + t of split
-// tile b / 16 over its ks partials, in K order (all ks loads issued first).
-constexpr uint32_t QG_SUM_WG = QG_BM * QG_BN / (4 * 256);  // workgroups per tile
+// Y of the split tiles: workgroup b sums float4 (b % per-tile) * 256 + t of
+// split tile b / per-tile over its ks partials, in K order (all ks loads
+// issued first).  BM is the tile's row count (128 or 256), BN = 128.
+template <uint32_t BM>
 __global__ __launch_bounds__(256) void gemm_split_sum_kernel(const float *__restrict__ part,
                                                              float *__restrict__ Y, uint32_t M,
                                                              uint32_t N, GemmSplit sp) {
-    const uint32_t lt = blockIdx.x / QG_SUM_WG, tile = sp.full + lt;
-    const uint32_t e = ((blockIdx.x % QG_SUM_WG) * 256 + threadIdx.x) * 4;
-    const uint32_t nl = e / QG_BM, ml = e % QG_BM;
-    const uint32_t m = tile / sp.tiles_n * QG_BM + ml, n = tile % sp.tiles_n * QG_BN + nl;
+    constexpr uint32_t WG = BM * QG_BN / (4 * 256);  // workgroups per tile
+    const uint32_t lt = blockIdx.x / WG, tile = sp.full + lt;
+    const uint32_t e = ((blockIdx.x % WG) * 256 + threadIdx.x) * 4;
+    const uint32_t nl = e / BM, ml = e % BM;
+    const uint32_t m = tile / sp.tiles_n * BM + ml, n = tile % sp.tiles_n * QG_BN + nl;
     if (n >= N || m >= M) return;
-    const float *p0 = part + (uint64_t)lt * sp.ks * (QG_BM * QG_BN) + e;
-    float4 w[8];
+    const float *p0 = part + (uint64_t)lt * sp.ks * (BM * QG_BN) + e;
+    float4 v = *(const float4 *)p0;
+    for (uint32_t c0 = 1; c0 < sp.ks; c0 += 8) {
+        float4 w[8];
 #pragma unroll
-    for (uint32_t c = 0; c < 8; c++)
-        if (c < sp.ks) w[c] = *(const float4 *)(p0 + (uint64_t)c * (QG_BM * QG_BN));
-    float4 v = w[0];
+        for (uint32_t c = 0; c < 8; c++)
+            if (c0 + c < sp.ks) w[c] = *(const float4 *)(p0 + (uint64_t)(c0 + c) * (BM * QG_BN));
 #pragma unroll
-    for (uint32_t c = 1; c < 8; c++)
-        if (c < sp.ks) {
-            v.x += w[c].x;
-            v.y += w[c].y;
-            v.z += w[c].z;
-            v.w += w[c].w;
-        }
+        for (uint32_t c = 0; c < 8; c++)
+            if (c0 + c < sp.ks) {
+                v.x += w[c].x;
+                v.y += w[c].y;
+                v.z += w[c].z;
+                v.w += w[c].w;
+            }
+    }
     float *dst = Y + (uint64_t)n * M + m;
     if (m + 3 < M && (M & 3) == 0) {
         *(float4 *)dst = v;
@@ -441,6 +445,318 @@ __global__ __launch_bounds__(256) void gemm_split_sum_kernel(const float *__rest
         for (int k = 0; k < 4; k++)
             if (m + k < M) dst[k] = vv[k];
     }
+}
+
+constexpr int QW_BM = 256;
+
+// Tile and K range of workgroup blockIdx.x of a wide-tile launch (whole tiles
+// first, one per CU, then the split units; each XCD's whole tiles share one
+// N tile when 8 is a multiple of the N tiles).  K range [sb0, sb1) in
+// superblocks.  False when the workgroup has nothing to do.
+__device__ __forceinline__ bool wide_tile_of(const GemmSplit &sp, uint32_t sbs, uint32_t &tile, uint32_t &unit,
+                                             uint32_t &sb0, uint32_t &sb1, bool &split) {
+    const uint32_t xcd = blockIdx.x % 8, slot = blockIdx.x / 8;
+    split = slot >= sp.full_xcd;
+    sb0 = 0;
+    sb1 = sbs;
+    unit = 0;
+    if (!split) {
+        if (8 % sp.tiles_n == 0) {
+            const uint32_t nt = xcd % sp.tiles_n, mt = (xcd / sp.tiles_n) * sp.full_xcd + slot;
+            tile = mt * sp.tiles_n + nt;
+        } else {
+            tile = xcd * sp.full_xcd + slot;
+        }
+    } else {
+        unit = xcd * sp.units_xcd + (slot - sp.full_xcd);
+        if (unit >= sp.units) return false;
+        tile = sp.full + unit / sp.ks;
+        const uint32_t c = unit % sp.ks;
+        sb0 = c * sbs / sp.ks;
+        sb1 = (c + 1) * sbs / sp.ks;
+    }
+    return tile < sp.tiles;
+}
+
+// ------------------------------------------------------------------------
+// The same 256 x 128 tile with eight wavefronts (two per SIMD): wavefronts
+// 0-3 take the even superblocks of the K range and 4-7 the odd ones, each
+// with a 64-row x 128-token slice.  While one
+// wavefront of a SIMD waits (on its loads, the barrier or LDS), the other
+// issues.  At the end the odd half's accumulators are added to the even
+// half's through LDS (even + odd, a fixed order).  When the range has an odd
+// number of superblocks the odd half runs its last superblock with zero
+// scales (every weight 0), so both halves meet at every barrier.
+//
+// The activations go from memory straight to LDS (global_load_lds_dwordx4,
+// XD steps ahead, XD + 2 stages per half): a stage is 128 tokens x 64 k
+// fp16 without padding, token t's 16-byte chunk c (k = 8 c .. 8 c + 7) at
+// t * 128 + 16 * (c ^ ((t >> 1) & 7)), so that the 16 lanes of each
+// ds_read_b128 quarter hit 16 different 16-byte bank groups.  The weight
+// bytes come D steps ahead in registers.
+//
+// The LDS reads are written out in asm with explicit waits: the compiler
+// cannot tell the stage being filled by the direct loads from the one being
+// read, and would otherwise wait for every outstanding load before each read.
+template <int D, int XD>
+__global__ __launch_bounds__(512, 1) void gemm_q4k_w8_kernel(const uint8_t *__restrict__ W, uint64_t row_bytes,
+                                                          uint32_t K, uint32_t M,
+                                                          const _Float16 *__restrict__ Xh, uint32_t N,
+                                                          float *__restrict__ Y, GemmSplit sp) {
+    constexpr uint32_t NST = XD + 2, STAGE_B = QG_BN * QG_BK * 2;  // bytes per stage
+    static_assert(2 * NST * STAGE_B >= 4 * 64 * 64 * 4, "the reduction reuses the stages");
+    __shared__ __attribute__((aligned(1024))) uint8_t Bs[2][NST][STAGE_B];  // [K half][stage]
+    const uint32_t sbs = K / 256;
+    uint32_t tile, unit, sb0, sb1;
+    bool split;
+    if (!wide_tile_of(sp, sbs, tile, unit, sb0, sb1, split)) return;
+    const uint32_t nt = tile % sp.tiles_n, mt = tile / sp.tiles_n;
+    const uint32_t m0 = mt * QW_BM, n0 = nt * QG_BN;
+
+    const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6, h = lane >> 5;
+    // (read through the first lane: the compiler then knows they are uniform)
+    const uint32_t wu = __builtin_amdgcn_readfirstlane(wave), kh = wu >> 2, wr = wu & 3;
+    const uint32_t rm = m0 + wr * 64 + (lane & 31);
+    const uint8_t *w0 = W + (uint64_t)min(rm, M - 1) * row_bytes;
+    const uint8_t *w1 = W + (uint64_t)min(rm + 32, M - 1) * row_bytes;
+    // direct loads: instruction i of wavefront wr fills chunk
+    // (4 wr + i) * 64 + lane of the stage = token xt, position xp
+    const uint32_t xt0 = (wr * 4) * 8 + (lane >> 3), xp = lane & 7;
+    uint32_t xsrc[4];  // element offsets into Xh (N * K < 2^32)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t tok = xt0 + i * 8, c = xp ^ ((tok >> 1) & 7);
+        xsrc[i] = min(n0 + tok, N - 1) * K + 8 * c;
+    }
+    typedef __attribute__((address_space(3))) void lds_void;
+    lds_void *const xdst = (lds_void *)(&Bs[kh][0][0] + (wr * 4) * 1024);
+
+    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+    struct WRegs {
+        u32x4v h0, h1, q0, q1;
+    };
+    // local step l of this half: superblock sb0 + 2 (l / 4) + kh (clamped
+    // to the row, so every load is unconditional), code group l % 4
+    auto lsb = [&](uint32_t l) { return min(sb0 + 2 * (l >> 2) + kh, sbs - 1); };
+    // (written out, like every load of the loop: the compiler's own count
+    // of outstanding loads is lost once a direct-to-LDS load is in flight,
+    // and it would wait for all of them; the waits below are explicit)
+    auto fetch_w = [&](uint32_t l, WRegs &r) {
+        const uint64_t sbo = (uint64_t)lsb(l) * 144, qo = sbo + 16 + (l & 3) * 32 + 16 * h;
+        asm volatile("global_load_dwordx4 %0, %4, off\n\t"
+                     "global_load_dwordx4 %1, %5, off\n\t"
+                     "global_load_dwordx4 %2, %6, off\n\t"
+                     "global_load_dwordx4 %3, %7, off"
+                     : "=&v"(r.h0), "=&v"(r.h1), "=&v"(r.q0), "=&v"(r.q1)
+                     : "v"(w0 + sbo), "v"(w1 + sbo), "v"(w0 + qo), "v"(w1 + qo));
+    };
+    // stage l % NST <- activations of local step l (4 direct loads per lane)
+    auto fetch_x = [&](uint32_t l, uint32_t st) {
+        const uint32_t ko = lsb(l) * 256 + (l & 3) * QG_BK;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            __builtin_amdgcn_global_load_lds((const void *)(Xh + xsrc[i] + ko),
+                                             (lds_void *)((__attribute__((address_space(3))) uint8_t *)xdst +
+                                                          st * STAGE_B + i * 1024),
+                                             16, 0, 0);
+    };
+    auto dq_row = [&](const u32x4v hdr, const u32x4v qv, uint32_t g, float vf, u32x4v *a) {
+        // every loaded dword counts as used here: a dword that a group does
+        // not need would otherwise be reused as a temporary while its load
+        // is still in flight, and that write has to wait for the load
+        asm volatile("" ::"v"(hdr), "v"(qv));
+        uint32_t sc0, mn0, sc1, mn1;
+        q4k_scale_min_pair(make_uint4(hdr[0], hdr[1], hdr[2], hdr[3]), g, sc0, mn0, sc1, mn1);
+        const float d = h2f(hdr[0] & 0xFFFF) * vf, dmin = h2f(hdr[0] >> 16) * vf;
+        const half2v a0 = (half2v)(_Float16)(d * (float)sc0), o0 = (half2v)(_Float16)(-dmin * (float)mn0);
+        const half2v a1 = (half2v)(_Float16)(d * (float)sc1), o1 = (half2v)(_Float16)(-dmin * (float)mn1);
+        const half2v m1024 = (half2v)(_Float16)-1024.0f;
+        uint32_t lo[8], hi[8];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t v = qv[i];
+            const uint32_t p01 = __builtin_amdgcn_perm(v, v, 0x0C010C00u);
+            const uint32_t p23 = __builtin_amdgcn_perm(v, v, 0x0C030C02u);
+            const uint32_t l01 = gbfi(0x000F000Fu, p01), l23 = gbfi(0x000F000Fu, p23);
+            const uint32_t h01 = gbfi(0x000F000Fu, p01 >> 4), h23 = gbfi(0x000F000Fu, p23 >> 4);
+            auto dq = [&](uint32_t x, half2v sa_, half2v so) {
+                const half2v q = __builtin_bit_cast(half2v, x) + m1024;
+                return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, sa_, so));
+            };
+            lo[2 * i] = dq(l01, a0, o0);
+            lo[2 * i + 1] = dq(l23, a0, o0);
+            hi[2 * i] = dq(h01, a1, o1);
+            hi[2 * i + 1] = dq(h23, a1, o1);
+        }
+        a[0] = u32x4v{lo[0], lo[1], lo[2], lo[3]};
+        a[1] = u32x4v{lo[4], lo[5], lo[6], lo[7]};
+        a[2] = u32x4v{hi[0], hi[1], hi[2], hi[3]};
+        a[3] = u32x4v{hi[4], hi[5], hi[6], hi[7]};
+    };
+    // B reads: MFMA kk takes chunk 2 h + (kk & 1) + 4 (kk >> 1) of token
+    // 32 jn + lane % 32; jn and the stage are immediate offsets
+    const uint32_t swz = ((lane & 31) >> 1) & 7;
+    const uint32_t bbase =
+        (uint32_t)(uintptr_t)((__attribute__((address_space(3))) uint8_t *)&Bs[kh][0][0]) + (lane & 31) * 128;
+    uint32_t baddr[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) baddr[kk] = bbase + 16 * ((2 * h + (kk & 1) + 4 * (kk >> 1)) ^ swz);
+    auto read_b = [&](uint32_t addr, u32x4v *b) {
+        asm volatile("ds_read_b128 %0, %4\n\t"
+                     "ds_read_b128 %1, %4 offset:4096\n\t"
+                     "ds_read_b128 %2, %4 offset:8192\n\t"
+                     "ds_read_b128 %3, %4 offset:12288"
+                     : "=&v"(b[0]), "=&v"(b[1]), "=&v"(b[2]), "=&v"(b[3])
+                     : "v"(addr));
+    };
+
+    typedef float floatx16 __attribute__((ext_vector_type(16)));
+    floatx16 acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = floatx16{};
+
+    // Two halves in ping-pong.  Every wavefront runs the same steps (issue
+    // the activations of step t + XD, dequantize step t and issue its
+    // weights of step t + D, MFMAs of step t), but the even half meets the
+    // step's barrier before its dequant and the odd half after it.  Between
+    // two barriers the even half dequantizes while the odd half runs its
+    // MFMAs, and then the other way round, so each SIMD always has one
+    // wavefront in a VALU phase and one in an MFMA + LDS phase.  (Only the
+    // waits and the barrier sit in the branches: a branch holding loads or
+    // MFMAs would make the compiler copy their registers at the join.)
+    //
+    // The odd half issues step t + XD's activations before the barrier, while
+    // its partners may still read stage t - 1: hence XD + 2 stages.
+    // Counting loads issued later (8 per step: 4 direct, 4 weight): at the
+    // even half's barrier the activations of step t are followed by
+    // 8 XD - 4 loads, at the odd half's by 8 XD + 4; the weights of step t
+    // at its dequant by 8 D - 4.
+    static_assert(NST == XD + 2, "stages");
+    constexpr int WAIT_X0 = 8 * XD - 4, WAIT_X1 = 8 * XD + 4, WAIT_W = 8 * D - 4;
+    WRegs r[D];
+    constexpr int PRE = D > XD ? D : XD;
+#pragma unroll
+    for (int k = -PRE; k < 0; k++) {
+        if (k + XD >= 0) fetch_x(k + XD, (k + XD) % NST);
+        __builtin_amdgcn_sched_barrier(0);
+        if (k + D >= 0) fetch_w(k + D, r[(k + D) % D]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    static_assert(PRE == D && PRE == XD, "the prologue issues whole steps");
+    const uint32_t nit = (sb1 - sb0 + 1) / 2;
+    // one loop trip is a superblock: the code group and every ring slot are static
+    static_assert(4 % D == 0 && 4 % NST == 0, "ring sizes divide the 4 steps of a superblock");
+    for (uint32_t l0 = 0; l0 < 4 * nit; l0 += 4) {
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) {
+            const uint32_t l = l0 + jj;
+            WRegs &rj = r[jj % D];
+            // (a bare barrier: __syncthreads' release fence would wait for
+            // every outstanding direct load, the prefetched ones included)
+            if (kh == 0) {
+                asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(WAIT_X0));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            fetch_x(l + XD, (jj + XD) % NST);
+            __builtin_amdgcn_sched_barrier(0);
+            const float vf = sb0 + 2 * (l >> 2) + kh < sb1 ? 1.0f : 0.0f;
+            asm volatile("s_waitcnt vmcnt(%4)" : "+v"(rj.h0), "+v"(rj.h1), "+v"(rj.q0), "+v"(rj.q1) : "n"(WAIT_W));
+            u32x4v a[2][4];
+            dq_row(rj.h0, rj.q0, jj, vf, a[0]);
+            dq_row(rj.h1, rj.q1, jj, vf, a[1]);
+            __builtin_amdgcn_sched_barrier(0);
+            fetch_w(l + D, rj);
+            __builtin_amdgcn_sched_barrier(0);
+            if (kh != 0) {
+                asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(WAIT_X1));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            const uint32_t so = (jj % NST) * STAGE_B;
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) {
+                u32x4v b[4];
+                read_b(baddr[kk] + so, b);
+                asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]));
+#pragma unroll
+                for (int i = 0; i < 2; i++)
+#pragma unroll
+                    for (int jn = 0; jn < 4; jn++)
+                        acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                            __builtin_bit_cast(half8, a[i][kk]), __builtin_bit_cast(half8, b[jn]), acc[i][jn], 0,
+                            0, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    // The loads issued past the end are still in flight: the direct ones
+    // write the stages, and the weight registers must stay allocated until
+    // their data has landed (an asm output whose value is never read could
+    // otherwise be handed to another value while the load still writes it).
+#pragma unroll
+    for (int j = 0; j < D; j++)
+        asm volatile("s_waitcnt vmcnt(0)" : "+v"(r[j].h0), "+v"(r[j].h1), "+v"(r[j].q0), "+v"(r[j].q1)::"memory");
+
+    // odd half -> even half, one row tile (i) at a time through LDS:
+    // red[(wr * 64 + e) * 64 + lane], e = 16 jn + register
+    float *red = (float *)&Bs[0][0][0];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        __syncthreads();
+        if (kh == 1) {
+#pragma unroll
+            for (int jn = 0; jn < 4; jn++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) red[(wr * 64 + jn * 16 + e) * 64 + lane] = acc[i][jn][e];
+        }
+        __syncthreads();
+        if (kh == 0) {
+#pragma unroll
+            for (int jn = 0; jn < 4; jn++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) acc[i][jn][e] += red[(wr * 64 + jn * 16 + e) * 64 + lane];
+        }
+    }
+    if (kh == 1) return;
+
+    if (split) {
+        float *pt = sp.part + (uint64_t)unit * (QW_BM * QG_BN);  // [n_local][m_local]
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int jn = 0; jn < 4; jn++) {
+                const uint32_t nl = jn * 32 + (lane & 31);
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const uint32_t ml = wr * 64 + i * 32 + 8 * q + 4 * h;
+                    const floatx16 &c = acc[i][jn];
+                    *(float4 *)(pt + nl * QW_BM + ml) =
+                        make_float4(c[4 * q], c[4 * q + 1], c[4 * q + 2], c[4 * q + 3]);
+                }
+            }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int jn = 0; jn < 4; jn++) {
+            const uint32_t n = n0 + jn * 32 + (lane & 31);
+            if (n >= N) continue;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const uint32_t m = m0 + wr * 64 + i * 32 + 8 * q + 4 * h;
+                float *dst = Y + (uint64_t)n * M + m;
+                const floatx16 &c = acc[i][jn];
+                if (m + 3 < M && (M & 3) == 0) {
+                    *(float4 *)dst = make_float4(c[4 * q], c[4 * q + 1], c[4 * q + 2], c[4 * q + 3]);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        if (m + e < M) dst[e] = c[4 * q + e];
+                }
+            }
+        }
 }
 
 }  // namespace okf

@@ -52,6 +52,8 @@ struct okf_ctx {
     // variables override them for measurements)
     int gemv_s = 0;      // K split across a workgroup's wavefronts (0 = auto)
     int gemv_wide = -1;  // one-workgroup-per-CU matvec: -1 auto, 0 never, 1 where it fits
+    int gemm_w = 1;      // Q4_K GEMM: 1 the 256-row wide tile, 0 the 128 x 128 tile
+    int gemm_ks = 0;     // wide-tile GEMM: K ranges per remainder tile (0 = auto)
     uint32_t cus = 256;  // compute units of the device
     double fault_rate = 0;
     uint64_t fault_state = 0;
@@ -324,6 +326,40 @@ int grow_part(okf_ctx *c, size_t need) {
     return OKF_OK;
 }
 
+// The wide-tile Q4_K GEMM (gemm_q4k_w8_kernel): one 256 x 128 tile per CU.
+// Whole rounds of `cus` tiles stay whole; each remaining tile is split over
+// ks K ranges of whole superblocks (ks * remaining <= cus), whose partial
+// tiles gemm_split_sum_kernel adds in K order.
+int launch_gemm_q4k_w(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t M, uint32_t N,
+                      float *Y) {
+    const uint32_t tm = (M + QW_BM - 1) / QW_BM, tn = (N + QG_BN - 1) / QG_BN, sbs = K / 256;
+    GemmSplit sp{};
+    sp.tiles_n = tn;
+    sp.tiles = tm * tn;
+    const uint32_t round = c->cus ? c->cus : 256, rem = sp.tiles % round;
+    sp.full = sp.tiles - rem;
+    sp.ks = rem ? std::min(c->gemm_ks > 0 ? (uint32_t)c->gemm_ks : round / rem, sbs) : 1;
+    if (sp.ks < 2) {
+        sp.full = sp.tiles + 7 & ~7u;  // no split: every tile whole
+        sp.ks = 1;
+    }
+    sp.full_xcd = sp.full / 8;
+    sp.units = sp.ks > 1 ? rem * sp.ks : 0;
+    sp.units_xcd = (sp.units + 7) / 8;
+    if (sp.units) {
+        const int st = grow_part(c, (size_t)sp.units * QW_BM * QG_BN * sizeof(float));
+        if (st) return st;
+        sp.part = c->part;
+    }
+    const uint32_t grid = 8 * (sp.full_xcd + sp.units_xcd);
+    hipLaunchKernelGGL((gemm_q4k_w8_kernel<2, 2>), dim3(grid), dim3(512), 0, c->stream, W, rb, K, M,
+                       (const _Float16 *)c->xh, N, Y, sp);
+    if (sp.units)
+        hipLaunchKernelGGL(gemm_split_sum_kernel<QW_BM>, dim3((sp.tiles - sp.full) * (QW_BM * QG_BN / 1024)),
+                           dim3(256), 0, c->stream, (const float *)c->part, Y, M, N, sp);
+    return OKF_OK;
+}
+
 template <int F>
 int launch_gemm(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t M, const float *X,
                 uint32_t N, float *Y) {
@@ -345,6 +381,7 @@ int launch_gemm(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t 
         const uint64_t n4 = (uint64_t)N * K / 4;
         hipLaunchKernelGGL(x_to_f16_kernel, dim3((uint32_t)((n4 + 255) / 256)), dim3(256), 0, c->stream,
                            X, c->xh, n4);
+        if (c->gemm_w) return launch_gemm_q4k_w(c, W, rb, K, M, N, Y);
         const uint32_t tm = (M + QG_BM - 1) / QG_BM, tn = (N + QG_BN - 1) / QG_BN;
         GemmSplit sp{};
         sp.tiles_n = tn;
@@ -370,8 +407,8 @@ int launch_gemm(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t 
         hipLaunchKernelGGL(gemm_q4k_kernel, dim3(grid), dim3(256), 0, c->stream, W, rb, K, M,
                            (const _Float16 *)c->xh, N, Y, sp);
         if (sp.units)
-            hipLaunchKernelGGL(gemm_split_sum_kernel, dim3((sp.tiles - sp.full) * QG_SUM_WG), dim3(256), 0, c->stream,
-                               (const float *)c->part, Y, M, N, sp);
+            hipLaunchKernelGGL(gemm_split_sum_kernel<QG_BM>, dim3((sp.tiles - sp.full) * (QG_BM * QG_BN / 1024)),
+                               dim3(256), 0, c->stream, (const float *)c->part, Y, M, N, sp);
         return OKF_OK;
     }
     dim3 grid((N + GB_N - 1) / GB_N, (M + GB_M - 1) / GB_M);
@@ -545,6 +582,8 @@ int okf_ctx_create(int device, okf_ctx **out) {
             c->cus = (uint32_t)v;
         if (const char *e = getenv("OKF_GEMV_S")) c->gemv_s = atoi(e);
         if (const char *e = getenv("OKF_GEMV_WIDE")) c->gemv_wide = atoi(e);
+        if (const char *e = getenv("OKF_GEMM_W")) c->gemm_w = atoi(e);
+        if (const char *e = getenv("OKF_GEMM_KS")) c->gemm_ks = atoi(e);
     } else if (device != -1) {
         delete c;
         return OKF_E_ARG;
