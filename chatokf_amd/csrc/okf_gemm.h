@@ -178,14 +178,10 @@ namespace okf {
 // ------------------------------------------------------------------------
 // Q4_K x fp16 tile GEMM (the pp512 prefill path).
 //
-// Y[n][m] = sum_k W[m][k] X[n][k] with X already in fp16 (Xh[N][K]).
-// Workgroup tile 128 (rows m) x 128 (tokens n), K step 64 (one 32-byte code
-// group of a superblock); four wavefronts in 2 x 2, each 64 x 64 with
-// v_mfma_f32_32x32x16_f16.  The Q4_K bytes and fp16 activations of a step
-// arrive in registers two steps ahead; they are dequantized with packed fp16
-// arithmetic and stored to the single LDS stage between two barriers.  Tiles are laid out
-// so that each XCD (workgroup id mod 8) owns a contiguous range of tiles.
-constexpr int QG_BM = 128, QG_BN = 128, QG_BK = 64, QG_LD = QG_BK + 8;
+// Y[n][m] = sum_k W[m][k] X[n][k] with X already in fp16 (Xh[N][K]).  Tiles
+// are 256 weight rows x QG_BN tokens, K steps of QG_BK (one 32-byte code
+// group of a superblock); the kernel is gemm_q4k_w8_kernel below.
+constexpr int QG_BN = 128, QG_BK = 64;
 
 // v_bfi_b32 with 0x64006400: drops the masked bits of a into the mantissas of
 // two fp16 1024.0 (written out: the compiler splits the constant form).
@@ -204,10 +200,10 @@ __global__ __launch_bounds__(256) void x_to_f16_kernel(const float *__restrict__
     ((half4 *)Xh)[i] = half4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
 }
 
-// Work split.  The first `full` tiles (a multiple of 256 = one per CU per
-// round) are whole tiles; each of the remaining tiles is split over `ks` K
-// ranges, so that a grid of 2 x 256 + 32 tiles (pp512) costs 2 + 1/8 tile
-// times per CU instead of 3.  A split workgroup stores its partial tile to
+// Work split.  The first `full` tiles (a multiple of the CU count = one per
+// CU per round) are whole tiles; each of the remaining tiles is split over
+// `ks` K ranges, so that a grid of 256 + 16 tiles (pp512) costs about 1 + 1/10
+// tile times per CU instead of 2.  A split workgroup stores its partial tile to
 // `part`; gemm_split_sum_kernel then adds each tile's partials in K order
 // (a kernel boundary, not an in-kernel fence: a device-scope fence writes
 // back and invalidates the whole L2 of the XCD, which costs the concurrent
@@ -216,197 +212,9 @@ struct GemmSplit {
     uint32_t tiles_n, tiles;
     uint32_t full, full_xcd;        // whole tiles, and per XCD
     uint32_t ks, units, units_xcd;  // K ranges per split tile, split workgroups, per XCD
-    float *part;                    // [units][QG_BN][QG_BM] partial tiles
+    float *part;                    // [units][QG_BN][256] partial tiles
+    uint32_t ng;                    // wide kernel: N tiles per XCD group (0: plain order)
 };
-
-__global__ __launch_bounds__(256, 2) void gemm_q4k_kernel(const uint8_t *__restrict__ W, uint64_t row_bytes,
-                                                       uint32_t K, uint32_t M,
-                                                       const _Float16 *__restrict__ Xh, uint32_t N,
-                                                       float *__restrict__ Y, GemmSplit sp) {
-    __shared__ __attribute__((aligned(16))) _Float16 As[1][QG_BM * QG_LD];
-    __shared__ __attribute__((aligned(16))) _Float16 Bs[1][QG_BN * QG_LD];
-    // Workgroup b runs on XCD b % 8; each XCD takes a contiguous range of
-    // whole tiles and of split units, with the split units spread evenly
-    // through its workgroup order (every third slot at pp512), so that
-    // whichever way the dispatcher fills CUs, each gets its share of both.
-    // The N tiles of one row block are adjacent, so they run together on one
-    // XCD and read that block's Q4_K bytes from HBM once (the rest hit its L2).
-    const uint32_t xcd = blockIdx.x % 8, slot = blockIdx.x / 8, pairs = K / (2 * QG_BK);
-    const uint32_t per = sp.full_xcd + sp.units_xcd;
-    const uint32_t sa = slot * sp.units_xcd / per, sb = (slot + 1) * sp.units_xcd / per;
-    uint32_t tile, unit = 0, s0 = 0, s1 = K / QG_BK;
-    const bool split = sb > sa;
-    if (!split) {
-        tile = xcd * sp.full_xcd + (slot - sa);
-    } else {
-        unit = xcd * sp.units_xcd + sa;
-        if (unit >= sp.units) return;
-        tile = sp.full + unit / sp.ks;
-        const uint32_t c = unit % sp.ks;  // K range c: whole step pairs
-        s0 = 2 * (c * pairs / sp.ks);
-        s1 = 2 * ((c + 1) * pairs / sp.ks);
-    }
-    if (tile >= sp.tiles) return;
-    const uint32_t nt = tile % sp.tiles_n, mt = tile / sp.tiles_n;
-    const uint32_t m0 = mt * QG_BM, n0 = nt * QG_BN;
-
-    const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const uint32_t wm = wave >> 1, wn = wave & 1;
-    // loader roles: weight row t/2, code half t%2; activation row t/2, half t%2
-    const uint32_t lr = t >> 1, lh = t & 1;
-    const uint8_t *wrow = W + (uint64_t)min(m0 + lr, M - 1) * row_bytes;
-    const _Float16 *xrow = Xh + (uint64_t)min(n0 + lr, N - 1) * K;
-    const uint32_t steps = K / QG_BK;
-
-    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
-    struct Regs {
-        u32x4v hdr, qv, xv[4];
-    };
-    // global -> registers for step s (clamped: the loads after the last step
-    // repeat it, so that every fetch is unconditional and the compiler's
-    // count of outstanding loads stays exact)
-    auto fetch = [&](uint32_t s, Regs &r) {
-        s = min(s, steps - 1);
-        const uint8_t *b = wrow + (uint64_t)(s >> 2) * 144;  // superblock s / 4, group s % 4
-        r.hdr = *(const u32x4v *)b;
-        r.qv = *(const u32x4v *)(b + 16 + (s & 3) * 32 + lh * 16);
-        const u32x4v *xp = (const u32x4v *)(xrow + (uint64_t)s * QG_BK + lh * 32);
-#pragma unroll
-        for (int i = 0; i < 4; i++) r.xv[i] = xp[i];
-    };
-    auto stash = [&](uint32_t s, const Regs &r, int buf) {
-        const u32x4v hdr = r.hdr, qv = r.qv;
-        // dequantize 32 weights of row lr: low nibbles -> k = 16 lh + i
-        // (sub-block 2g), high nibbles -> k = 32 + 16 lh + i (sub-block 2g+1).
-        // Packed fp16: a nibble pair becomes fp16 (1024 + q) by v_bfi, minus
-        // 1024 (exact), then one fused q * (d*sc) - dmin*m with the two scale
-        // products rounded to fp16 (the result is rounded once).
-        const uint32_t g = s & 3;
-        uint32_t sc0, mn0, sc1, mn1;
-        q4k_scale_min_pair(make_uint4(hdr[0], hdr[1], hdr[2], hdr[3]), g, sc0, mn0, sc1, mn1);
-        const float d = h2f(hdr[0] & 0xFFFF), dmin = h2f(hdr[0] >> 16);
-        const half2v a0 = (half2v)(_Float16)(d * (float)sc0), o0 = (half2v)(_Float16)(-dmin * (float)mn0);
-        const half2v a1 = (half2v)(_Float16)(d * (float)sc1), o1 = (half2v)(_Float16)(-dmin * (float)mn1);
-        const half2v m1024 = (half2v)(_Float16)-1024.0f;
-        uint32_t lo[8], hi[8];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t v = qv[i];
-            const uint32_t p01 = __builtin_amdgcn_perm(v, v, 0x0C010C00u);  // b0, b1 -> 16-bit lanes
-            const uint32_t p23 = __builtin_amdgcn_perm(v, v, 0x0C030C02u);
-            const uint32_t l01 = gbfi(0x000F000Fu, p01), l23 = gbfi(0x000F000Fu, p23);
-            const uint32_t h01 = gbfi(0x000F000Fu, p01 >> 4), h23 = gbfi(0x000F000Fu, p23 >> 4);
-            auto dq = [&](uint32_t x, half2v a, half2v o) {
-                const half2v q = __builtin_bit_cast(half2v, x) + m1024;
-                return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, a, o));
-            };
-            lo[2 * i] = dq(l01, a0, o0);
-            lo[2 * i + 1] = dq(l23, a0, o0);
-            hi[2 * i] = dq(h01, a1, o1);
-            hi[2 * i + 1] = dq(h23, a1, o1);
-        }
-        _Float16 *ad = As[buf] + lr * QG_LD + lh * 16;
-        *(u32x4v *)(ad) = u32x4v{lo[0], lo[1], lo[2], lo[3]};
-        *(u32x4v *)(ad + 8) = u32x4v{lo[4], lo[5], lo[6], lo[7]};
-        *(u32x4v *)(ad + 32) = u32x4v{hi[0], hi[1], hi[2], hi[3]};
-        *(u32x4v *)(ad + 40) = u32x4v{hi[4], hi[5], hi[6], hi[7]};
-        _Float16 *bd = Bs[buf] + lr * QG_LD + lh * 32;
-#pragma unroll
-        for (int i = 0; i < 4; i++) *(u32x4v *)(bd + i * 8) = r.xv[i];
-    };
-    typedef float floatx16 __attribute__((ext_vector_type(16)));
-    floatx16 acc[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = floatx16{};
-
-    // v_mfma_f32_32x32x16_f16 (about twice the throughput of 16x16x32 on
-    // gfx950): lane l supplies row l % 32, k = 8 (l / 32) .. +8 of A (weights)
-    // and column l % 32, same k, of B (tokens).
-    auto mfma_step = [&](int buf) {
-        const _Float16 *A = As[buf], *B = Bs[buf];
-#pragma unroll
-        for (int kk = 0; kk < QG_BK / 16; kk++) {
-            const uint32_t kc = kk * 16 + (lane >> 5) * 8;
-            half8 a[2], b[2];
-#pragma unroll
-            for (int i = 0; i < 2; i++)
-                a[i] = *(const half8 *)(A + (wm * 64 + i * 32 + (lane & 31)) * QG_LD + kc);
-#pragma unroll
-            for (int j = 0; j < 2; j++)
-                b[j] = *(const half8 *)(B + (wn * 64 + j * 32 + (lane & 31)) * QG_LD + kc);
-#pragma unroll
-            for (int i = 0; i < 2; i++)
-#pragma unroll
-                for (int j = 0; j < 2; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
-        }
-    };
-
-    // One LDS stage (so three workgroups fit per CU and the whole grid is
-    // resident) and two register sets: step s + 1 is stored to LDS from
-    // registers loaded a full step earlier, while the loads of step s + 2 are
-    // in flight.
-    Regs ra, rb;
-    fetch(s0, ra);
-    fetch(s0 + 1, rb);
-    // steps = K / 64 is a multiple of 4 (K is whole 256-weight superblocks),
-    // and every K range is a whole number of step pairs
-    for (uint32_t s = s0; s < s1; s += 2) {
-        __syncthreads();
-        stash(s, ra, 0);
-        __syncthreads();
-        fetch(s + 2, ra);
-        mfma_step(0);
-        __syncthreads();
-        stash(s + 1, rb, 0);
-        __syncthreads();
-        fetch(s + 3, rb);
-        mfma_step(0);
-    }
-
-    // C fragment of a 32 x 32 tile: register e of lane l holds row
-    // 8 (e / 4) + 4 (l / 32) + e % 4 (weight rows m) of column l % 32 (token n)
-    if (split) {
-        // partial tile, [n_local][m_local]
-        float *pt = sp.part + (uint64_t)unit * (QG_BM * QG_BN);
-#pragma unroll
-        for (int i = 0; i < 2; i++)
-#pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const uint32_t nl = wn * 64 + j * 32 + (lane & 31);
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const uint32_t ml = wm * 64 + i * 32 + 8 * q + 4 * (lane >> 5);
-                    const floatx16 &c = acc[i][j];
-                    *(float4 *)(pt + nl * QG_BM + ml) =
-                        make_float4(c[4 * q], c[4 * q + 1], c[4 * q + 2], c[4 * q + 3]);
-                }
-            }
-        return;
-    }
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const uint32_t n = n0 + wn * 64 + j * 32 + (lane & 31);
-            if (n >= N) continue;
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const uint32_t m = m0 + wm * 64 + i * 32 + 8 * q + 4 * (lane >> 5);
-                float *dst = Y + (uint64_t)n * M + m;
-                const floatx16 &c = acc[i][j];
-                if (m + 3 < M && (M & 3) == 0) {
-                    *(float4 *)dst = make_float4(c[4 * q], c[4 * q + 1], c[4 * q + 2], c[4 * q + 3]);
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; e++)
-                        if (m + e < M) dst[e] = c[4 * q + e];
-                }
-            }
-        }
-}
 
 // Y of the split tiles: workgroup b sums float4 (b % per-tile) * 256 + t of
 // split tile b / per-tile over its ks partials, in K order (all ks loads
@@ -461,8 +269,12 @@ __device__ __forceinline__ bool wide_tile_of(const GemmSplit &sp, uint32_t sbs, 
     sb1 = sbs;
     unit = 0;
     if (!split) {
-        if (8 % sp.tiles_n == 0) {
-            const uint32_t nt = xcd % sp.tiles_n, mt = (xcd / sp.tiles_n) * sp.full_xcd + slot;
+        // groups of ng N tiles; XCD x takes N-tile group x % groups and, in
+        // its slots, ng consecutive N tiles of each of its row blocks
+        const uint32_t ng = sp.ng, groups = sp.tiles_n / ng;
+        if (ng && sp.tiles_n % ng == 0 && 8 % groups == 0 && sp.full_xcd % ng == 0) {
+            const uint32_t nt = (xcd % groups) * ng + slot % ng;
+            const uint32_t mt = (xcd / groups) * (sp.full_xcd / ng) + slot / ng;
             tile = mt * sp.tiles_n + nt;
         } else {
             tile = xcd * sp.full_xcd + slot;

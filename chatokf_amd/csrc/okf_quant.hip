@@ -52,8 +52,8 @@ struct okf_ctx {
     // variables override them for measurements)
     int gemv_s = 0;      // K split across a workgroup's wavefronts (0 = auto)
     int gemv_wide = -1;  // one-workgroup-per-CU matvec: -1 auto, 0 never, 1 where it fits
-    int gemm_w = 1;      // Q4_K GEMM: 1 the 256-row wide tile, 0 the 128 x 128 tile
     int gemm_ks = 0;     // wide-tile GEMM: K ranges per remainder tile (0 = auto)
+    int gemm_ng = 4;     // wide-tile GEMM: N tiles that share an XCD's row blocks
     uint32_t cus = 256;  // compute units of the device
     double fault_rate = 0;
     uint64_t fault_state = 0;
@@ -346,6 +346,7 @@ int launch_gemm_q4k_w(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uin
     sp.full_xcd = sp.full / 8;
     sp.units = sp.ks > 1 ? rem * sp.ks : 0;
     sp.units_xcd = (sp.units + 7) / 8;
+    sp.ng = (uint32_t)c->gemm_ng;
     if (sp.units) {
         const int st = grow_part(c, (size_t)sp.units * QW_BM * QG_BN * sizeof(float));
         if (st) return st;
@@ -381,35 +382,7 @@ int launch_gemm(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t 
         const uint64_t n4 = (uint64_t)N * K / 4;
         hipLaunchKernelGGL(x_to_f16_kernel, dim3((uint32_t)((n4 + 255) / 256)), dim3(256), 0, c->stream,
                            X, c->xh, n4);
-        if (c->gemm_w) return launch_gemm_q4k_w(c, W, rb, K, M, N, Y);
-        const uint32_t tm = (M + QG_BM - 1) / QG_BM, tn = (N + QG_BN - 1) / QG_BN;
-        GemmSplit sp{};
-        sp.tiles_n = tn;
-        sp.tiles = tm * tn;
-        // whole rounds of 256 tiles stay whole; the remainder is split over
-        // up to 8 K ranges (whole step pairs) to give every CU a share
-        const uint32_t pairs = K / (2 * QG_BK), rem = sp.tiles % 256;
-        sp.full = sp.tiles - rem;
-        sp.ks = rem ? std::min(std::min(256u / rem, 8u), pairs) : 1;
-        if (sp.ks < 2) {
-            sp.full = sp.tiles + 7 & ~7u;  // no split: every tile whole
-            sp.ks = 1;
-        }
-        sp.full_xcd = sp.full / 8;
-        sp.units = sp.ks > 1 ? rem * sp.ks : 0;
-        sp.units_xcd = (sp.units + 7) / 8;
-        if (sp.units) {
-            const int st = grow_part(c, (size_t)sp.units * QG_BM * QG_BN * sizeof(float));
-            if (st) return st;
-            sp.part = c->part;
-        }
-        const uint32_t grid = 8 * (sp.full_xcd + sp.units_xcd);
-        hipLaunchKernelGGL(gemm_q4k_kernel, dim3(grid), dim3(256), 0, c->stream, W, rb, K, M,
-                           (const _Float16 *)c->xh, N, Y, sp);
-        if (sp.units)
-            hipLaunchKernelGGL(gemm_split_sum_kernel<QG_BM>, dim3((sp.tiles - sp.full) * (QG_BM * QG_BN / 1024)),
-                               dim3(256), 0, c->stream, (const float *)c->part, Y, M, N, sp);
-        return OKF_OK;
+        return launch_gemm_q4k_w(c, W, rb, K, M, N, Y);
     }
     dim3 grid((N + GB_N - 1) / GB_N, (M + GB_M - 1) / GB_M);
     hipLaunchKernelGGL((gemm_mfma_kernel<F>), grid, dim3(256), 0, c->stream, W, rb, K, M, X, N, Y,
@@ -582,8 +555,8 @@ int okf_ctx_create(int device, okf_ctx **out) {
             c->cus = (uint32_t)v;
         if (const char *e = getenv("OKF_GEMV_S")) c->gemv_s = atoi(e);
         if (const char *e = getenv("OKF_GEMV_WIDE")) c->gemv_wide = atoi(e);
-        if (const char *e = getenv("OKF_GEMM_W")) c->gemm_w = atoi(e);
         if (const char *e = getenv("OKF_GEMM_KS")) c->gemm_ks = atoi(e);
+        if (const char *e = getenv("OKF_GEMM_NG")) c->gemm_ng = atoi(e);
     } else if (device != -1) {
         delete c;
         return OKF_E_ARG;
