@@ -225,6 +225,30 @@ __device__ __forceinline__ float slot_total(u32x4 v) {
     return t;
 }
 
+// The per-32 sum staged beside the packed activations: sum(x) for every
+// format but Q2_0.  Q2_0 decodes the pair at position c of a code dword
+// (codes c and c + 8) as fp16 base_c + code, base_c = 2^(10 - 2c) for
+// c <= 4 (the code bits inserted in place by one v_bfi into an fp16 2^(10-2c)
+// whose mantissa bit 2c is worth 1) and 1024 for c >= 5 (shifted down
+// first); then sum((code - 1) x) = sum((base + code) x) - sum((base + 1) x),
+// and the second sum is staged here.  Slot 2j + h holds the pairs at
+// positions c = 4h + e.  Every base + 1 (1025, 257, 65, 17, 5) is exact in
+// fp16, so each product is exact in fp32 as in slot_total.
+template <int F>
+__device__ __forceinline__ float slot_bias(u32x4 v, uint32_t sidx) {
+    if constexpr (F == Q2_0) {
+        constexpr uint32_t B1025 = 0x64016401u, B257 = 0x5C045C04u, B65 = 0x54105410u, B17 = 0x4C404C40u,
+                           B5 = 0x45004500u;
+        const bool h = sidx & 1;
+        float t = dot2(v[0], h ? B5 : B1025, 0.0f);
+        t = dot2(v[1], h ? B1025 : B257, t);
+        t = dot2(v[2], h ? B1025 : B65, t);
+        return dot2(v[3], h ? B1025 : B17, t);
+    } else {
+        return slot_total(v);
+    }
+}
+
 // LDS layout of the staged activations of one column: units in groups of L
 // (one per lane of a row slot); within a group, the unit's pairs as slots of
 // 4 pairs, each slot [L lanes][4 pairs] so a row slot's lanes read contiguous
@@ -547,46 +571,55 @@ struct Compute<IQ4_NL, NC, R, TS> {
 
 template <int NC, int R, int TS>
 struct Compute<Q2_0, NC, R, TS> {
+    // Pair position c of code dword j (codes c and c + 8, weights
+    // 16j + c, 16j + c + 8) becomes fp16 base_c + code: for c <= 4 one v_bfi
+    // of the code bits, in place, into 2^(10 - 2c); for c >= 5 a shift, then
+    // v_bfi into 1024.  xsp holds the staged sum((base + 1) x) (slot_bias),
+    // so sum((code - 1) x) = s - xsp.  Two accumulators (even and odd c)
+    // halve the dot2 dependency chain.
     __device__ __forceinline__ static void run(const Unit<Q2_0, R> &w, const uint32_t *xp, uint32_t ss, uint32_t cs,
                                                const float *xsp, uint32_t xcs, uint32_t,
                                                float (&acc)[R][NC], const u32x4 *) {
-        float xsum[NC], s[R][NC];
+        constexpr uint32_t MAGIC_C[5] = {0x64006400u, 0x5C005C00u, 0x54005400u, 0x4C004C00u, 0x44004400u};
+        float xb[NC], s[R][NC], s2[R][NC];
 #pragma unroll
         for (int n = 0; n < NC; n++) {
             const float2 t = *(const float2 *)(xsp + n * xcs);
-            xsum[n] = t.x + t.y;
+            xb[n] = t.x + t.y;
         }
 #pragma unroll
         for (int r = 0; r < R; r++)
 #pragma unroll
-            for (int n = 0; n < NC; n++) s[r][n] = 0;
+            for (int n = 0; n < NC; n++) s[r][n] = s2[r][n] = 0;
 #pragma unroll
         for (int j = 0; j < 4; j++) {  // code dword j: pairs 8j .. 8j + 7 = slots 2j, 2j + 1
-            u32x4 xa[NC], xb[NC];
+            u32x4 xa[NC], xc[NC];
 #pragma unroll
             for (int n = 0; n < NC; n++) {
                 xa[n] = *(const u32x4 *)(xp + n * cs + (2 * j) * ss);
-                xb[n] = *(const u32x4 *)(xp + n * cs + (2 * j + 1) * ss);
+                xc[n] = *(const u32x4 *)(xp + n * cs + (2 * j + 1) * ss);
             }
 #pragma unroll
             for (int r = 0; r < R; r++) {
                 const uint32_t v = w.q[r][j];
 #pragma unroll
                 for (int c = 0; c < 8; c++) {
-                    // codes c and c + 8 of the dword -> fp16 (1024 + code)
-                    const uint32_t hv = bfi(0x00030003u, v >> (2 * c), MAGIC2);
+                    const uint32_t hv = c <= 4 ? bfi(0x00030003u << (2 * c), v, MAGIC_C[c < 5 ? c : 0])
+                                               : bfi(0x00030003u, v >> (2 * c), MAGIC2);
 #pragma unroll
-                    for (int n = 0; n < NC; n++)
-                        s[r][n] = dot2(hv, c < 4 ? xa[n][c] : xb[n][c - 4], s[r][n]);
+                    for (int n = 0; n < NC; n++) {
+                        const uint32_t xv = c < 4 ? xa[n][c] : xc[n][c - 4];
+                        if (c & 1) s2[r][n] = dot2(hv, xv, s2[r][n]);
+                        else s[r][n] = dot2(hv, xv, s[r][n]);
+                    }
                 }
             }
         }
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const float d = h2f(w.d[r]);
-            // sum((code - 1) x) = sum((1024 + code) x) - 1025 sum(x)
 #pragma unroll
-            for (int n = 0; n < NC; n++) acc[r][n] += d * (s[r][n] - 1025.0f * xsum[n]);
+            for (int n = 0; n < NC; n++) acc[r][n] += d * ((s[r][n] + s2[r][n]) - xb[n]);
         }
     }
 };
@@ -840,11 +873,15 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(float *__restrict__ a,
 
 // With SILU the activations are silu(X) * X2 (the FFN's gate and up
 // outputs), computed here in fp32 before the fp16 rounding.
-template <int F, int NC, int L, uint32_t SP, bool SILU>
+// after_loads() runs once, right after the first round's activation loads
+// are issued: the caller issues its weight loads there, behind them, so that
+// the packing below waits only for the activations (loads complete in issue
+// order) while the weights are in flight.
+template <int F, int NC, int L, uint32_t SP, bool SILU, typename AfterLoads>
 __device__ __forceinline__ void stage_x(const float *__restrict__ X, const float *__restrict__ X2,
                                         uint32_t K, uint32_t c0,
                                         uint32_t nslots, uint32_t tid, uint32_t nthr, uint32_t *xs,
-                                        uint32_t cs, float *xsum, uint32_t xcs) {
+                                        uint32_t cs, float *xsum, uint32_t xcs, AfterLoads after_loads) {
     constexpr uint32_t UW = unit_weights<F>(), SL = UW / 8;
     for (uint32_t q0 = 0; q0 < nslots; q0 += SP * nthr) {
         floatx4 A[SP][NC], B[SP][NC], A2[SILU ? SP : 1][SILU ? NC : 1], B2[SILU ? SP : 1][SILU ? NC : 1];
@@ -864,6 +901,11 @@ __device__ __forceinline__ void stage_x(const float *__restrict__ X, const float
                 }
             }
         }
+        if (q0 == 0) {
+            __builtin_amdgcn_sched_barrier(0);
+            after_loads();
+            __builtin_amdgcn_sched_barrier(0);
+        }
 #pragma unroll
         for (uint32_t p = 0; p < SP; p++) {
             const uint32_t q = q0 + p * nthr + tid, u = q / SL, sidx = q % SL;
@@ -875,7 +917,7 @@ __device__ __forceinline__ void stage_x(const float *__restrict__ X, const float
                     B[p][n] = silu_mul4(B[p][n], B2[p][n]);
                 }
                 const u32x4 v = slot_pack<F>(A[p][n], B[p][n]);
-                const float pt = quad_sum(slot_total(v));
+                const float pt = quad_sum(slot_bias<F>(v, sidx));
                 if (in) {
                     *(u32x4 *)(xs + n * cs + xs_index<F, L>(u, 4 * sidx)) = v;
                     if ((q & 3) == 0) xsum[n * xcs + q / 4] = pt;
@@ -922,16 +964,19 @@ __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ W, uint64_
         const uint32_t cn = min(cunits, units - c0);
         // this wavefront's steps: t = part, part + S, ... of the chunk
         const uint32_t steps = ((cn + L - 1) / L + S - 1 - part) / S, last = cn - 1;
-        // The first D steps' weights are requested before the activations are
-        // staged, so their latency overlaps the staging.  Loads are
-        // unconditional (past the end they re-read the chunk's last unit, a
-        // cache hit) so that no branch hides a load from the compiler's count
-        // of outstanding loads, and the wait before a compute covers only the
-        // loads of that buffer.
+        // The first D steps' weights are requested right behind the
+        // activation loads of the staging (stage_x's after_loads), so their
+        // latency overlaps the staging and the staging waits only for the
+        // activations.  Loads are unconditional (past the end they re-read
+        // the chunk's last unit, a cache hit) so that no branch hides a load
+        // from the compiler's count of outstanding loads, and the wait before
+        // a compute covers only the loads of that buffer.
         Unit<F, R> buf[D];
+        auto load_first = [&]() {
 #pragma unroll
-        for (int j = 0; j < D; j++)
-            load_unit<F, R>(rows, c0 + min(i + L * (part + S * j), last), buf[j]);
+            for (int j = 0; j < D; j++)
+                load_unit<F, R>(rows, c0 + min(i + L * (part + S * j), last), buf[j]);
+        };
 
         // stage units [c0, c0 + cn) of every column as fp16 pairs
         __syncthreads();
@@ -942,11 +987,12 @@ __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ W, uint64_
         constexpr uint32_t SP = NC == 1 ? 4 : NC == 2 ? 2 : 1;
         // (a chunk that one or three passes cover takes that copy: no idle passes)
         if (nslots <= nthr)
-            stage_x<F, NC, L, 1, SILU>(X, X2, K, c0, nslots, tid, nthr, xs, cs, xsum, xcs);
+            stage_x<F, NC, L, 1, SILU>(X, X2, K, c0, nslots, tid, nthr, xs, cs, xsum, xcs, load_first);
         else if (SP == 4 && nslots <= 3 * nthr)
-            stage_x<F, NC, L, (SP == 4 ? 3 : 1), SILU>(X, X2, K, c0, nslots, tid, nthr, xs, cs, xsum, xcs);
+            stage_x<F, NC, L, (SP == 4 ? 3 : 1), SILU>(X, X2, K, c0, nslots, tid, nthr, xs, cs, xsum, xcs,
+                                                       load_first);
         else
-            stage_x<F, NC, L, SP, SILU>(X, X2, K, c0, nslots, tid, nthr, xs, cs, xsum, xcs);
+            stage_x<F, NC, L, SP, SILU>(X, X2, K, c0, nslots, tid, nthr, xs, cs, xsum, xcs, load_first);
         __syncthreads();
         // stream the wavefront's units u = c0 + i + L (part + S t) through
         // the ring

@@ -117,7 +117,7 @@ __global__ __launch_bounds__(GW_THREADS) void gemv_wide_kernel(const uint8_t *__
 #pragma unroll
         for (int n = 0; n < NC; n++) {
             const u32x4 v = slot_pack<F>(A[p][n], B[p][n]);
-            const float pt = quad_sum(slot_total(v));
+            const float pt = quad_sum(slot_bias<F>(v, sidx));
             if (q < nslots) {
                 *(u32x4 *)(xs + n * cs + xs_index<F, L>(u, 4 * sidx)) = v;
                 if ((q & 3) == 0) xsum[n * xcs + q / 4] = pt;
