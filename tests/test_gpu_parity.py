@@ -367,10 +367,14 @@ def test_parallel_group_matches_single_calls(enc):
 # (The metric is relative to max|ref| over the output, so every case keeps
 # enough outputs for that maximum to be representative; a single dot product
 # can cancel to near zero, where fp16 staging error is not bounded by 1e-3.)
-# The Q4_K kernel splits the tiles beyond whole rounds of 256 over K ranges:
-# (4224, 256, 512) has 132 tiles and no split, the others split 2..8 ways.
+# The Q4_K kernel (256-row x 128-token tiles, one per CU) splits the tiles
+# beyond whole rounds of 256 over K ranges of whole superblocks: the small
+# cases are all split (2..9 ways, odd superblock counts leave the odd K half
+# empty); (8192, 512, 1024) is exactly 256 whole tiles with eight N tiles
+# per row block, grouped four to an XCD.
 TILE = [(Q8_0, 300, 2048, 37), (Q2_0, 130, 1024, 129), (Q4_K, 260, 2304, 77), (IQ2_XXS, 129, 1536, 6),
         (Q4_K, 1, 256, 64), (Q8_0, 5, 96, 200), (Q4_K, 4224, 256, 512), (Q4_K, 1000, 512, 300),
+        (Q4_K, 8192, 512, 1024),
         (Q4_0, 300, 2048, 37), (IQ4_NL, 130, 1024, 70), (Q5_K, 200, 1024, 40), (Q6_K, 129, 768, 33),
         (IQ4_XS, 260, 1280, 90)] + [(t, 130, 768, 41) for t in (IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M, Q2_K, Q3_K, F32,
                                                                 F16, BF16)]
