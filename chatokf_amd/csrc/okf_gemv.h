@@ -33,7 +33,7 @@ namespace okf {
 // any K that is a whole number of blocks works).
 template <int F>
 __host__ __device__ constexpr uint32_t unit_weights() {
-    return (F == Q8_0 || F == Q4_0 || F == IQ4_NL || F == Q6_K || grid_fmt(F)) ? 32 : 64;
+    return (F == Q8_0 || F == Q4_0 || F == IQ4_NL || grid_fmt(F)) ? 32 : 64;
 }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -105,9 +105,10 @@ struct Unit<Q5_K, R> {  // header, the 32 qh bytes, 32 code bytes of group g
     u32x4 hdr[R], h0[R], h1[R], q0[R], q1[R];
 };
 template <int R>
-struct Unit<Q6_K, R> {  // d, the two scales, 32 ql bytes, 32 qh bytes
-    uint32_t d[R], sc[R];
-    u32x4 q0[R], q1[R], h0[R], h1[R];
+struct Unit<Q6_K, R> {  // d, the half's 8 scales, ql bytes l and l + 32, qh bytes l (l = 16 is ..)
+    uint32_t d[R];
+    uint2 sc[R];
+    u32x4 qa[R], qb[R], qh[R];
 };
 template <int R>
 struct Unit<IQ4_XS, R> {  // d, scales_h, scales_l (8 bytes) + 32 code bytes of sub-blocks 2g, 2g + 1
@@ -142,15 +143,14 @@ __device__ __forceinline__ void load_unit(const uint8_t *const rows[R], uint32_t
             w.h1[r] = ldu<u32x4>(b + 32);
             w.q0[r] = ldu<u32x4>(b + 48 + g * 32);
             w.q1[r] = ldu<u32x4>(b + 64 + g * 32);
-        } else if constexpr (F == Q6_K) {  // unit = 32 weights (n, r) of superblock u >> 3
-            const uint8_t *b = rows[r] + (uint64_t)(u >> 3) * 210;
-            const uint32_t n = (u >> 2) & 1, rr = u & 3;
+        } else if constexpr (F == Q6_K) {  // unit (n, is) of superblock u >> 2: see Compute<Q6_K>
+            const uint8_t *b = rows[r] + (uint64_t)(u >> 2) * 210;
+            const uint32_t n = (u >> 1) & 1, is = u & 1;
             w.d[r] = ldu<uint16_t>(b + 208);
-            w.sc[r] = ldu<uint16_t>(b + 192 + n * 8 + 2 * rr);
-            w.q0[r] = ldu<u32x4>(b + n * 64 + (rr & 1) * 32);
-            w.q1[r] = ldu<u32x4>(b + n * 64 + (rr & 1) * 32 + 16);
-            w.h0[r] = ldu<u32x4>(b + 128 + n * 32);
-            w.h1[r] = ldu<u32x4>(b + 144 + n * 32);
+            w.sc[r] = ldu<uint2>(b + 192 + n * 8);
+            w.qa[r] = ldu<u32x4>(b + n * 64 + is * 16);
+            w.qb[r] = ldu<u32x4>(b + n * 64 + 32 + is * 16);
+            w.qh[r] = ldu<u32x4>(b + 128 + n * 32 + is * 16);
         } else if constexpr (F == IQ4_XS) {  // unit = sub-blocks 2g, 2g + 1 of superblock u >> 2
             const uint8_t *b = rows[r] + (uint64_t)(u >> 2) * 136;
             const uint32_t g = u & 3;
@@ -184,12 +184,27 @@ __device__ __forceinline__ void load_unit(const uint8_t *const rows[R], uint32_t
 //  Q4_0: as Q4_K with 16 code bytes: slots 0, 1 are the low nibbles
 //        (weights 0..15), slots 2, 3 the high ones (16..31).
 //  Q5_K: as Q4_K (32 code bytes of one group: low nibbles, then high).
-//  Q6_K: as Q4_K within its 32 weights (code dword i gives pairs (4i, 4i+2),
-//        (4i+1, 4i+3)).
+//  Q6_K: 8 weights 16 is + 32 grp + 8 i2 .. of the half per slot 2 grp + i2,
+//        packed as Q4_K's (code dword i gives pairs (4i, 4i+2), (4i+1, 4i+3)).
 //  Q8_0, IQ2_XXS, IQ4_NL, IQ4_XS: natural order, A = x[8s..], B = x[8s+4..].
+// Index in x of the first weight of unit u (a row's units in order).  The
+// Q6_K unit (half n, is) of superblock u / 4 holds weights 16 is + e +
+// {0, 32, 64, 96} of its half (e < 16), so its slots start 16 is into the
+// half; every other unit is UW contiguous weights.
+template <int F>
+__device__ __forceinline__ uint64_t unit_x_base(uint32_t u) {
+    if constexpr (F == Q6_K) return (uint64_t)(u >> 1) * 128 + (u & 1) * 16;
+    else return (uint64_t)u * unit_weights<F>();
+}
+
 template <int F>
 __device__ __forceinline__ uint32_t slot_first(uint32_t s, uint32_t &second) {
-    if constexpr (F == Q2_0) {
+    if constexpr (F == Q6_K) {
+        // slot s = 2 grp + i2: weights 32 grp + 8 i2 .. past unit_x_base
+        const uint32_t base = 32 * (s >> 1) + 8 * (s & 1);
+        second = base + 4;
+        return base;
+    } else if constexpr (F == Q2_0) {
         const uint32_t base = 16 * (s >> 1) + 4 * (s & 1);
         second = base + 8;
         return base;
@@ -692,24 +707,28 @@ struct Compute<Q5_K, NC, R, TS> {
 
 template <int NC, int R, int TS>
 struct Compute<Q6_K, NC, R, TS> {
-    // Unit (n, r): the 6-bit q of weight l is nibble r >> 1 of ql byte l with
-    // bits 2r, 2r + 1 of qh byte l on top.  v_bfi makes fp16 1024 + q, one
-    // packed fp16 add makes it q - 32 (exact), and the two 16-weight halves
-    // take their own int8 scale: acc += d s0 sum_0..15 + d s1 sum_16..31.
+    // Unit (n, is): weights l, l + 32, l + 64, l + 96 of half n for
+    // l = 16 is .. 16 is + 15 (KQuant.q6K's q1..q4).  Group grp of the four:
+    // the low (grp < 2) or high nibble of ql byte l (grp even) or l + 32
+    // (grp odd), with bits 2 grp, 2 grp + 1 of qh byte l on top.  v_bfi
+    // makes fp16 1024 + q, one packed fp16 add makes it q - 32 (exact), and
+    // each group takes its int8 scale: scales[8 n + is + 2 grp].  The unit
+    // reads exactly its 48 code bytes.
     __device__ __forceinline__ static void run(const Unit<Q6_K, R> &w, const uint32_t *xp, uint32_t ss, uint32_t cs,
                                                const float *, uint32_t, uint32_t u, float (&acc)[R][NC],
                                                const u32x4 *) {
-        const uint32_t rr = u & 3, shq = 4 * (rr >> 1), shh = 2 * rr;
+        const uint32_t is = u & 1;
         const half2v bias = {(_Float16)-1056.0f, (_Float16)-1056.0f};
-        float s[2][R][NC];
+        float s[4][R][NC];
 #pragma unroll
-        for (int p = 0; p < 2; p++)
+        for (int g = 0; g < 4; g++)
 #pragma unroll
             for (int r = 0; r < R; r++)
 #pragma unroll
-                for (int n = 0; n < NC; n++) s[p][r][n] = 0;
+                for (int n = 0; n < NC; n++) s[g][r][n] = 0;
 #pragma unroll
-        for (int sl = 0; sl < 4; sl++) {  // code dwords 2 sl, 2 sl + 1 (weights 8 sl ..)
+        for (int sl = 0; sl < 8; sl++) {  // slot 2 grp + i2: code dwords 2 i2, 2 i2 + 1 of group grp
+            const int grp = sl >> 1, i2 = sl & 1;
             u32x4 xv[NC];
 #pragma unroll
             for (int n = 0; n < NC; n++) xv[n] = *(const u32x4 *)(xp + n * cs + sl * ss);
@@ -717,18 +736,18 @@ struct Compute<Q6_K, NC, R, TS> {
             for (int r = 0; r < R; r++) {
 #pragma unroll
                 for (int h = 0; h < 2; h++) {
-                    const int i = 2 * sl + h;
-                    const uint32_t v = i < 4 ? w.q0[r][i] : w.q1[r][i - 4];
-                    const uint32_t hq = i < 4 ? w.h0[r][i] : w.h1[r][i - 4];
-                    const uint32_t q = ((v >> shq) & 0x0F0F0F0Fu) | (((hq >> shh) & 0x03030303u) << 4);
+                    const int i = 2 * i2 + h;
+                    const uint32_t v = (grp & 1) ? w.qb[r][i] : w.qa[r][i];
+                    const uint32_t q = ((v >> (4 * (grp >> 1))) & 0x0F0F0F0Fu) |
+                                       (((w.qh[r][i] >> (2 * grp)) & 0x03030303u) << 4);
                     const uint32_t p02 = __builtin_bit_cast(
                         uint32_t, __builtin_bit_cast(half2v, bfi(0x003F003Fu, q, MAGIC2)) + bias);
                     const uint32_t p13 = __builtin_bit_cast(
                         uint32_t, __builtin_bit_cast(half2v, bfi(0x003F003Fu, q >> 8, MAGIC2)) + bias);
 #pragma unroll
                     for (int n = 0; n < NC; n++) {
-                        s[sl >> 1][r][n] = dot2(p02, xv[n][2 * h], s[sl >> 1][r][n]);
-                        s[sl >> 1][r][n] = dot2(p13, xv[n][2 * h + 1], s[sl >> 1][r][n]);
+                        s[grp][r][n] = dot2(p02, xv[n][2 * h], s[grp][r][n]);
+                        s[grp][r][n] = dot2(p13, xv[n][2 * h + 1], s[grp][r][n]);
                     }
                 }
             }
@@ -736,9 +755,14 @@ struct Compute<Q6_K, NC, R, TS> {
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const float d = h2f(w.d[r]);
-            const float d0 = d * (float)(int8_t)(w.sc[r] & 0xFF), d1 = d * (float)(int8_t)(w.sc[r] >> 8);
+            // scale bytes is + 2 grp of the half's 8
+            const uint32_t s4 = __builtin_amdgcn_perm(w.sc[r].y, w.sc[r].x, is ? 0x07050301u : 0x06040200u);
+            float dg[4];
 #pragma unroll
-            for (int n = 0; n < NC; n++) acc[r][n] += d0 * s[0][r][n] + d1 * s[1][r][n];
+            for (int g = 0; g < 4; g++) dg[g] = d * (float)(int8_t)((s4 >> (8 * g)) & 0xFF);
+#pragma unroll
+            for (int n = 0; n < NC; n++)
+                acc[r][n] += dg[0] * s[0][r][n] + dg[1] * s[1][r][n] + dg[2] * s[2][r][n] + dg[3] * s[3][r][n];
         }
     }
 };
@@ -892,7 +916,7 @@ __device__ __forceinline__ void stage_x(const float *__restrict__ X, const float
             const uint32_t ka = slot_first<F>(q % SL, kb);
 #pragma unroll
             for (int n = 0; n < NC; n++) {
-                const uint64_t xo = (uint64_t)n * K + (uint64_t)(c0 + u) * UW;
+                const uint64_t xo = (uint64_t)n * K + unit_x_base<F>(c0 + u);
                 A[p][n] = *(const floatx4 *)(X + xo + ka);
                 B[p][n] = *(const floatx4 *)(X + xo + kb);
                 if constexpr (SILU) {

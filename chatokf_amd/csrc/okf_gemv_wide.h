@@ -97,7 +97,7 @@ __global__ __launch_bounds__(GW_THREADS) void gemv_wide_kernel(const uint8_t *__
         const uint32_t ka = slot_first<F>(q % SL, kb);
 #pragma unroll
         for (int n = 0; n < NC; n++) {
-            const uint64_t xo = (uint64_t)n * K + (uint64_t)u * UW;
+            const uint64_t xo = (uint64_t)n * K + unit_x_base<F>(u);
             A[p][n] = *(const floatx4 *)(X + xo + ka);
             B[p][n] = *(const floatx4 *)(X + xo + kb);
         }
