@@ -156,10 +156,11 @@ void launch_gemv_s(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32
         if (steps >= 3) return launch_gemv_s<F, NC, S, SILU, 3>(c, calls, n, rb, K, cunits, lds);
     }
     // two rows per slot (each staged activation read serves both) where
-    // measured faster: IQ2_XXS with 2..5 columns, Q4_K and Q2_0 with 5; a
-    // three-deep weight ring for the Q4_K matvec (its rows run 5+ steps)
+    // measured faster: IQ2_XXS with 2..5 columns, Q4_K and Q2_0 with 5.  (A
+    // three-deep ring for the Q4_K matvec measured 3-4 % slower than two
+    // once the weight loads were issued behind the staging's.)
     constexpr int R = ((F == IQ2_XXS && NC >= 2) || (NC == 5 && F != Q8_0 && F != Q5_K && F != Q6_K && F != IQ4_XS && !grid_fmt(F))) ? 2 : 1,
-                  D = DX ? DX : (F == Q4_K && NC == 1) ? 3 : 2, WAVES = 4;
+                  D = DX ? DX : 2, WAVES = 4;
     const void *fn = (const void *)gemv_kernel<F, NC, R, D, S, SILU>;
     static bool attr = false;  // one attribute call per instantiation
     if (!attr) {
