@@ -191,13 +191,65 @@ __device__ __forceinline__ uint32_t gbfi(uint32_t mask, uint32_t a) {
     return r;
 }
 
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
+// Q4_K code group g (64 weights) of one row as the four MFMA A operands of a
+// 32x32x16 f16 step: lane half h holds the group's code bytes 16 h .. 16 h + 15
+// in qv, and operand kk, element e is weight k = 16 h + 8 (kk & 1) +
+// 32 (kk >> 1) + e of the group (low nibbles are k < 32, high nibbles k >= 32).
+// The weight is fma(q, fp16(d sc), fp16(-dmin m)) in packed fp16 (q exact as
+// 1024 + q - 1024); vf (0 or 1) scales d and dmin, so vf = 0 gives zeros.
+__device__ __forceinline__ void q4k_dq_mfma_a(const u32x4v hdr, const u32x4v qv, uint32_t g, float vf,
+                                              u32x4v *a) {
+    // every loaded dword counts as used here: a dword that a group does
+    // not need would otherwise be reused as a temporary while its load
+    // is still in flight, and that write has to wait for the load
+    asm volatile("" ::"v"(hdr), "v"(qv));
+    uint32_t sc0, mn0, sc1, mn1;
+    q4k_scale_min_pair(make_uint4(hdr[0], hdr[1], hdr[2], hdr[3]), g, sc0, mn0, sc1, mn1);
+    const float d = h2f(hdr[0] & 0xFFFF) * vf, dmin = h2f(hdr[0] >> 16) * vf;
+    const half2v a0 = (half2v)(_Float16)(d * (float)sc0), o0 = (half2v)(_Float16)(-dmin * (float)mn0);
+    const half2v a1 = (half2v)(_Float16)(d * (float)sc1), o1 = (half2v)(_Float16)(-dmin * (float)mn1);
+    const half2v m1024 = (half2v)(_Float16)-1024.0f;
+    uint32_t lo[8], hi[8];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t v = qv[i];
+        const uint32_t p01 = __builtin_amdgcn_perm(v, v, 0x0C010C00u);
+        const uint32_t p23 = __builtin_amdgcn_perm(v, v, 0x0C030C02u);
+        const uint32_t l01 = gbfi(0x000F000Fu, p01), l23 = gbfi(0x000F000Fu, p23);
+        const uint32_t h01 = gbfi(0x000F000Fu, p01 >> 4), h23 = gbfi(0x000F000Fu, p23 >> 4);
+        auto dq = [&](uint32_t x, half2v sa_, half2v so) {
+            const half2v q = __builtin_bit_cast(half2v, x) + m1024;
+            return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, sa_, so));
+        };
+        lo[2 * i] = dq(l01, a0, o0);
+        lo[2 * i + 1] = dq(l23, a0, o0);
+        hi[2 * i] = dq(h01, a1, o1);
+        hi[2 * i + 1] = dq(h23, a1, o1);
+    }
+    a[0] = u32x4v{lo[0], lo[1], lo[2], lo[3]};
+    a[1] = u32x4v{lo[4], lo[5], lo[6], lo[7]};
+    a[2] = u32x4v{hi[0], hi[1], hi[2], hi[3]};
+    a[3] = u32x4v{hi[4], hi[5], hi[6], hi[7]};
+}
+
+// X fp32 -> fp16 (round to nearest even), XV float4 per thread with all
+// loads issued before the first store; n4 float4 in all.
+constexpr uint32_t XV = 4;
 __global__ __launch_bounds__(256) void x_to_f16_kernel(const float *__restrict__ X,
                                                        _Float16 *__restrict__ Xh, uint64_t n4) {
-    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= n4) return;
-    const floatx4 v = ((const floatx4 *)X)[i];
     typedef _Float16 half4 __attribute__((ext_vector_type(4)));
-    ((half4 *)Xh)[i] = half4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+    const uint64_t i0 = (uint64_t)blockIdx.x * (256 * XV) + threadIdx.x;
+    floatx4 v[XV];
+#pragma unroll
+    for (uint32_t j = 0; j < XV; j++)
+        if (i0 + j * 256 < n4) v[j] = ((const floatx4 *)X)[i0 + j * 256];
+#pragma unroll
+    for (uint32_t j = 0; j < XV; j++)
+        if (i0 + j * 256 < n4)
+            ((half4 *)Xh)[i0 + j * 256] =
+                half4{(_Float16)v[j][0], (_Float16)v[j][1], (_Float16)v[j][2], (_Float16)v[j][3]};
 }
 
 // Work split.  The first `full` tiles (a multiple of the CU count = one per
@@ -343,7 +395,6 @@ __global__ __launch_bounds__(512, 1) void gemm_q4k_w8_kernel(const uint8_t *__re
     typedef __attribute__((address_space(3))) void lds_void;
     lds_void *const xdst = (lds_void *)(&Bs[kh][0][0] + (wr * 4) * 1024);
 
-    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
     struct WRegs {
         u32x4v h0, h1, q0, q1;
     };
@@ -373,37 +424,7 @@ __global__ __launch_bounds__(512, 1) void gemm_q4k_w8_kernel(const uint8_t *__re
                                              16, 0, 0);
     };
     auto dq_row = [&](const u32x4v hdr, const u32x4v qv, uint32_t g, float vf, u32x4v *a) {
-        // every loaded dword counts as used here: a dword that a group does
-        // not need would otherwise be reused as a temporary while its load
-        // is still in flight, and that write has to wait for the load
-        asm volatile("" ::"v"(hdr), "v"(qv));
-        uint32_t sc0, mn0, sc1, mn1;
-        q4k_scale_min_pair(make_uint4(hdr[0], hdr[1], hdr[2], hdr[3]), g, sc0, mn0, sc1, mn1);
-        const float d = h2f(hdr[0] & 0xFFFF) * vf, dmin = h2f(hdr[0] >> 16) * vf;
-        const half2v a0 = (half2v)(_Float16)(d * (float)sc0), o0 = (half2v)(_Float16)(-dmin * (float)mn0);
-        const half2v a1 = (half2v)(_Float16)(d * (float)sc1), o1 = (half2v)(_Float16)(-dmin * (float)mn1);
-        const half2v m1024 = (half2v)(_Float16)-1024.0f;
-        uint32_t lo[8], hi[8];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t v = qv[i];
-            const uint32_t p01 = __builtin_amdgcn_perm(v, v, 0x0C010C00u);
-            const uint32_t p23 = __builtin_amdgcn_perm(v, v, 0x0C030C02u);
-            const uint32_t l01 = gbfi(0x000F000Fu, p01), l23 = gbfi(0x000F000Fu, p23);
-            const uint32_t h01 = gbfi(0x000F000Fu, p01 >> 4), h23 = gbfi(0x000F000Fu, p23 >> 4);
-            auto dq = [&](uint32_t x, half2v sa_, half2v so) {
-                const half2v q = __builtin_bit_cast(half2v, x) + m1024;
-                return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, sa_, so));
-            };
-            lo[2 * i] = dq(l01, a0, o0);
-            lo[2 * i + 1] = dq(l23, a0, o0);
-            hi[2 * i] = dq(h01, a1, o1);
-            hi[2 * i + 1] = dq(h23, a1, o1);
-        }
-        a[0] = u32x4v{lo[0], lo[1], lo[2], lo[3]};
-        a[1] = u32x4v{lo[4], lo[5], lo[6], lo[7]};
-        a[2] = u32x4v{hi[0], hi[1], hi[2], hi[3]};
-        a[3] = u32x4v{hi[4], hi[5], hi[6], hi[7]};
+        q4k_dq_mfma_a(hdr, qv, g, vf, a);
     };
     // B reads: MFMA kk takes chunk 2 h + (kk & 1) + 4 (kk >> 1) of token
     // 32 jn + lane % 32; jn and the stage are immediate offsets
@@ -569,6 +590,115 @@ __global__ __launch_bounds__(512, 1) void gemm_q4k_w8_kernel(const uint8_t *__re
                 }
             }
         }
+}
+
+// ------------------------------------------------------------------------
+// Leftover tiles of the wide-tile launch (the tiles past the last whole
+// round of one tile per CU, 16 of them at pp512).  Each 256 x 128 tile is
+// cut into 16 pieces of 64 rows x 32 tokens over the whole K, one 512-thread
+// workgroup per piece: wavefront w takes the 64-weight code-group steps
+// w, w + 8, ... of K (weights and activations straight into registers, two
+// steps in flight), with two 32x32x16 f16 MFMAs per step, and the eight
+// partial tiles are added through LDS in wavefront order.  Every output is
+// written once, with no partial tiles in memory and no second kernel, and
+// 16 x the leftover count of small workgroups spread over all the CUs.
+constexpr uint32_t QT_BM = 64, QT_BN = 32;
+
+template <int NW, int D>
+__global__ __launch_bounds__(NW * 64) void gemm_q4k_thin_kernel(const uint8_t *__restrict__ W,
+                                                              uint64_t row_bytes, uint32_t K, uint32_t M,
+                                                              const _Float16 *__restrict__ Xh, uint32_t N,
+                                                              float *__restrict__ Y, uint32_t tile0,
+                                                              uint32_t tiles_n, uint32_t pieces) {
+    __shared__ float red[NW][32][64];  // [wavefront][accumulator][lane]
+    // (pieces in plain order: a contiguous piece range per XCD measured
+    // the same)
+    const uint32_t pc = blockIdx.x;
+    if (pc >= pieces) return;
+    const uint32_t tile = tile0 + pc / 16;
+    const uint32_t m0 = tile / tiles_n * QW_BM + (pc % 16) / 4 * QT_BM;
+    const uint32_t n0 = tile % tiles_n * QG_BN + (pc % 4) * QT_BN;
+    if (m0 >= M || n0 >= N) return;  // (uniform over the workgroup)
+    const uint32_t t = threadIdx.x, lane = t & 63, h = lane >> 5;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const uint32_t rm = m0 + (lane & 31);
+    const uint8_t *w0 = W + (uint64_t)min(rm, M - 1) * row_bytes;
+    const uint8_t *w1 = W + (uint64_t)min(rm + 32, M - 1) * row_bytes;
+    const _Float16 *xr = Xh + (uint64_t)min(n0 + (lane & 31), N - 1) * K;
+    const uint32_t steps = K / QG_BK;
+
+    struct Regs {
+        u32x4v h0, h1, q0, q1, x[4];
+    };
+    // step s: code group s % 4 of superblock s / 4; activation operand kk
+    // is chunk 2 h + (kk & 1) + 4 (kk >> 1) of the step's 64 k (the order
+    // q4k_dq_mfma_a gives the weights).  Past the end a load re-reads the
+    // last step (a cache hit), so every load is unconditional.
+    auto load = [&](uint32_t s, Regs &r) {
+        s = min(s, steps - 1);
+        const uint64_t sbo = (uint64_t)(s >> 2) * 144, qo = sbo + 16 + (s & 3) * 32 + 16 * h;
+        r.h0 = *(const u32x4v *)(w0 + sbo);
+        r.h1 = *(const u32x4v *)(w1 + sbo);
+        r.q0 = *(const u32x4v *)(w0 + qo);
+        r.q1 = *(const u32x4v *)(w1 + qo);
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++)
+            r.x[kk] = *(const u32x4v *)(xr + (uint64_t)s * QG_BK + 8 * (2 * h + (kk & 1) + 4 * (kk >> 1)));
+    };
+    typedef float floatx16 __attribute__((ext_vector_type(16)));
+    floatx16 acc[2] = {floatx16{}, floatx16{}};
+    auto compute = [&](uint32_t s, const Regs &r) {
+        u32x4v a[2][4];
+        q4k_dq_mfma_a(r.h0, r.q0, s & 3, 1.0f, a[0]);
+        q4k_dq_mfma_a(r.h1, r.q1, s & 3, 1.0f, a[1]);
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a[i][kk]),
+                                                                __builtin_bit_cast(half8, r.x[kk]), acc[i], 0, 0,
+                                                                0);
+    };
+    // wavefront w takes steps w, w + NW, ...; D of them in flight
+    Regs r[D];
+#pragma unroll
+    for (int j = 0; j < D; j++) load(wave + j * NW, r[j]);
+    for (uint32_t s = wave; s < steps; s += D * NW) {
+#pragma unroll
+        for (int j = 0; j < D; j++) {
+            if (s + j * NW < steps) compute(s + j * NW, r[j]);
+            load(s + (j + D) * NW, r[j]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) red[wave][16 * i + e][lane] = acc[i][e];
+    __syncthreads();
+    // the 2048 outputs as 512 groups of 4 rows: group q = t + 64 NW c holds
+    // accumulators 4 (q / 64) .. + 3 of lane q % 64, added over the
+    // wavefronts in order; rows 32 (g / 4) + 8 (g % 4) + 4 h + j, g = q / 64
+    for (uint32_t q = t; q < 512; q += NW * 64) {
+        const uint32_t g = q >> 6;
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            float a = red[0][4 * g + j][lane];
+#pragma unroll
+            for (int w = 1; w < NW; w++) a += red[w][4 * g + j][lane];
+            v[j] = a;
+        }
+        const uint32_t n = n0 + (lane & 31), m = m0 + 32 * (g / 4) + 8 * (g % 4) + 4 * h;
+        if (n >= N) continue;
+        float *dst = Y + (uint64_t)n * M + m;
+        if (m + 3 < M && (M & 3) == 0) {
+            *(float4 *)dst = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (m + j < M) dst[j] = v[j];
+        }
+    }
 }
 
 }  // namespace okf

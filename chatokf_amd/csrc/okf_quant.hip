@@ -53,6 +53,7 @@ struct okf_ctx {
     int gemv_s = 0;      // K split across a workgroup's wavefronts (0 = auto)
     int gemv_wide = -1;  // one-workgroup-per-CU matvec: -1 auto, 0 never, 1 where it fits
     int gemm_ks = 0;     // wide-tile GEMM: K ranges per remainder tile (0 = auto)
+    int gemm_thin = 0;   // leftover-tile kernel variant (A/B switch)
     int gemm_ng = 4;     // wide-tile GEMM: N tiles that share an XCD's row blocks
     uint32_t cus = 256;  // compute units of the device
     double fault_rate = 0;
@@ -337,8 +338,10 @@ int grow_part(okf_ctx *c, size_t need) {
 
 // The wide-tile Q4_K GEMM (gemm_q4k_w8_kernel): one 256 x 128 tile per CU.
 // Whole rounds of `cus` tiles stay whole; each remaining tile is split over
-// ks K ranges of whole superblocks (ks * remaining <= cus), whose partial
-// tiles gemm_split_sum_kernel adds in K order.
+// 16 thin pieces of 64 rows x 32 tokens (gemm_q4k_thin_kernel), or, with
+// OKF_GEMM_KS set, over ks K ranges of whole superblocks
+// (ks * remaining <= cus), whose partial tiles gemm_split_sum_kernel adds in
+// K order.
 int launch_gemm_q4k_w(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t M, uint32_t N,
                       float *Y) {
     const uint32_t tm = (M + QW_BM - 1) / QW_BM, tn = (N + QG_BN - 1) / QG_BN, sbs = K / 256;
@@ -351,6 +354,26 @@ int launch_gemm_q4k_w(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uin
     if (sp.ks < 2) {
         sp.full = sp.tiles + 7 & ~7u;  // no split: every tile whole
         sp.ks = 1;
+    } else if (c->gemm_ks == 0) {
+        // the leftover tiles as 16 thin pieces each (gemm_q4k_thin_kernel)
+        if (sp.full) {
+            sp.ks = 1;
+            sp.full_xcd = sp.full / 8;
+            hipLaunchKernelGGL((gemm_q4k_w8_kernel<2, 2>), dim3(sp.full), dim3(512), 0, c->stream, W, rb, K, M,
+                               (const _Float16 *)c->xh, N, Y, sp);
+        }
+        auto thin = [&](auto kern, uint32_t nw) {
+            hipLaunchKernelGGL(kern, dim3((rem * 16 + 7) & ~7u), dim3(nw * 64), 0, c->stream, W, rb, K, M,
+                               (const _Float16 *)c->xh, N, Y, sp.full, tn, rem * 16);
+        };
+        switch (c->gemm_thin) {
+            case 1: thin(gemm_q4k_thin_kernel<8, 2>, 8); break;
+            case 2: thin(gemm_q4k_thin_kernel<8, 4>, 8); break;
+            case 3: thin(gemm_q4k_thin_kernel<4, 2>, 4); break;
+            case 5: thin(gemm_q4k_thin_kernel<4, 6>, 4); break;
+            default: thin(gemm_q4k_thin_kernel<4, 4>, 4); break;
+        }
+        return OKF_OK;
     }
     sp.full_xcd = sp.full / 8;
     sp.units = sp.ks > 1 ? rem * sp.ks : 0;
@@ -389,8 +412,8 @@ int launch_gemm(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t 
             c->xh_bytes = need;
         }
         const uint64_t n4 = (uint64_t)N * K / 4;
-        hipLaunchKernelGGL(x_to_f16_kernel, dim3((uint32_t)((n4 + 255) / 256)), dim3(256), 0, c->stream,
-                           X, c->xh, n4);
+        hipLaunchKernelGGL(x_to_f16_kernel, dim3((uint32_t)((n4 + 256 * XV - 1) / (256 * XV))), dim3(256), 0,
+                           c->stream, X, c->xh, n4);
         return launch_gemm_q4k_w(c, W, rb, K, M, N, Y);
     }
     dim3 grid((N + GB_N - 1) / GB_N, (M + GB_M - 1) / GB_M);
@@ -566,6 +589,7 @@ int okf_ctx_create(int device, okf_ctx **out) {
         if (const char *e = getenv("OKF_GEMV_WIDE")) c->gemv_wide = atoi(e);
         if (const char *e = getenv("OKF_GEMM_KS")) c->gemm_ks = atoi(e);
         if (const char *e = getenv("OKF_GEMM_NG")) c->gemm_ng = atoi(e);
+        if (const char *e = getenv("OKF_GEMM_THIN")) c->gemm_thin = atoi(e);
     } else if (device != -1) {
         delete c;
         return OKF_E_ARG;

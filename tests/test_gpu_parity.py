@@ -367,11 +367,12 @@ def test_parallel_group_matches_single_calls(enc):
 # (The metric is relative to max|ref| over the output, so every case keeps
 # enough outputs for that maximum to be representative; a single dot product
 # can cancel to near zero, where fp16 staging error is not bounded by 1e-3.)
-# The Q4_K kernel (256-row x 128-token tiles, one per CU) splits the tiles
-# beyond whole rounds of 256 over K ranges of whole superblocks: the small
-# cases are all split (2..9 ways, odd superblock counts leave the odd K half
-# empty); (8192, 512, 1024) is exactly 256 whole tiles with eight N tiles
-# per row block, grouped four to an XCD.
+# The Q4_K kernel (256-row x 128-token tiles, one per CU) runs the tiles
+# beyond whole rounds of 256 as 16 thin pieces each (64 rows x 32 tokens,
+# whole K): the small cases are all thin pieces (M and N not multiples of the
+# piece, K of 1 superblock leaves wavefronts without steps); (8192, 512,
+# 1024) is exactly 256 whole tiles with eight N tiles per row block, grouped
+# four to an XCD.
 TILE = [(Q8_0, 300, 2048, 37), (Q2_0, 130, 1024, 129), (Q4_K, 260, 2304, 77), (IQ2_XXS, 129, 1536, 6),
         (Q4_K, 1, 256, 64), (Q8_0, 5, 96, 200), (Q4_K, 4224, 256, 512), (Q4_K, 1000, 512, 300),
         (Q4_K, 8192, 512, 1024),
@@ -390,6 +391,34 @@ def test_tile_gemm_matches_oracle(enc, t, M, K, N):
     assert rel(got, ref) <= TOL
     if N > 5:  # the auto path takes the tile for N > 5
         assert np.array_equal(run_gemm(enc, t, M, K, w, X), got)
+
+
+# With OKF_GEMM_KS=k the leftover tiles are split over k K ranges of whole
+# superblocks instead (partial tiles added by a second kernel in K order):
+# 2..9 ways, odd superblock counts leave the odd K half empty.
+@pytest.fixture(scope="module")
+def enc_ksplit():
+    import os
+    os.environ["OKF_GEMM_KS"] = "5"
+    try:
+        e = ok.Enc(0)
+    finally:
+        del os.environ["OKF_GEMM_KS"]
+    yield e
+    e.close()
+
+
+@pytest.mark.parametrize("M,K,N", [(260, 2304, 77), (4224, 256, 512), (1000, 512, 300), (17408, 2560, 512)])
+def test_q4_k_ksplit_matches_thin(enc, enc_ksplit, M, K, N):
+    say("ksplit", M, K, N)
+    w = weights(Q4_K, M, K, 21)
+    X = acts(N, K, 22)
+    ref = oracle.matmul(Q4_K, w, K, M, X).astype(np.float64) if M * N <= 300_000 else None
+    got = run_gemm(enc_ksplit, Q4_K, M, K, w, X)
+    thin = run_gemm(enc, Q4_K, M, K, w, X)
+    if ref is not None:
+        assert rel(got, ref) <= TOL
+    assert rel(got, thin.astype(np.float64)) <= 1e-3
 
 
 def test_q4_k_pp512_full_config(enc):
