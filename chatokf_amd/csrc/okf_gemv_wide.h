@@ -35,8 +35,8 @@ __device__ __forceinline__ uint32_t gw_start(uint32_t z, uint32_t T) {
     return (uint32_t)((uint64_t)z * T / GW_SLOTS);
 }
 
-// Dynamic LDS: [replicated IQ2_XXS tables], NC columns of staged pairs
-// (cs uint32 each), NC columns of 32-weight sums (xcs floats each), then
+// Dynamic LDS: [replicated IQ2_XXS tables], NC columns of staged digit
+// planes (cs uint32 each), NC columns of group data (gcs float4 each), then
 // the parked partials [64 slots][kmax rows][NC].
 template <int F, int NC, int D, uint32_t SP>
 __global__ __launch_bounds__(GW_THREADS) void gemv_wide_kernel(const uint8_t *__restrict__ W,
@@ -55,11 +55,12 @@ __global__ __launch_bounds__(GW_THREADS) void gemv_wide_kernel(const uint8_t *__
     if (r0 == r1) return;  // whole workgroup: no rows (M < grid)
     const uint32_t units = K / UW, P = (units + L - 1) / L;  // steps per row
     const uint32_t T = (r1 - r0) * P, s0 = gw_start(z, T), s1 = gw_start(z + 1, T);
-    const uint32_t cunits = P * L, cs = cunits * (UW / 2), xcs = cunits * (UW / 32);
+    constexpr uint32_t UG = unit_groups<F>();
+    const uint32_t cunits = P * L, cs = cunits * unit_chunks<F>() * 4, gcs = cunits * UG;
     u32x4 *tab = lds;
     uint32_t *xs = (uint32_t *)(lds + TAB);
-    float *xsum = (float *)(xs + NC * cs);
-    float *part = xsum + NC * xcs;
+    floatx4 *gdp = (floatx4 *)(xs + NC * cs);
+    float *part = (float *)(gdp + NC * gcs);
 
     // Weight loads walk the slot's steps in order: step ls is unit
     // lsu L + i of row lrow.  The cursor stops at the range's last step, so
@@ -89,18 +90,12 @@ __global__ __launch_bounds__(GW_THREADS) void gemv_wide_kernel(const uint8_t *__
 #pragma unroll
     for (uint32_t k = 0; k < TPT; k++) trow[k] = tab_g[(tid + k * GW_THREADS) / L];
     const uint32_t nslots = units * SL;  // <= SP * GW_THREADS (host-checked)
-    floatx4 A[SP][NC], B[SP][NC];
+    float v[SP][NC][8];
 #pragma unroll
     for (uint32_t p = 0; p < SP; p++) {
         const uint32_t q = min(p * GW_THREADS + tid, nslots - 1), u = q / SL;
-        uint32_t kb;
-        const uint32_t ka = slot_first<F>(q % SL, kb);
 #pragma unroll
-        for (int n = 0; n < NC; n++) {
-            const uint64_t xo = (uint64_t)n * K + unit_x_base<F>(u);
-            A[p][n] = *(const floatx4 *)(X + xo + ka);
-            B[p][n] = *(const floatx4 *)(X + xo + kb);
-        }
+        for (int n = 0; n < NC; n++) load_slot<F>(X + (uint64_t)n * K + unit_x_base<F>(u), q % SL, v[p][n]);
     }
     __builtin_amdgcn_sched_barrier(0);  // (keep the order of the loads)
     Unit<F, 1> buf[D];
@@ -110,19 +105,11 @@ __global__ __launch_bounds__(GW_THREADS) void gemv_wide_kernel(const uint8_t *__
 
 #pragma unroll
     for (uint32_t k = 0; k < TPT; k++) tab[tid + k * GW_THREADS] = trow[k];
-    // x as packed fp16 slots and per-32 sums (as stage_x)
+    // x as digit planes and group data (as stage_x)
 #pragma unroll
     for (uint32_t p = 0; p < SP; p++) {
-        const uint32_t q = p * GW_THREADS + tid, u = q / SL, sidx = q % SL;
-#pragma unroll
-        for (int n = 0; n < NC; n++) {
-            const u32x4 v = slot_pack<F>(A[p][n], B[p][n]);
-            const float pt = quad_sum(slot_bias<F>(v, sidx));
-            if (q < nslots) {
-                *(u32x4 *)(xs + n * cs + xs_index<F, L>(u, 4 * sidx)) = v;
-                if ((q & 3) == 0) xsum[n * xcs + q / 4] = pt;
-            }
-        }
+        const uint32_t q = p * GW_THREADS + tid;
+        stage_slot<F, NC, L, false>(v[p], q / SL, q % SL, q < nslots, xs, cs, gdp, gcs);
     }
     __syncthreads();
 
@@ -146,7 +133,7 @@ __global__ __launch_bounds__(GW_THREADS) void gemv_wide_kernel(const uint8_t *__
                 const uint32_t u = su * L + i;
                 if (u < units)
                     Compute<F, NC, 1, (F == IQ2_XXS ? L : 1)>::run(
-                        buf[j], xs + xs_index<F, L>(u, 0), 4 * L, cs, xsum + u * (UW / 32), xcs, u, acc,
+                        buf[j], xs + xs_index<F, L>(u, 0), 4 * L, cs, gdp + u * UG, gcs, u, acc,
                         tab + i);
                 if (++su == P && t + j + 1 < s1) {  // next step starts a row
                     flush();
@@ -195,12 +182,27 @@ __global__ __launch_bounds__(GW_THREADS) void gemv_wide_kernel(const uint8_t *__
 // 17408 x 5120: N = 2 18.6 -> 16.2 us, N = 4 22.7 -> 17.3 us.
 //
 // Activations in LDS, per unit u: 8 k-slots s of 8 halves for each of the 4
-// columns c at 16-byte slot u * 36 + s * 4 + c (4 slots of padding per unit
-// put the 16 lanes of a read on 16 distinct 16-byte bank groups).
+// columns c, hi at 16-byte slot u * 68 + s * 4 + c and lo 32 slots further
+// (the 4 slots of padding per unit put the 16 lanes of a read on 16
+// distinct 16-byte bank groups); after them the per-32 scales, one float4
+// (the 4 columns) per (unit, sub-block).  The tables are replicated 8 times
+// (lane i reads copy i % 8), which leaves room for the hi / lo activations
+// of 4 columns at K = 5120.
 constexpr uint32_t GM_WAVES = GW_THREADS / 64;
-constexpr uint32_t GM_UNIT = 36;  // 16-byte x slots per unit
+constexpr uint32_t GM_UNIT = 68;  // 16-byte x slots per unit
+constexpr uint32_t GM_COPIES = 8;
+constexpr uint32_t GM_TAB = 384 * GM_COPIES;
 
 typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
+    const half2v h = {(_Float16)a, (_Float16)b};
+    return __builtin_bit_cast(uint32_t, h);
+}
+// 8 values in order as 4 packed fp16 pairs
+__device__ __forceinline__ u32x4 pack_h8(floatx4 A, floatx4 B) {
+    return u32x4{pack_h2(A[0], A[1]), pack_h2(A[2], A[3]), pack_h2(B[0], B[1]), pack_h2(B[2], B[3])};
+}
 
 __device__ __forceinline__ uint32_t gm_start(uint32_t z, uint32_t T) {
     return (uint32_t)((uint64_t)z * T / GM_WAVES);
@@ -224,14 +226,16 @@ __global__ __launch_bounds__(GW_THREADS) void gemv_wide_iq2mm_kernel(const uint8
     const uint32_t units = K / UW, P = (units + L - 1) / L;
     const uint32_t nq = (r1 - r0 + 3) / 4, T = nq * P, s0 = gm_start(z, T), s1 = gm_start(z + 1, T);
     u32x4 *tab = lds;
-    u32x4 *xs = lds + GW_TAB;
-    float *part = (float *)(xs + (size_t)P * L * GM_UNIT);
+    u32x4 *xs = lds + GM_TAB;
+    floatx4 *xf = (floatx4 *)(xs + (size_t)P * L * GM_UNIT);
+    float *part = (float *)(xf + (size_t)P * L * 2);
 
     // loads: table entries, then activations, then the weight ring
-    constexpr uint32_t TPT = GW_TAB / GW_THREADS;
+    constexpr uint32_t TPT = GM_TAB / GW_THREADS;
+    static_assert(GM_TAB % GW_THREADS == 0, "table entries per thread");
     u32x4 trow[TPT];
 #pragma unroll
-    for (uint32_t k = 0; k < TPT; k++) trow[k] = tab_g[(tid + k * GW_THREADS) / L];
+    for (uint32_t k = 0; k < TPT; k++) trow[k] = tab_g[(tid + k * GW_THREADS) / GM_COPIES];
     const uint32_t nx = units * 8 * 4;  // (unit, k-slot, column) entries, <= SP * 1024
     floatx4 A[SP], B[SP];
 #pragma unroll
@@ -267,19 +271,43 @@ __global__ __launch_bounds__(GW_THREADS) void gemv_wide_iq2mm_kernel(const uint8
     for (uint32_t k = 0; k < TPT; k++) tab[tid + k * GW_THREADS] = trow[k];
 #pragma unroll
     for (uint32_t p = 0; p < SP; p++) {
+        // (c, sl, u) = lane bits 0-1, 2-4, 5-: a 32-weight group of column c
+        // is k-slots 0-3 or 4-7, the lanes that differ in bits 2 and 3; its
+        // scale and hi / lo split as split_slot's
         const uint32_t e = p * GW_THREADS + tid;
+        const uint32_t c = e & 3, sl = (e >> 2) & 7, u = e >> 5;
+        float m = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) m = fmaxf(m, fmaxf(fabsf(A[p][k]), fabsf(B[p][k])));
+        m = fmaxf(m, __shfl_xor(m, 4, 64));
+        m = fmaxf(m, __shfl_xor(m, 8, 64));
+        const int ex = min(__builtin_amdgcn_frexp_expf(m), 127);
+        floatx4 Ah, Al, Bh, Bl;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float a = __builtin_amdgcn_ldexpf(A[p][k], -ex), b = __builtin_amdgcn_ldexpf(B[p][k], -ex);
+            Ah[k] = (float)(_Float16)a;
+            Bh[k] = (float)(_Float16)b;
+            Al[k] = a - Ah[k];
+            Bl[k] = b - Bh[k];
+        }
+        u32x4 hi = pack_h8(Ah, Bh), lo = pack_h8(Al, Bl);
+        float f = __builtin_amdgcn_ldexpf(1.0f, ex);
+        if (c >= (uint32_t)NC) {
+            hi = lo = u32x4{0, 0, 0, 0};
+            f = 0;
+        }
         if (e < nx) {
-            const uint32_t c = e & 3, sl = (e >> 2) & 7, u = e >> 5;
-            u32x4 v = slot_pack<IQ2_XXS>(A[p], B[p]);
-            if (c >= (uint32_t)NC) v = u32x4{0, 0, 0, 0};
-            xs[u * GM_UNIT + sl * 4 + c] = v;
+            xs[u * GM_UNIT + sl * 4 + c] = hi;
+            xs[u * GM_UNIT + 32 + sl * 4 + c] = lo;
+            if ((sl & 3) == 0) ((float *)xf)[(u * 2 + (sl >> 2)) * 4 + c] = f;
         }
     }
     __syncthreads();
 
     floatx4 tot = {0, 0, 0, 0};
     uint32_t su = s0 % P, k = 0;
-    const u32x4 *tl = tab + (lane & (L - 1));  // this lane's table copy
+    const u32x4 *tl = tab + (lane & (GM_COPIES - 1));  // this lane's table copy
     auto flush = [&]() {
 #pragma unroll
         for (int c = 0; c < 4; c++) {
@@ -309,19 +337,21 @@ __global__ __launch_bounds__(GW_THREADS) void gemv_wide_iq2mm_kernel(const uint8
                     floatx4 acc = {0, 0, 0, 0};
 #pragma unroll
                     for (int l = 0; l < 4; l++) {
-                        const u32x4 gv = tl[((a0 >> (8 * l)) & 0xFF) * L];
-                        const u32x4 sg = tl[(256 + ((a1 >> (7 * l)) & 127)) * L];
-                        const u32x4 xv = xp[(4 * sb + l) * 4];
+                        const u32x4 gv = tl[((a0 >> (8 * l)) & 0xFF) * GM_COPIES];
+                        const u32x4 sg = tl[(256 + ((a1 >> (7 * l)) & 127)) * GM_COPIES];
+                        const u32x4 xv = xp[(4 * sb + l) * 4], xl = xp[32 + (4 * sb + l) * 4];
                         const u32x4 wv = gv ^ sg;
-                        acc = __builtin_amdgcn_mfma_f32_4x4x4f16(
-                            __builtin_bit_cast(half4v, uint2{xv[0], xv[1]}),
-                            __builtin_bit_cast(half4v, uint2{wv[0], wv[1]}), acc, 0, 0, 0);
-                        acc = __builtin_amdgcn_mfma_f32_4x4x4f16(
-                            __builtin_bit_cast(half4v, uint2{xv[2], xv[3]}),
-                            __builtin_bit_cast(half4v, uint2{wv[2], wv[3]}), acc, 0, 0, 0);
+#pragma unroll
+                        for (int h = 0; h < 2; h++) {
+                            const half4v wh = __builtin_bit_cast(half4v, uint2{wv[2 * h], wv[2 * h + 1]});
+                            acc = __builtin_amdgcn_mfma_f32_4x4x4f16(
+                                __builtin_bit_cast(half4v, uint2{xv[2 * h], xv[2 * h + 1]}), wh, acc, 0, 0, 0);
+                            acc = __builtin_amdgcn_mfma_f32_4x4x4f16(
+                                __builtin_bit_cast(half4v, uint2{xl[2 * h], xl[2 * h + 1]}), wh, acc, 0, 0, 0);
+                        }
                     }
                     const float db = live ? h2f(w.d[0]) * (0.5f + (float)(a1 >> 28)) * 0.25f : 0.0f;
-                    tot += db * acc;
+                    tot += db * (acc * xf[min(u, units - 1) * 2 + sb]);
                 }
                 if (++su == P && st + j + 1 < s1) {  // next step starts a row quad
                     flush();

@@ -46,7 +46,8 @@ struct okf_ctx {
     hipStream_t stream = nullptr;
     uint2 *grid = nullptr;  // 256 IQ2_XXS grid entries in device memory
     uint8_t *grids = nullptr;  // the grids of IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S / IQ1_M (GT_* offsets)
-    okf::u32x4 *tab = nullptr;   // IQ2_XXS fp16 grid (256 x 8 halves) + sign masks (128)
+    okf::u32x4 *tab = nullptr;   // IQ2_XXS fp16 grid (256 x 8 halves) + sign masks (128): MFMA kernel
+    okf::u32x4 *tab8 = nullptr;  // IQ2_XXS int8 grid (256) + sign byte masks (128): dot4 kernels
     size_t max_lds = 65536;  // dynamic LDS a workgroup may use
     // matvec tuning (defaults chosen per shape; OKF_GEMV_* environment
     // variables override them for measurements)
@@ -145,6 +146,29 @@ void build_iq2_tables(uint32_t *t) {
     }
 }
 
+// The same tables for the integer dot-product kernels: grid entry e as its 8
+// unsigned bytes {lo, hi, 0, 0}; sign entry s7 as the byte mask M (0xFF per
+// negative weight) and M & 0x01010101, {M.lo, M.hi, M1.lo, M1.hi}, so that a
+// signed weight byte is (g ^ M) + M1.
+void build_iq2_tables8(uint32_t *t) {
+    for (int e = 0; e < 256; e++) {
+        const uint64_t g = okf_iq2xxs_grid_host[e];
+        t[e * 4 + 0] = (uint32_t)g;
+        t[e * 4 + 1] = (uint32_t)(g >> 32);
+        t[e * 4 + 2] = t[e * 4 + 3] = 0;
+    }
+    for (int s7 = 0; s7 < 128; s7++) {
+        const uint32_t s = s7 | ((__builtin_popcount(s7) & 1u) << 7);
+        uint32_t m[2] = {0, 0};
+        for (int j = 0; j < 8; j++)
+            if ((s >> j) & 1) m[j >> 2] |= 0xFFu << (8 * (j & 3));
+        t[(256 + s7) * 4 + 0] = m[0];
+        t[(256 + s7) * 4 + 1] = m[1];
+        t[(256 + s7) * 4 + 2] = m[0] & 0x01010101u;
+        t[(256 + s7) * 4 + 3] = m[1] & 0x01010101u;
+    }
+}
+
 template <int F, int NC, int S, bool SILU, int DX = 0>
 void launch_gemv_s(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32_t K,
                    uint32_t cunits, size_t lds) {
@@ -183,7 +207,7 @@ void launch_gemv_s(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32
     g.n = (uint32_t)n;
     // the tables the compute reads: IQ2_XXS's LDS rows (copied from c->tab),
     // or the grid formats' device-memory grids
-    const u32x4 *tabs = grid_fmt(F) ? (const u32x4 *)c->grids : c->tab;
+    const u32x4 *tabs = grid_fmt(F) ? (const u32x4 *)c->grids : c->tab8;
     hipLaunchKernelGGL((gemv_kernel<F, NC, R, D, S, SILU>), dim3(total), dim3(64 * WAVES), lds, c->stream,
                        g, rb, K, tabs, cunits);
 }
@@ -207,7 +231,7 @@ void launch_wide_sp(okf_ctx *c, const GemvCall &call, uint64_t rb, uint32_t K, u
         attr = true;
     }
     hipLaunchKernelGGL((gemv_wide_kernel<F, NC, D, SP>), dim3(G), dim3(GW_THREADS), lds, c->stream, call.W,
-                       rb, K, call.M, call.X, call.Y, c->tab, kmax);
+                       rb, K, call.M, call.X, call.Y, c->tab8, kmax);
 }
 
 // Where the one-workgroup-per-CU kernel measured faster on MI355X than the
@@ -232,7 +256,7 @@ bool launch_iq2mm(okf_ctx *c, const GemvCall &call, uint64_t rb, uint32_t K) {
     const uint32_t G = std::min(c->cus, call.M), units = K / 64, P = (units + GV_L - 1) / GV_L;
     const uint64_t nq = ((call.M + G - 1) / G + 3) / 4, lmax = (nq * P + GM_WAVES - 1) / GM_WAVES;
     const uint32_t kmax = (uint32_t)((lmax + P - 1) / P + 1);
-    const size_t lds = GW_TAB * 16 + (size_t)P * GV_L * GM_UNIT * 16 + (size_t)GM_WAVES * kmax * 4 * NC * 4;
+    const size_t lds = GM_TAB * 16 + (size_t)P * GV_L * (GM_UNIT + 2) * 16 + (size_t)GM_WAVES * kmax * 4 * NC * 4;
     const uint32_t sp = (units * 32 + GW_THREADS - 1) / GW_THREADS;
     if (lds > c->max_lds || sp > 3 || nq * P * GM_WAVES >= (1ull << 32)) return false;
     constexpr int D = 4;
@@ -266,7 +290,7 @@ bool launch_gemv_wide(okf_ctx *c, const GemvCall &call, uint64_t rb, uint32_t K)
     const uint64_t nmax = (call.M + G - 1) / G, lmax = (nmax * P + GW_SLOTS - 1) / GW_SLOTS;
     const uint32_t kmax = (uint32_t)((lmax + P - 1) / P + 1);
     const uint64_t cunits = (uint64_t)P * GV_L;
-    const size_t lds = (F == IQ2_XXS ? GW_TAB * 16 : 0) + (size_t)NC * cunits * (UW * 2 + UW / 32 * 4) +
+    const size_t lds = (F == IQ2_XXS ? GW_TAB * 16 : 0) + (size_t)NC * cunits * unit_lds_bytes<F>() +
                        (size_t)GW_SLOTS * kmax * NC * sizeof(float);
     // one staging round (x slots per thread <= SP), step indices in 32 bits
     const uint32_t nslots = K / 8, sp = (nslots + GW_THREADS - 1) / GW_THREADS;
@@ -290,8 +314,9 @@ void launch_gemv_nc(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint3
     constexpr uint32_t UW = unit_weights<F>();
     const size_t tab = F == IQ2_XXS ? 384 * 16 : 0;
     const uint32_t units = K / UW;
-    // stage all of x when it fits, else in chunks of 64-unit groups
-    const size_t per_unit = (size_t)NC * (UW * 2 + UW / 32 * 4);
+    // stage all of x when it fits, else in chunks of 64-unit groups (per
+    // 32 weights: three 32-byte digit planes and a float4 of group data)
+    const size_t per_unit = (size_t)NC * unit_lds_bytes<F>();
     const size_t red = 4 * GV_SLOTS * NC * 4 * sizeof(float);
     uint32_t cunits = (units + 63) / 64 * 64;
     const size_t budget = c->max_lds - tab - red;
@@ -570,10 +595,14 @@ int okf_ctx_create(int device, okf_ctx **out) {
         build_iq2_tables(tabh);
         if (e == hipSuccess) e = hipMalloc((void **)&c->tab, sizeof(tabh));
         if (e == hipSuccess) e = hipMemcpy(c->tab, tabh, sizeof(tabh), hipMemcpyHostToDevice);
+        build_iq2_tables8(tabh);
+        if (e == hipSuccess) e = hipMalloc((void **)&c->tab8, sizeof(tabh));
+        if (e == hipSuccess) e = hipMemcpy(c->tab8, tabh, sizeof(tabh), hipMemcpyHostToDevice);
         if (e != hipSuccess) {
             if (c->grid) (void)hipFree(c->grid);
             if (c->grids) (void)hipFree(c->grids);
             if (c->tab) (void)hipFree(c->tab);
+            if (c->tab8) (void)hipFree(c->tab8);
             if (c->stream) (void)hipStreamDestroy(c->stream);
             delete c;
             return OKF_E_HIP;
@@ -607,6 +636,7 @@ int okf_ctx_destroy(okf_ctx *c) {
         (void)hipFree(c->grid);
         (void)hipFree(c->grids);
         (void)hipFree(c->tab);
+        (void)hipFree(c->tab8);
         if (c->xh) (void)hipFree(c->xh);
         if (c->part) (void)hipFree(c->part);
         (void)hipStreamDestroy(c->stream);

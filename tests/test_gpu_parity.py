@@ -1,9 +1,13 @@
 """GPU parity: the HIP library (through its C ABI) against the CPU oracle.
 
-Bars (written in each test): dequantized weights bit-identical; matvec,
-narrow matmul and tile GEMM outputs within max|gpu - ref| / max|ref| <= 1e-3
-(the reference's relative metric, LLM/Qwen/QwenMetalSelfTest.swift:441-445,
-at the north-star tolerance); narrow-N vs N x gemv within 1e-5
+Bars (written in each test): dequantized weights bit-identical; matvec and
+narrow (N = 2..5) outputs within max|gpu - ref| / max|ref| <= 1e-4 (the
+reference's relative metric, LLM/Qwen/QwenMetalSelfTest.swift:441-445, at
+the gate its own gemv self-test applies, :580), the activations being
+carried at fp32 precision as the reference's gemv reads them
+(LLM/metal/Kernels.metal:46-52, :1681-1690); tile GEMM outputs (fp16
+activation tiles, as the reference's gemm_mm stages them, Kernels.metal:282)
+within 1e-3, the north-star tolerance; narrow-N vs N x gemv within 1e-5
 (QwenMetalSelfTest.swift:478-483).
 """
 import ctypes
@@ -23,7 +27,8 @@ import chatokf_amd as ok  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
-TOL = 1e-3
+TOL = 1e-3      # tile GEMM (fp16 activation tiles)
+TOL_MV = 1e-4   # matvec / narrow: QwenMetalSelfTest.swift:580
 
 
 def say(*a):
@@ -123,7 +128,7 @@ def test_gemv_full_config(enc, name, t, M, K, seed):
     got = run_gemm(enc, t, M, K, w, x)[0]
     r = rel(got, ref)
     say("  rel", r)
-    assert r <= TOL
+    assert r <= TOL_MV
 
 
 # Shapes that exercise tails: M not a multiple of the rows per workgroup, a
@@ -137,12 +142,12 @@ EDGE = [(Q8_0, 1, 32), (Q8_0, 3, 96), (Q8_0, 4099, 2080), (Q2_0, 5, 128), (Q2_0,
     [(t, M, K) for t in (F32, F16, BF16) for M, K in ((3, 32), (4101, 1056))]
 
 
-def fp16_bound(t, w, K, M, x):
-    """Per-row bound on |y_gpu - y| from rounding x to fp16 (relative error
-    <= 2^-11 per element): 2^-11 sum_i |w_i x_i|, plus fp32 summation slack."""
+def l1_rows(t, w, K, M, x):
+    """Per-row sum_i |w_i x_i| in float64: the scale fp32 summation error is
+    relative to when a row's dot product cancels."""
     rb = row_bytes(t, K)
     W = np.stack([oracle.dequant(t, w[m * rb:(m + 1) * rb], K) for m in range(M)]).astype(np.float64)
-    return np.abs(W) @ np.abs(x.astype(np.float64)) * (2.0 ** -11 * 1.001) + 1e-6
+    return np.abs(W) @ np.abs(x.astype(np.float64))
 
 
 @pytest.mark.parametrize("t,M,K", EDGE)
@@ -152,20 +157,47 @@ def test_gemv_edges(enc, t, M, K):
     x = acts(1, K, 8)
     ref = oracle.matvec(t, w, K, M, x[0]).astype(np.float64)
     got = run_gemm(enc, t, M, K, w, x)[0]
-    # the kernel's arithmetic: the oracle on fp16-rounded x, up to fp32
-    # summation order and the cancellation of the 1024-bias of the fp16
-    # integer encoding (sum((1024 + q) x) - 1024 sum(x))
-    ref16 = oracle.matvec(t, w, K, M, x[0].astype(np.float16).astype(np.float32)).astype(np.float64)
-    slack = 2e-4 * np.abs(ref16).max()
-    assert np.abs(got - ref16).max() <= slack
-    # every row within the fp16-activation bound of the fp32 reference
+    r = rel(got, ref)
+    say("  rel", r)
+    # the reference's metric at its gemv gate, for every shape
+    assert r <= TOL_MV
+    # every row within fp32-summation distance of the oracle, measured
+    # against the row's sum of |w x| (meaningful also where a row cancels)
     if M <= 64:
-        assert (np.abs(got - ref) <= fp16_bound(t, w, K, M, x[0]) + slack).all()
-    # the reference's relative metric; with a handful of rows max|y| can be
-    # a cancelled sum, where the bound above is the meaningful check (IQ4_XS
-    # 2 x 512: 1.45e-3, the same on the CPU oracle fed fp16-rounded x)
-    if M >= 16:
-        assert rel(got, ref) <= TOL
+        assert (np.abs(got - ref) <= 2e-6 * l1_rows(t, w, K, M, x[0]) + 1e-30).all()
+
+
+# Activations of any fp32 magnitude: each 32-weight group carries its own
+# power-of-two scale, so tiny, huge and mixed-magnitude vectors keep the
+# reference's fp32 relative precision (no fp16 overflow or underflow).
+@pytest.mark.parametrize("t", [Q8_0, Q2_0, Q4_K, IQ2_XXS], ids=lambda t: NAMES[t])
+@pytest.mark.parametrize("scale", ["1e-20", "1e-5", "1e5", "1e20", "mixed"])
+def test_gemv_activation_range(enc, t, scale):
+    M, K = 1030, 2048
+    say("gemv range", NAMES[t], scale)
+    w = weights(t, M, K, 31)
+    x = acts(1, K, 32).copy()
+    if scale == "mixed":
+        x *= (10.0 ** np.random.default_rng(33).uniform(-8, 8, K)).astype(np.float32)
+    else:
+        x *= np.float32(float(scale))
+    ref = oracle.matvec(t, w, K, M, x[0]).astype(np.float64)
+    got = run_gemm(enc, t, M, K, w, x)[0]
+    say("  rel", rel(got, ref))
+    assert np.isfinite(got).all()
+    assert rel(got, ref) <= TOL_MV
+    for N in (2, 5):  # the narrow kernels stage the same way
+        X = np.repeat(x, N, axis=0)
+        assert rel(run_gemm(enc, t, M, K, w, X)[N - 1], ref) <= TOL_MV
+
+
+def test_gemv_nan_propagates(enc):
+    # a NaN activation makes every output NaN, as fp32 products do
+    t, M, K = Q4_K, 300, 1024
+    w = weights(t, M, K, 34)
+    x = acts(1, K, 35).copy()
+    x[0, 517] = np.nan
+    assert np.isnan(run_gemm(enc, t, M, K, w, x)[0]).all()
 
 
 def test_gemv_weight_offset(enc):
@@ -179,7 +211,7 @@ def test_gemv_weight_offset(enc):
     y = torch.empty(M, device="cuda")
     enc.gemv(ok.QuantTensor(dev(buf), K, M, t, off=pad), dev(x), y)
     ref = oracle.matvec(t, w, K, M, x[0]).astype(np.float64)
-    assert rel(host(y), ref) <= TOL
+    assert rel(host(y), ref) <= TOL_MV
 
 
 # ------------------------------------------------------------------ narrow N = 2..5
@@ -193,7 +225,8 @@ def test_narrow_matches_oracle_and_gemv(enc, t, N):
     X = acts(N, K, 14)
     ref = oracle.matmul(t, w, K, M, X).astype(np.float64)
     got = run_gemm(enc, t, M, K, w, X)
-    assert rel(got, ref) <= TOL
+    say("  rel", rel(got, ref))
+    assert rel(got, ref) <= TOL_MV
     for n in range(N):
         g1 = run_gemm(enc, t, M, K, w, X[n:n + 1])[0]
         assert rel(got[n], g1.astype(np.float64)) <= 1e-5
@@ -207,7 +240,7 @@ def test_iq2_xxs_mtp_verify_full_config(enc):
     ref = oracle.matmul(t, w, K, M, X).astype(np.float64)
     r = rel(run_gemm(enc, t, M, K, w, X), ref)
     say("iq2_xxs M=4 rel", r)
-    assert r <= TOL
+    assert r <= TOL_MV
 
 
 # ------------------------------------------- one workgroup per CU (wide)
@@ -243,7 +276,8 @@ def test_wide_matches_oracle_and_default(enc, enc_wide, t, M, K, N):
     X = acts(N, K, 22)
     ref = oracle.matmul(t, w, K, M, X).astype(np.float64)
     got = run_gemm(enc_wide, t, M, K, w, X)
-    assert rel(got, ref) <= TOL
+    say("  rel", rel(got, ref))
+    assert rel(got, ref) <= TOL_MV
     assert rel(got, run_gemm(enc, t, M, K, w, X).astype(np.float64)) <= 1e-5
 
 
@@ -325,7 +359,8 @@ def test_gemv_silu_matches_silu_mul_then_matvec(enc, t, M, K, seed):
     enc.gemv_silu(ok.QuantTensor(dev(w), K, M, t), gd, ud, y)
     got = host(y)
     say("gemv_silu", NAMES[t], M, K, rel(got, ref))
-    assert rel(got, ref) <= TOL
+    # (silu's device exp and reciprocal are within a few ulp of the C library's)
+    assert rel(got, ref) <= TOL_MV
     assert np.array_equal(host(gd), g)  # gate is not modified
     # the two-call form: silu_mul in place, then gemv
     enc.silu_mul(gd, ud, K)
@@ -359,7 +394,7 @@ def test_parallel_group_matches_single_calls(enc):
         got, one = host(y), host(y1)
         ref = oracle.matvec(t, weights(t, M, K, seed), K, M, acts(1, K, 70 + K)[0]).astype(np.float64)
         say("group", NAMES[t], M, K, rel(got, ref))
-        assert rel(got, ref) <= TOL
+        assert rel(got, ref) <= TOL_MV
         assert rel(got, one.astype(np.float64)) <= 1e-5
 
 
@@ -514,7 +549,7 @@ def test_gguf_upload_then_gemv(enc, tmp_path):
                 y = torch.full((M,), float("nan"), device="cuda")
                 enc.gemv(g.weight(name, base), dev(x), y)
                 ref = oracle.matvec(t, w, K, M, x[0]).astype(np.float64)
-                assert rel(host(y), ref) <= TOL
+                assert rel(host(y), ref) <= TOL_MV
         finally:
             enc.sync()
             enc._lib.okf_gguf_free_device(enc.h, ctypes.c_void_p(base))
