@@ -26,7 +26,7 @@ LIB_PATH = os.environ.get("OKF_LIB") or os.path.join(HERE, "libokf_quant.so")
 
 # Every symbol include/okf_quant.h declares.
 EXPORTS = (
-    "okf_ctx_create", "okf_ctx_destroy", "okf_ctx_stream", "okf_row_bytes",
+    "okf_ctx_create", "okf_ctx_destroy", "okf_ctx_stream", "okf_ctx_reserve", "okf_row_bytes",
     "okf_gemv", "okf_gemv_silu", "okf_silu_mul", "okf_gemm", "okf_gemm_tile", "okf_dequant_row",
     "okf_embed_batch", "okf_add_rmsnorm_batch", "okf_argmax_rows",
     "okf_parallel_begin",
@@ -83,6 +83,7 @@ def _lib():
             "okf_ctx_create": [ctypes.c_int, ctypes.POINTER(vp)],
             "okf_ctx_destroy": [vp],
             "okf_ctx_stream": [vp, ctypes.POINTER(vp)],
+            "okf_ctx_reserve": [vp, u64, u32, u32],
             "okf_row_bytes": [i32, u64, ctypes.POINTER(u64)],
             "okf_gemv": [vp, W, vp, vp],
             "okf_gemv_silu": [vp, W, vp, vp, vp],
@@ -260,6 +261,11 @@ class Enc:
         """out[row] = argmax of row (MetalEnc.argmaxRows)."""
         self._check(self._lib.okf_argmax_rows(self.h, _ptr(x), int(n), int(rows), _ptr(out)),
                     "okf_argmax_rows")
+
+    def reserve(self, gemm_nk: int, argmax_n: int, argmax_rows: int):
+        """okf_ctx_reserve: allocate the scratch now; later calls allocate nothing."""
+        self._check(self._lib.okf_ctx_reserve(self.h, int(gemm_nk), int(argmax_n), int(argmax_rows)),
+                    "okf_ctx_reserve")
 
     def sync(self):
         self._check(self._lib.okf_sync(self.h), "okf_sync")

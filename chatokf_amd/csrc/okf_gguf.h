@@ -174,7 +174,11 @@ inline int parse(File &f) {
         std::string key = c.str();
         Value v;
         if (!value(c, v) || !c.ok) return 8;
-        if (key == "general.alignment" && v.kind == Value::Int && v.i > 0) alignment = (uint64_t)v.i;
+        if (key == "general.alignment" && v.kind == Value::Int) {
+            // a power of two up to 1 MiB (GGUF requires a power of two)
+            if (v.i <= 0 || v.i > (1 << 20) || (v.i & (v.i - 1))) return 8;
+            alignment = (uint64_t)v.i;
+        }
         f.meta[key] = std::move(v);
     }
     for (uint64_t k = 0; k < nt; k++) {
@@ -185,8 +189,9 @@ inline int parse(File &f) {
         uint64_t n = 1;
         for (uint32_t d = 0; d < t.n_dims; d++) {
             t.dims[d] = c.get<uint64_t>();
-            n *= t.dims[d];
+            if (__builtin_mul_overflow(n, t.dims[d], &n)) return 8;
         }
+        if (n > (1ull << 60)) return 8;  // (so that row_bytes cannot wrap)
         t.type = (int32_t)c.get<uint32_t>();
         t.offset = c.get<uint64_t>();
         if (!c.ok) return 8;
@@ -196,9 +201,9 @@ inline int parse(File &f) {
         f.tensors.push_back(std::move(t));
     }
     f.data_start = (c.pos + alignment - 1) / alignment * alignment;
+    if (f.data_start > f.size) return 8;  // (also with no tensors)
     for (const Tensor &t : f.tensors)
-        if (f.data_start > f.size || t.offset > f.size - f.data_start ||
-            t.bytes > f.size - f.data_start - t.offset)
+        if (t.offset > f.size - f.data_start || t.bytes > f.size - f.data_start - t.offset)
             return 8;  // tensor past the end of the file
     return 0;
 }

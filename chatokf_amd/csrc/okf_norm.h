@@ -88,8 +88,10 @@ __global__ __launch_bounds__(NORM_THREADS) void add_rmsnorm_kernel(float *X,
 // value above -inf gives 0 (the kernel's start, bv = -inf, bi = 0).
 //
 // A 248320-wide vocabulary row is 1 MB, so one row is split over many
-// workgroups: stage 1 reduces ARGMAX_CHUNK values per workgroup to a
-// (value, index) pair, stage 2 reduces a row's pairs in chunk order.
+// workgroups, in one launch: each reduces ARGMAX_CHUNK values to a
+// (value, index) pair, and the last workgroup of a row to finish (counted
+// in cnt[row]) reduces the row's pairs in chunk order and sets cnt[row]
+// back to 0 for the next call.
 constexpr uint32_t ARGMAX_CHUNK = NORM_THREADS * 4;  // one float4 per thread: ~240 workgroups per row
 
 struct ArgPair {
@@ -115,12 +117,15 @@ __device__ __forceinline__ void block_argmax(float &bv, int32_t &bi, ArgPair *re
     for (int k = 1; k < NORM_THREADS / 64; k++) arg_take(bv, bi, red[k].v, red[k].i);
 }
 
-// grid (chunks, rows): pairs[row * chunks + chunk]
-__global__ __launch_bounds__(NORM_THREADS) void argmax_chunk_kernel(const float *__restrict__ X, uint32_t n,
-                                                                    ArgPair *__restrict__ pairs) {
+// grid (chunks, rows): pairs[row * chunks + chunk]; cnt[rows] are 0 on entry
+// and on exit.
+__global__ __launch_bounds__(NORM_THREADS) void argmax_kernel(const float *__restrict__ X, uint32_t n,
+                                                              ArgPair *__restrict__ pairs, uint32_t *cnt,
+                                                              int32_t *__restrict__ out) {
     __shared__ ArgPair red[NORM_THREADS / 64];
-    const uint32_t c = blockIdx.x, chunks = gridDim.x;
-    const float *x = X + (uint64_t)blockIdx.y * n;
+    __shared__ uint32_t last;
+    const uint32_t c = blockIdx.x, chunks = gridDim.x, row = blockIdx.y;
+    const float *x = X + (uint64_t)row * n;
     const uint32_t b = c * ARGMAX_CHUNK, e = min(b + ARGMAX_CHUNK, n);
     float bv = -__builtin_inff();
     int32_t bi = 0;
@@ -143,18 +148,29 @@ __global__ __launch_bounds__(NORM_THREADS) void argmax_chunk_kernel(const float 
             }
     }
     block_argmax(bv, bi, red);
-    if (threadIdx.x == 0) pairs[(uint64_t)blockIdx.y * chunks + c] = ArgPair{bv, bi};
-}
-
-__global__ __launch_bounds__(NORM_THREADS) void argmax_final_kernel(const ArgPair *__restrict__ pairs,
-                                                                    uint32_t chunks, int32_t *__restrict__ out) {
-    __shared__ ArgPair red[NORM_THREADS / 64];
-    const ArgPair *p = pairs + (uint64_t)blockIdx.x * chunks;
-    float bv = -__builtin_inff();
-    int32_t bi = 0;
-    for (uint32_t c = threadIdx.x; c < chunks; c += NORM_THREADS) arg_take(bv, bi, p[c].v, p[c].i);
+    ArgPair *p = pairs + (uint64_t)row * chunks;
+    if (threadIdx.x == 0) {
+        p[c] = ArgPair{bv, bi};
+        // release: the pair is visible device-wide before the count says so
+        const uint32_t prev = __hip_atomic_fetch_add(cnt + row, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        last = prev == chunks - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    // acquire for every thread of the last workgroup: the other pairs are visible
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    bv = -__builtin_inff();
+    bi = 0;
+    for (uint32_t k = threadIdx.x; k < chunks; k += NORM_THREADS) {
+        const ArgPair q = p[k];
+        arg_take(bv, bi, q.v, q.i);
+    }
+    __syncthreads();  // (red is reused)
     block_argmax(bv, bi, red);
-    if (threadIdx.x == 0) out[blockIdx.x] = bi;
+    if (threadIdx.x == 0) {
+        out[row] = bi;
+        __hip_atomic_store(cnt + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 }  // namespace okf

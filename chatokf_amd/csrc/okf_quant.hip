@@ -41,6 +41,7 @@ struct okf_gguf {
     okf_gguf_impl::File f;
 };
 
+
 struct okf_ctx {
     int device = -1;
     hipStream_t stream = nullptr;
@@ -71,8 +72,11 @@ struct okf_ctx {
     };
     bool grouping = false;
     std::vector<Pending> pending;
-    float *part = nullptr;   // split-tile partial sums of the Q4_K GEMM (grown on demand)
+    float *part = nullptr;   // split-tile partial sums of the Q4_K GEMM, argmax pairs
     size_t part_bytes = 0;
+    uint32_t *cnt = nullptr;  // argmax per-row counters (zero between calls)
+    size_t cnt_n = 0;
+    bool reserved = false;    // okf_ctx_reserve fixed the scratch sizes: no growth
 };
 
 namespace {
@@ -119,6 +123,15 @@ int check_weight(const okf_weight *w, uint64_t *row_bytes) {
 }
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+// Raises a kernel's dynamic LDS limit once per device (done: one bit per
+// device, shared by every context and thread; a repeated call is harmless).
+void set_lds_attr(const okf_ctx *c, const void *fn, std::atomic<uint64_t> &done) {
+    const uint64_t bit = 1ull << (c->device & 63);
+    if (done.load(std::memory_order_acquire) & bit) return;
+    (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)c->max_lds);
+    done.fetch_or(bit, std::memory_order_acq_rel);
+}
 
 int finish(okf_ctx *c) {
     hipError_t e = hipGetLastError();
@@ -187,11 +200,8 @@ void launch_gemv_s(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32
     constexpr int R = ((F == IQ2_XXS && NC >= 2) || (NC == 5 && F != Q8_0 && F != Q5_K && F != Q6_K && F != IQ4_XS && !grid_fmt(F))) ? 2 : 1,
                   D = DX ? DX : 2, WAVES = 4;
     const void *fn = (const void *)gemv_kernel<F, NC, R, D, S, SILU>;
-    static bool attr = false;  // one attribute call per instantiation
-    if (!attr) {
-        (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)c->max_lds);
-        attr = true;
-    }
+    static std::atomic<uint64_t> attr{0};  // devices that have the attribute set
+    set_lds_attr(c, fn, attr);
     const uint32_t rows_per_wg = (WAVES / S) * GV_SLOTS * R;
     GemvGroup g{};
     uint32_t total = 0;
@@ -225,11 +235,8 @@ void launch_wide_sp(okf_ctx *c, const GemvCall &call, uint64_t rb, uint32_t K, u
                       : F == Q2_0                ? (NC == 1 ? 6 : 2)
                                                  : (NC <= 2 ? 6 : NC == 3 ? 4 : 3);
     const void *fn = (const void *)gemv_wide_kernel<F, NC, D, SP>;
-    static bool attr = false;
-    if (!attr) {
-        (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)c->max_lds);
-        attr = true;
-    }
+    static std::atomic<uint64_t> attr{0};  // devices that have the attribute set
+    set_lds_attr(c, fn, attr);
     hipLaunchKernelGGL((gemv_wide_kernel<F, NC, D, SP>), dim3(G), dim3(GW_THREADS), lds, c->stream, call.W,
                        rb, K, call.M, call.X, call.Y, c->tab8, kmax);
 }
@@ -263,11 +270,8 @@ bool launch_iq2mm(okf_ctx *c, const GemvCall &call, uint64_t rb, uint32_t K) {
     auto go = [&](auto spc) {
         constexpr uint32_t SP = decltype(spc)::value;
         const void *fn = (const void *)gemv_wide_iq2mm_kernel<NC, D, SP>;
-        static bool attr = false;
-        if (!attr) {
-            (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)c->max_lds);
-            attr = true;
-        }
+        static std::atomic<uint64_t> attr{0};  // devices that have the attribute set
+        set_lds_attr(c, fn, attr);
         hipLaunchKernelGGL((gemv_wide_iq2mm_kernel<NC, D, SP>), dim3(G), dim3(GW_THREADS), lds, c->stream,
                            call.W, rb, K, call.M, call.X, call.Y, c->tab, kmax);
     };
@@ -348,8 +352,11 @@ void launch_gemv(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32_t
 
 // The context's scratch (split-tile partial sums, argmax pairs), grown to at
 // least `need` bytes; the stream is drained before an old buffer is freed.
+// After okf_ctx_reserve the sizes are fixed: a call that needs more is an
+// OKF_E_SHAPE, so nothing on the hot path allocates or synchronises.
 int grow_part(okf_ctx *c, size_t need) {
     if (need <= c->part_bytes) return OKF_OK;
+    if (c->reserved) return OKF_E_SHAPE;
     hipError_t e = hipStreamSynchronize(c->stream);
     if (e != hipSuccess) return hip_fail(c, e);
     if (c->part) (void)hipFree(c->part);
@@ -358,6 +365,39 @@ int grow_part(okf_ctx *c, size_t need) {
     e = hipMalloc((void **)&c->part, need);
     if (e != hipSuccess) return hip_fail(c, e);
     c->part_bytes = need;
+    return OKF_OK;
+}
+
+// argmax row counters, zeroed when allocated (the kernel leaves them zero)
+int grow_cnt(okf_ctx *c, size_t rows) {
+    if (rows <= c->cnt_n) return OKF_OK;
+    if (c->reserved) return OKF_E_SHAPE;
+    hipError_t e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) return hip_fail(c, e);
+    if (c->cnt) (void)hipFree(c->cnt);
+    c->cnt = nullptr;
+    c->cnt_n = 0;
+    e = hipMalloc((void **)&c->cnt, rows * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMemset(c->cnt, 0, rows * sizeof(uint32_t));
+    if (e != hipSuccess) return hip_fail(c, e);
+    c->cnt_n = rows;
+    return OKF_OK;
+}
+
+// the fp16 copy of a Q4_K GEMM's activations: N K values
+int grow_xh(okf_ctx *c, size_t need) {
+    if (need <= c->xh_bytes) return OKF_OK;
+    if (c->reserved) return OKF_E_SHAPE;
+    if (c->xh) {
+        hipError_t e = hipStreamSynchronize(c->stream);
+        if (e != hipSuccess) return hip_fail(c, e);
+        (void)hipFree(c->xh);
+        c->xh = nullptr;
+        c->xh_bytes = 0;
+    }
+    hipError_t e = hipMalloc((void **)&c->xh, need);
+    if (e != hipSuccess) return hip_fail(c, e);
+    c->xh_bytes = need;
     return OKF_OK;
 }
 
@@ -423,19 +463,8 @@ int launch_gemm(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t 
                 uint32_t N, float *Y) {
     if constexpr (F == Q4_K) {
         // fp16 activations, converted once per call into the context's buffer
-        const size_t need = (size_t)N * K * sizeof(_Float16);
-        if (need > c->xh_bytes) {
-            if (c->xh) {
-                hipError_t e = hipStreamSynchronize(c->stream);
-                if (e != hipSuccess) return hip_fail(c, e);
-                (void)hipFree(c->xh);
-                c->xh = nullptr;
-                c->xh_bytes = 0;
-            }
-            hipError_t e = hipMalloc((void **)&c->xh, need);
-            if (e != hipSuccess) return hip_fail(c, e);
-            c->xh_bytes = need;
-        }
+        const int st = grow_xh(c, (size_t)N * K * sizeof(_Float16));
+        if (st) return st;
         const uint64_t n4 = (uint64_t)N * K / 4;
         hipLaunchKernelGGL(x_to_f16_kernel, dim3((uint32_t)((n4 + 256 * XV - 1) / (256 * XV))), dim3(256), 0,
                            c->stream, X, c->xh, n4);
@@ -502,7 +531,13 @@ int run_gemm(okf_ctx *c, const okf_weight *w, const float *X, uint32_t N, float 
         const GemvCall call{W, X, Y, w->M, X2};
         if (c->grouping && N == 1) {
             // inside a parallel group: launched together at okf_parallel_end
-            c->pending.push_back({w->ggml_type, w->K, rb, call});
+            // (capacity for a whole launch group is reserved at
+            // okf_parallel_begin; past it a failed allocation is a status)
+            try {
+                c->pending.push_back({w->ggml_type, w->K, rb, call});
+            } catch (const std::bad_alloc &) {
+                return OKF_E_ARG;
+            }
             return OKF_OK;
         }
         OKF_DISPATCH(w->ggml_type, launch_gemv, c, &call, 1, rb, w->K, N);
@@ -639,6 +674,7 @@ int okf_ctx_destroy(okf_ctx *c) {
         (void)hipFree(c->tab8);
         if (c->xh) (void)hipFree(c->xh);
         if (c->part) (void)hipFree(c->part);
+        if (c->cnt) (void)hipFree(c->cnt);
         (void)hipStreamDestroy(c->stream);
     }
     delete c;
@@ -724,15 +760,37 @@ int okf_argmax_rows(okf_ctx *c, const float *x, uint32_t n, uint32_t rows, int32
     if (st) return st;
     const uint32_t chunks = (n + ARGMAX_CHUNK - 1) / ARGMAX_CHUNK;
     if ((st = grow_part(c, (size_t)chunks * rows * sizeof(ArgPair)))) return st;
-    ArgPair *pairs = (ArgPair *)c->part;
-    hipLaunchKernelGGL(argmax_chunk_kernel, dim3(chunks, rows), dim3(NORM_THREADS), 0, c->stream, x, n, pairs);
-    hipLaunchKernelGGL(argmax_final_kernel, dim3(rows), dim3(NORM_THREADS), 0, c->stream, pairs, chunks, out);
+    if ((st = grow_cnt(c, rows))) return st;
+    hipLaunchKernelGGL(argmax_kernel, dim3(chunks, rows), dim3(NORM_THREADS), 0, c->stream, x, n,
+                       (ArgPair *)c->part, c->cnt, out);
     return finish(c);
+}
+
+int okf_ctx_reserve(okf_ctx *c, uint64_t gemm_nk, uint32_t argmax_n, uint32_t argmax_rows) {
+    if (!c) return OKF_E_ARG;
+    if (c->device < 0) return OKF_E_NODEV;
+    if (argmax_rows > 65535 || argmax_n > 0x7FFFFFFFu) return OKF_E_SHAPE;
+    (void)hipSetDevice(c->device);
+    c->reserved = false;  // (grow up to the reservation)
+    int st = grow_xh(c, (size_t)gemm_nk * sizeof(_Float16));
+    const uint32_t chunks = (argmax_n + ARGMAX_CHUNK - 1) / ARGMAX_CHUNK;
+    if (!st) st = grow_part(c, std::max<size_t>((size_t)chunks * argmax_rows * sizeof(ArgPair), 1));
+    if (!st) st = grow_cnt(c, std::max<uint32_t>(argmax_rows, 1));
+    if (st) return st;
+    hipError_t e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) return hip_fail(c, e);
+    c->reserved = true;
+    return OKF_OK;
 }
 
 int okf_parallel_begin(okf_ctx *c) {
     if (!c) return OKF_E_ARG;
     if (c->grouping) return OKF_E_ARG;
+    try {
+        c->pending.reserve(4 * GV_GROUP);
+    } catch (const std::bad_alloc &) {
+        return OKF_E_ARG;
+    }
     c->grouping = true;
     return OKF_OK;
 }
@@ -744,7 +802,12 @@ int okf_parallel_end(okf_ctx *c) {
     if (c->pending.empty()) return OKF_OK;
     if (c->device < 0) return OKF_E_NODEV;
     (void)hipSetDevice(c->device);
-    return flush_group(c);
+    try {
+        return flush_group(c);
+    } catch (const std::bad_alloc &) {
+        c->pending.clear();
+        return OKF_E_ARG;
+    }
 }
 
 int okf_embed_batch(okf_ctx *c, const okf_weight *w, const int32_t *ids, uint32_t N, float *out) {
@@ -766,7 +829,13 @@ int okf_sync(okf_ctx *c) {
     (void)hipSetDevice(c->device);
     if (!c->pending.empty()) {
         c->grouping = false;
-        int st = flush_group(c);
+        int st;
+        try {
+            st = flush_group(c);
+        } catch (const std::bad_alloc &) {
+            c->pending.clear();
+            st = OKF_E_ARG;
+        }
         if (st) return st;
     }
     hipError_t e = hipStreamSynchronize(c->stream);
@@ -801,7 +870,12 @@ int okf_gguf_open(const char *path, okf_gguf **out) {
         return OKF_E_IO;
     }
     f.map = (const uint8_t *)m;
-    const int st2 = okf_gguf_impl::parse(f);
+    int st2;
+    try {  // (the directory's strings and maps allocate)
+        st2 = okf_gguf_impl::parse(f);
+    } catch (const std::bad_alloc &) {
+        st2 = OKF_E_FORMAT;
+    }
     if (st2) {
         delete g;
         return st2;

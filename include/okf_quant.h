@@ -93,6 +93,16 @@ int okf_ctx_destroy(okf_ctx *ctx);
 /* The hipStream_t the context launches on (for events / interop). */
 int okf_ctx_stream(okf_ctx *ctx, void **stream);
 
+/* Allocates the context's scratch up front, the counterpart of the
+ * reference's engine-owned buffers (MetalContext.swift:216-236; MetalEnc
+ * allocates nothing on the hot path): the fp16 activation copy of a Q4_K
+ * tile GEMM with N * K <= gemm_nk, and the pairs and row counters of
+ * okf_argmax_rows over up to argmax_rows rows of argmax_n values.  Afterwards
+ * no call allocates or synchronises; one that needs more scratch than
+ * reserved returns OKF_E_SHAPE.  Without it the scratch grows on demand
+ * (hipMalloc after draining the stream). */
+int okf_ctx_reserve(okf_ctx *ctx, uint64_t gemm_nk, uint32_t argmax_n, uint32_t argmax_rows);
+
 /* GGUF.rowByteCount (LLM/Base/GGUF.swift:160-188) for the types above: n a
  * whole number of blocks, or any n for f32 / f16 / bf16. */
 int okf_row_bytes(int32_t ggml_type, uint64_t n, uint64_t *out);
@@ -150,6 +160,7 @@ int okf_add_rmsnorm_batch(okf_ctx *ctx, float *x, const float *r, const float *w
  * row's n values, ties to the lower index; NaN never wins and a row with no
  * value above -inf gives 0.  x and out are device memory; rows <= 65535. */
 int okf_argmax_rows(okf_ctx *ctx, const float *x, uint32_t n, uint32_t rows, int32_t *out);
+
 
 /* MetalEnc.embedBatch (MetalEnc.swift:1096-1146; kernels embed_batch,
  * q4_k_embed_batch, iq_embed_batch, LLM/metal/Kernels.metal:1444-1482):

@@ -81,3 +81,34 @@ def test_upload_needs_a_device(tmp_path):
         g.upload(e)
     assert err.value.status == ok.OKF_E_NODEV
     e.close()
+
+
+def test_tensorless_file_ending_before_the_alignment(tmp_path):
+    # no tensors, and the directory ends inside the last alignment unit: the
+    # data region would start past the end of the file
+    path = tmp_path / "e.gguf"
+    gw.write(path, [("general.alignment", gw.U32, 256)], [])
+    raw = path.read_bytes()
+    path.write_bytes(raw[:len(raw) - 100])  # drop part of the trailing padding
+    with pytest.raises(ok.OkfError) as e:
+        ok.GGUF(str(path))
+    assert e.value.status == ok.OKF_E_FORMAT
+
+
+@pytest.mark.parametrize("dims", [[1 << 32, 1 << 32, 1 << 8], [1 << 62, 4], [(1 << 64) - 1, 2]])
+def test_overflowing_dims_are_rejected(tmp_path, dims):
+    # element counts whose product (or byte count) would wrap to a small value
+    path = tmp_path / "o.gguf"
+    gw.write(path, [], [("w", dims, 0, b"\0" * 64)])
+    with pytest.raises(ok.OkfError) as e:
+        ok.GGUF(str(path))
+    assert e.value.status == ok.OKF_E_FORMAT
+
+
+@pytest.mark.parametrize("alignment", [0, 48, 1 << 21])
+def test_bad_alignment_is_rejected(tmp_path, alignment):
+    path = tmp_path / "a.gguf"
+    gw.write(path, [("general.alignment", gw.U32, alignment)], [("w", [32, 1], 0, b"\0" * 128)])
+    with pytest.raises(ok.OkfError) as e:
+        ok.GGUF(str(path))
+    assert e.value.status == ok.OKF_E_FORMAT

@@ -331,6 +331,53 @@ def test_argmax_rows_matches_oracle(enc, n, rows, skew):
     assert np.array_equal(host(out), ref)
 
 
+def test_argmax_repeated_calls_reset_counters(enc):
+    # the single-launch argmax counts finished workgroups per row and the last
+    # one resets the count: back-to-back calls of different shapes stay right
+    rng = np.random.default_rng(77)
+    for n, rows in ((248320, 2), (5000, 5), (248320, 1), (1025, 3)):
+        x = rng.standard_normal((rows, n)).astype(np.float32)
+        out = torch.full((rows,), -7, dtype=torch.int32, device="cuda")
+        enc.argmax_rows(dev(x), n, rows, out)
+        assert np.array_equal(host(out), oracle.argmax_rows(x))
+
+
+# ------------------------------------------------------------ reserve
+def test_reserve_then_no_allocation():
+    # okf_ctx_reserve sizes the scratch once; the Q4_K tile GEMM and argmax
+    # then run without any device allocation, and a call beyond the
+    # reservation is refused rather than growing the scratch
+    e = ok.Enc(0)
+    try:
+        t, M, K, N = Q4_K, 512, 2048, 64
+        w, X = dev(weights(t, M, K, 41)), dev(acts(N, K, 42))
+        Y = torch.empty((N, M), device="cuda")
+        xa = torch.randn(3, 100000, device="cuda")
+        out = torch.empty(3, dtype=torch.int32, device="cuda")
+        X2 = dev(acts(2 * N, K, 43))
+        Y2 = torch.empty((2 * N, M), device="cuda")
+        e.reserve(N * K, 100000, 3)
+        torch.cuda.synchronize()
+        free0 = torch.cuda.mem_get_info()[0]
+        qt = ok.QuantTensor(w, K, M, t)
+        for _ in range(3):
+            e.gemm(qt, X, Y, N)
+            e.argmax_rows(xa, 100000, 3, out)
+            e.gemm(qt, X[:N // 2], Y[:N // 2], N // 2)
+        e.sync()
+        assert torch.cuda.mem_get_info()[0] == free0
+        with pytest.raises(ok.OkfError) as err:
+            e.gemm(qt, X2, Y2, 2 * N)
+        assert err.value.status == ok.OKF_E_SHAPE
+        with pytest.raises(ok.OkfError):
+            e.argmax_rows(xa, 100000, 4, out)  # (4 rows > 3 reserved)
+        ref = oracle.matmul(t, weights(t, M, K, 41), K, M, acts(N, K, 42)).astype(np.float64)
+        assert rel(host(Y), ref) <= TOL
+        assert np.array_equal(host(out), oracle.argmax_rows(host(xa)))
+    finally:
+        e.close()
+
+
 # ------------------------------------------------------------ SiLU-gated FFN
 def test_silu_mul_matches_oracle(enc):
     a = np.random.default_rng(4).standard_normal(6144).astype(np.float32) * 3
