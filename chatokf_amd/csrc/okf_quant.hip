@@ -41,6 +41,14 @@ struct okf_gguf {
     okf_gguf_impl::File f;
 };
 
+// The scratch of okf_argmax_rows_noalloc: OKF_NOALLOC_ARGMAX_PAIRS
+// (value, index) pairs, then OKF_NOALLOC_ARGMAX_ROWS row counters (zero
+// between calls: zero at load, and each call's last workgroup per row sets
+// its counter back).  Each GPU holds its own copy until the process ends;
+// host code uses the device address hipGetSymbolAddress gives, never the
+// name (which is a host-side stand-in).
+constexpr size_t SCRATCH_CNT_OFF = (size_t)OKF_NOALLOC_ARGMAX_PAIRS * 8;
+static __device__ __align__(256) uint8_t scratch[SCRATCH_CNT_OFF + (size_t)OKF_NOALLOC_ARGMAX_ROWS * 4];
 
 struct okf_ctx {
     int device = -1;
@@ -77,6 +85,7 @@ struct okf_ctx {
     uint32_t *cnt = nullptr;  // argmax per-row counters (zero between calls)
     size_t cnt_n = 0;
     bool reserved = false;    // okf_ctx_reserve fixed the scratch sizes: no growth
+    uint8_t *scratch = nullptr;  // this device's copy of the static scratch array
 };
 
 namespace {
@@ -642,6 +651,16 @@ int okf_ctx_create(int device, okf_ctx **out) {
             delete c;
             return OKF_E_HIP;
         }
+        if (e == hipSuccess) e = hipGetSymbolAddress((void **)&c->scratch, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) {
+            if (c->grid) (void)hipFree(c->grid);
+            if (c->grids) (void)hipFree(c->grids);
+            if (c->tab) (void)hipFree(c->tab);
+            if (c->tab8) (void)hipFree(c->tab8);
+            if (c->stream) (void)hipStreamDestroy(c->stream);
+            delete c;
+            return OKF_E_HIP;
+        }
         int v = 0;
         if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, device) ==
                 hipSuccess && v > 0)
@@ -763,6 +782,22 @@ int okf_argmax_rows(okf_ctx *c, const float *x, uint32_t n, uint32_t rows, int32
     if ((st = grow_cnt(c, rows))) return st;
     hipLaunchKernelGGL(argmax_kernel, dim3(chunks, rows), dim3(NORM_THREADS), 0, c->stream, x, n,
                        (ArgPair *)c->part, c->cnt, out);
+    return finish(c);
+}
+
+int okf_argmax_rows_noalloc(okf_ctx *c, const float *x, uint32_t n, uint32_t rows, int32_t *out) {
+    if (!x || !out) return OKF_E_ARG;
+    if (n == 0 || rows == 0 || n > 0x7FFFFFFFu || rows > OKF_NOALLOC_ARGMAX_ROWS) return OKF_E_SHAPE;
+    const uint32_t chunks = (n + ARGMAX_CHUNK - 1) / ARGMAX_CHUNK;
+    if ((uint64_t)chunks * rows > OKF_NOALLOC_ARGMAX_PAIRS) return OKF_E_SHAPE;
+    int st = begin(c);
+    if (st) return st;
+    // the device's scratch array through its device address (c->scratch,
+    // from hipGetSymbolAddress at okf_ctx_create): pairs, then row counters
+    ArgPair *pairs = (ArgPair *)c->scratch;
+    uint32_t *cnt = (uint32_t *)(c->scratch + SCRATCH_CNT_OFF);
+    hipLaunchKernelGGL(argmax_kernel, dim3(chunks, rows), dim3(NORM_THREADS), 0, c->stream, x, n, pairs, cnt,
+                       out);
     return finish(c);
 }
 

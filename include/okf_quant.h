@@ -161,6 +161,18 @@ int okf_add_rmsnorm_batch(okf_ctx *ctx, float *x, const float *r, const float *w
  * value above -inf gives 0.  x and out are device memory; rows <= 65535. */
 int okf_argmax_rows(okf_ctx *ctx, const float *x, uint32_t n, uint32_t rows, int32_t *out);
 
+/* okf_argmax_rows for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  It has no
+ * counterpart in the reference.  Its scratch is a fixed array in device
+ * memory, one per GPU, held until the process ends: at most
+ * OKF_NOALLOC_ARGMAX_PAIRS (value, index) pairs, i.e. rows * ceil(n / 1024)
+ * <= 131072, and rows <= OKF_NOALLOC_ARGMAX_ROWS; larger calls return
+ * OKF_E_SHAPE.  It calls no hipMalloc / hipFree and no allocating routine.
+ * Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+ * (two streams, two contexts) race. */
+#define OKF_NOALLOC_ARGMAX_PAIRS 131072
+#define OKF_NOALLOC_ARGMAX_ROWS 4096
+int okf_argmax_rows_noalloc(okf_ctx *ctx, const float *x, uint32_t n, uint32_t rows, int32_t *out);
 
 /* MetalEnc.embedBatch (MetalEnc.swift:1096-1146; kernels embed_batch,
  * q4_k_embed_batch, iq_embed_batch, LLM/metal/Kernels.metal:1444-1482):
