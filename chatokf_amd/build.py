@@ -4,14 +4,20 @@ Usage: ``python -m chatokf_amd.build`` (or ``__graft_entry__.build()``).
 The library is compiled here, on the CPU, and travels to the GPU box as a
 file; nothing is compiled at import time.
 """
+import glob
 import os
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
-SRC = os.path.join(HERE, "csrc", "okf_quant.hip")
+CSRC = os.path.join(HERE, "csrc")
+# the C ABI (okf_quant.hip) and one translation unit per group of formats
+# (okf_fmt_*.hip), compiled in parallel and linked into one library
+SRCS = [os.path.join(CSRC, "okf_quant.hip")] + sorted(glob.glob(os.path.join(CSRC, "okf_fmt_*.hip")))
 LIB = os.path.join(HERE, "libokf_quant.so")
+OBJ = os.path.join(HERE, "_build")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
@@ -19,7 +25,6 @@ FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     # no packed fp32 instructions anywhere in device code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     # keep private arrays in registers: LDS promotion of a prefetch buffer
@@ -31,17 +36,25 @@ FLAGS = [
 ]
 
 
-def build(verbose: bool = False) -> str:
-    cmd = [HIPCC, *FLAGS, SRC, "-o", LIB + ".tmp"]
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass warns that it does not know the packed-fp32 feature
     err = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l and l.strip())
     if r.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({r.returncode}):\n{err}")
+        raise RuntimeError(f"hipcc failed ({r.returncode}): {' '.join(cmd)}\n{err}")
     if verbose and err:
         print(err, file=sys.stderr)
+
+
+def build(verbose: bool = False) -> str:
+    os.makedirs(OBJ, exist_ok=True)
+    objs = [os.path.join(OBJ, os.path.basename(src)[:-4] + ".o") for src in SRCS]
+    jobs = min(len(SRCS), int(os.environ.get("MAX_JOBS", os.cpu_count() or 4)), 16)
+    with ThreadPoolExecutor(jobs) as ex:
+        list(ex.map(lambda so: _run([HIPCC, *FLAGS, "-c", so[0], "-o", so[1]], verbose), zip(SRCS, objs)))
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", LIB + ".tmp"], verbose)
     os.replace(LIB + ".tmp", LIB)
     return LIB
 

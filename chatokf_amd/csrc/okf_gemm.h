@@ -237,7 +237,7 @@ __device__ __forceinline__ void q4k_dq_mfma_a(const u32x4v hdr, const u32x4v qv,
 // X fp32 -> fp16 (round to nearest even), XV float4 per thread with all
 // loads issued before the first store; n4 float4 in all.
 constexpr uint32_t XV = 4;
-__global__ __launch_bounds__(256) void x_to_f16_kernel(const float *__restrict__ X,
+static __global__ __launch_bounds__(256) void x_to_f16_kernel(const float *__restrict__ X,
                                                        _Float16 *__restrict__ Xh, uint64_t n4) {
     typedef _Float16 half4 __attribute__((ext_vector_type(4)));
     const uint64_t i0 = (uint64_t)blockIdx.x * (256 * XV) + threadIdx.x;

@@ -769,7 +769,7 @@ __device__ __forceinline__ floatx4 silu_mul4(floatx4 g, floatx4 u) {
 
 // a[i] = silu(a[i]) * b[i], the FFN glue between gate/up and down
 // (silu_mul, LLM/metal/Kernels.metal:3280-3285)
-__global__ __launch_bounds__(256) void silu_mul_kernel(float *__restrict__ a,
+static __global__ __launch_bounds__(256) void silu_mul_kernel(float *__restrict__ a,
                                                        const float *__restrict__ b, uint32_t n) {
     const uint32_t i = blockIdx.x * 256 + threadIdx.x;
     if (i < n) a[i] = silu_mul1(a[i], b[i]);
