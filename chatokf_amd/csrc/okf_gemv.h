@@ -341,21 +341,31 @@ __device__ __forceinline__ void stage_slot(const float (&v)[NC][8], uint32_t u, 
 }
 
 // ------------------------------------------------------------- compute --
-// acc[r][n] += unit contribution.  xp = this lane's chunk 0 of column 0
-// (chunk c at xp + c ss, column n at + n cs); gp = the unit's group data
-// (group gi of column n at gp[n gcs + gi]).
+// acc[r][n] += unit contribution.  The unit's staged activations come
+// through an accessor xa: xa.chunk(n, c) is 16-byte chunk c of column n,
+// xa.gd(n, gi) the data of group gi of column n (XLds: from LDS, as staged
+// per workgroup).
+struct XLds {
+    const uint32_t *xp;  // this lane's chunk 0 of column 0
+    uint32_t ss, cs;     // uint32 stride between chunks, between columns
+    const floatx4 *gp;   // the unit's group data of column 0
+    uint32_t gcs;        // float4 stride between columns
+    __device__ __forceinline__ u32x4 chunk(int n, uint32_t ch) const {
+        return *(const u32x4 *)(xp + n * cs + ch * ss);
+    }
+    __device__ __forceinline__ floatx4 gd(int n, uint32_t gi) const { return gp[n * gcs + gi]; }
+};
 //
 // dot_half: for group gi and chunk half h (plane dwords 4h .. 4h + 3), the
 // weight dwords wf(r, k) (int8 bytes in the staged order of plane dword
 // 4h + k) dotted with each digit plane into s[digit][r][n].
-template <int NC, int R, class WF>
-__device__ __forceinline__ void dot_half(const uint32_t *xp, uint32_t ss, uint32_t cs, uint32_t gi, uint32_t h,
-                                         WF wf, int (&s)[3][R][NC]) {
+template <int NC, int R, class XA, class WF>
+__device__ __forceinline__ void dot_half(const XA &xa, uint32_t gi, uint32_t h, WF wf, int (&s)[3][R][NC]) {
     u32x4 x[3][NC];
 #pragma unroll
     for (int p = 0; p < 3; p++)
 #pragma unroll
-        for (int n = 0; n < NC; n++) x[p][n] = *(const u32x4 *)(xp + n * cs + chunk_of(gi, p, h) * ss);
+        for (int n = 0; n < NC; n++) x[p][n] = xa.chunk(n, chunk_of(gi, p, h));
 #pragma unroll
     for (int r = 0; r < R; r++)
 #pragma unroll
@@ -394,8 +404,8 @@ struct Compute {
     // memory, tab) and multiplied in fp32 into the staged activations
     // rebuilt as integers (exact in fp32), scaled once per group.
     static_assert(grid_fmt(F), "no matvec compute for this format");
-    __device__ __forceinline__ static void run(const Unit<F, R> &w, const uint32_t *xp, uint32_t ss, uint32_t cs,
-                                               const floatx4 *gp, uint32_t gcs, uint32_t u, float (&acc)[R][NC],
+    template <class XA>
+    __device__ __forceinline__ static void run(const Unit<F, R> &w, const XA &xa, uint32_t u, float (&acc)[R][NC],
                                                const u32x4 *tab) {
 #pragma unroll
         for (int r = 0; r < R; r++) {
@@ -406,9 +416,9 @@ struct Compute {
                 float a = 0;
 #pragma unroll
                 for (int h = 0; h < 2; h++) {
-                    const u32x4 p0 = *(const u32x4 *)(xp + n * cs + chunk_of(0, 0, h) * ss);
-                    const u32x4 p1 = *(const u32x4 *)(xp + n * cs + chunk_of(0, 1, h) * ss);
-                    const u32x4 p2 = *(const u32x4 *)(xp + n * cs + chunk_of(0, 2, h) * ss);
+                    const u32x4 p0 = xa.chunk(n, chunk_of(0, 0, h));
+                    const u32x4 p1 = xa.chunk(n, chunk_of(0, 1, h));
+                    const u32x4 p2 = xa.chunk(n, chunk_of(0, 2, h));
 #pragma unroll
                     for (int k = 0; k < 4; k++)
 #pragma unroll
@@ -419,7 +429,7 @@ struct Compute {
                             a = fmaf(wv[16 * h + 4 * k + b], (float)X, a);
                         }
                 }
-                acc[r][n] += a * gp[n * gcs][3];
+                acc[r][n] += a * xa.gd(n, 0)[3];
             }
         }
     }
@@ -429,8 +439,8 @@ template <int NC, int R, int TS>
 struct Compute<Q4_K, NC, R, TS> {
     // Code dword i (bytes 4i..4i+3 of the unit's 32): low nibbles are weights
     // 4i.. of sub-block 2g (group 0), high nibbles of sub-block 2g + 1.
-    __device__ __forceinline__ static void run(const Unit<Q4_K, R> &w, const uint32_t *xp, uint32_t ss, uint32_t cs,
-                                               const floatx4 *gp, uint32_t gcs, uint32_t u,
+    template <class XA>
+    __device__ __forceinline__ static void run(const Unit<Q4_K, R> &w, const XA &xa, uint32_t u,
                                                float (&acc)[R][NC], const u32x4 *) {
         const uint32_t g = u & 3;
         int s0[3][R][NC], s1[3][R][NC];
@@ -439,8 +449,8 @@ struct Compute<Q4_K, NC, R, TS> {
         auto code = [&](int r, int i) { return i < 4 ? w.q0[r][i] : w.q1[r][i - 4]; };
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-            dot_half<NC, R>(xp, ss, cs, 0, h, [&](int r, int k) { return code(r, 4 * h + k) & 0x0F0F0F0Fu; }, s0);
-            dot_half<NC, R>(xp, ss, cs, 1, h,
+            dot_half<NC, R>(xa, 0, h, [&](int r, int k) { return code(r, 4 * h + k) & 0x0F0F0F0Fu; }, s0);
+            dot_half<NC, R>(xa, 1, h,
                             [&](int r, int k) { return (code(r, 4 * h + k) >> 4) & 0x0F0F0F0Fu; }, s1);
         }
 #pragma unroll
@@ -453,7 +463,7 @@ struct Compute<Q4_K, NC, R, TS> {
             const float b0 = dmin * (float)mn0, b1 = dmin * (float)mn1;
 #pragma unroll
             for (int n = 0; n < NC; n++) {
-                const floatx4 g0 = gp[n * gcs], g1 = gp[n * gcs + 1];
+                const floatx4 g0 = xa.gd(n, 0), g1 = xa.gd(n, 1);
                 acc[r][n] += g0[3] * (a0 * comb(s0, r, n) - b0 * g0[2]) + g1[3] * (a1 * comb(s1, r, n) - b1 * g1[2]);
             }
         }
@@ -468,8 +478,8 @@ struct Compute<IQ2_XXS, NC, R, TS> {
     // (g ^ M) + (M & 1) = +-g, no carry between bytes (g <= 43).  Entry e at
     // tab[e * TS] (TS = 16: the replicated, conflict-free layout of
     // gemv_wide_kernel, tab offset by the lane's copy).
-    __device__ __forceinline__ static void run(const Unit<IQ2_XXS, R> &w, const uint32_t *xp, uint32_t ss,
-                                               uint32_t cs, const floatx4 *gp, uint32_t gcs, uint32_t,
+    template <class XA>
+    __device__ __forceinline__ static void run(const Unit<IQ2_XXS, R> &w, const XA &xa, uint32_t,
                                                float (&acc)[R][NC], const u32x4 *tab) {
 #pragma unroll
         for (int sb = 0; sb < 2; sb++) {  // the unit's two sub-blocks = groups
@@ -490,14 +500,14 @@ struct Compute<IQ2_XXS, NC, R, TS> {
                         wv[r][2 * e + 1] = (gv.y ^ sg[1]) + sg[3];
                     }
                 }
-                dot_half<NC, R>(xp, ss, cs, sb, h, [&](int r, int k) { return wv[r][k]; }, s);
+                dot_half<NC, R>(xa, sb, h, [&](int r, int k) { return wv[r][k]; }, s);
             }
 #pragma unroll
             for (int r = 0; r < R; r++) {
                 const uint32_t a1 = w.a[r][2 * sb + 1];
                 const float db = h2f(w.d[r]) * (0.5f + (float)(a1 >> 28)) * 0.25f;
 #pragma unroll
-                for (int n = 0; n < NC; n++) acc[r][n] += db * (comb(s, r, n) * gp[n * gcs + sb][3]);
+                for (int n = 0; n < NC; n++) acc[r][n] += db * (comb(s, r, n) * xa.gd(n, sb)[3]);
             }
         }
     }
@@ -506,18 +516,18 @@ struct Compute<IQ2_XXS, NC, R, TS> {
 template <int NC, int R, int TS>
 struct Compute<Q8_0, NC, R, TS> {
     // the 32 int8 codes are the weight bytes as they are
-    __device__ __forceinline__ static void run(const Unit<Q8_0, R> &w, const uint32_t *xp, uint32_t ss, uint32_t cs,
-                                               const floatx4 *gp, uint32_t gcs, uint32_t,
+    template <class XA>
+    __device__ __forceinline__ static void run(const Unit<Q8_0, R> &w, const XA &xa, uint32_t,
                                                float (&acc)[R][NC], const u32x4 *) {
         int s[3][R][NC];
         zero3(s);
-        dot_half<NC, R>(xp, ss, cs, 0, 0, [&](int r, int k) { return w.q0[r][k]; }, s);
-        dot_half<NC, R>(xp, ss, cs, 0, 1, [&](int r, int k) { return w.q1[r][k]; }, s);
+        dot_half<NC, R>(xa, 0, 0, [&](int r, int k) { return w.q0[r][k]; }, s);
+        dot_half<NC, R>(xa, 0, 1, [&](int r, int k) { return w.q1[r][k]; }, s);
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const float d = h2f(w.d[r]);
 #pragma unroll
-            for (int n = 0; n < NC; n++) acc[r][n] += d * (comb(s, r, n) * gp[n * gcs][3]);
+            for (int n = 0; n < NC; n++) acc[r][n] += d * (comb(s, r, n) * xa.gd(n, 0)[3]);
         }
     }
 };
@@ -526,19 +536,19 @@ template <int NC, int R, int TS>
 struct Compute<Q4_0, NC, R, TS> {
     // Code dword i: low nibbles are weights 4i.., high nibbles 16 + 4i..;
     // sum((q - 8) X) = sum(q X) - 8 sum(X).
-    __device__ __forceinline__ static void run(const Unit<Q4_0, R> &w, const uint32_t *xp, uint32_t ss, uint32_t cs,
-                                               const floatx4 *gp, uint32_t gcs, uint32_t,
+    template <class XA>
+    __device__ __forceinline__ static void run(const Unit<Q4_0, R> &w, const XA &xa, uint32_t,
                                                float (&acc)[R][NC], const u32x4 *) {
         int s[3][R][NC];
         zero3(s);
-        dot_half<NC, R>(xp, ss, cs, 0, 0, [&](int r, int k) { return w.q[r][k] & 0x0F0F0F0Fu; }, s);
-        dot_half<NC, R>(xp, ss, cs, 0, 1, [&](int r, int k) { return (w.q[r][k] >> 4) & 0x0F0F0F0Fu; }, s);
+        dot_half<NC, R>(xa, 0, 0, [&](int r, int k) { return w.q[r][k] & 0x0F0F0F0Fu; }, s);
+        dot_half<NC, R>(xa, 0, 1, [&](int r, int k) { return (w.q[r][k] >> 4) & 0x0F0F0F0Fu; }, s);
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const float d = h2f(w.d[r]);
 #pragma unroll
             for (int n = 0; n < NC; n++) {
-                const floatx4 g = gp[n * gcs];
+                const floatx4 g = xa.gd(n, 0);
                 acc[r][n] += d * ((comb(s, r, n) - 8.0f * g[2]) * g[3]);
             }
         }
@@ -565,20 +575,20 @@ struct IQ4Levels {
 template <int NC, int R, int TS>
 struct Compute<IQ4_NL, NC, R, TS> {
     // as Q4_0, each nibble looked up as its signed level
-    __device__ __forceinline__ static void run(const Unit<IQ4_NL, R> &w, const uint32_t *xp, uint32_t ss, uint32_t cs,
-                                               const floatx4 *gp, uint32_t gcs, uint32_t,
+    template <class XA>
+    __device__ __forceinline__ static void run(const Unit<IQ4_NL, R> &w, const XA &xa, uint32_t,
                                                float (&acc)[R][NC], const u32x4 *) {
         int s[3][R][NC];
         zero3(s);
-        dot_half<NC, R>(xp, ss, cs, 0, 0,
+        dot_half<NC, R>(xa, 0, 0,
                         [&](int r, int k) { return IQ4Levels::levels(w.q[r][k] & 0x0F0F0F0Fu); }, s);
-        dot_half<NC, R>(xp, ss, cs, 0, 1,
+        dot_half<NC, R>(xa, 0, 1,
                         [&](int r, int k) { return IQ4Levels::levels((w.q[r][k] >> 4) & 0x0F0F0F0Fu); }, s);
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const float d = h2f(w.d[r]);
 #pragma unroll
-            for (int n = 0; n < NC; n++) acc[r][n] += d * (comb(s, r, n) * gp[n * gcs][3]);
+            for (int n = 0; n < NC; n++) acc[r][n] += d * (comb(s, r, n) * xa.gd(n, 0)[3]);
         }
     }
 };
@@ -588,15 +598,15 @@ struct Compute<Q2_0, NC, R, TS> {
     // code dword j, field k: bytes (v >> 2k) & 0x03030303 = plane dword
     // 4j + k of the staged order (group j >> 1, chunk half j & 1);
     // sum((code - 1) X) = sum(code X) - sum(X) per group.
-    __device__ __forceinline__ static void run(const Unit<Q2_0, R> &w, const uint32_t *xp, uint32_t ss, uint32_t cs,
-                                               const floatx4 *gp, uint32_t gcs, uint32_t,
+    template <class XA>
+    __device__ __forceinline__ static void run(const Unit<Q2_0, R> &w, const XA &xa, uint32_t,
                                                float (&acc)[R][NC], const u32x4 *) {
         int s0[3][R][NC], s1[3][R][NC];
         zero3(s0);
         zero3(s1);
 #pragma unroll
         for (int j = 0; j < 4; j++)
-            dot_half<NC, R>(xp, ss, cs, j >> 1, j & 1,
+            dot_half<NC, R>(xa, j >> 1, j & 1,
                             [&](int r, int k) { return (w.q[r][j] >> (2 * k)) & 0x03030303u; },
                             j < 2 ? s0 : s1);
 #pragma unroll
@@ -604,7 +614,7 @@ struct Compute<Q2_0, NC, R, TS> {
             const float d = h2f(w.d[r]);
 #pragma unroll
             for (int n = 0; n < NC; n++) {
-                const floatx4 g0 = gp[n * gcs], g1 = gp[n * gcs + 1];
+                const floatx4 g0 = xa.gd(n, 0), g1 = xa.gd(n, 1);
                 acc[r][n] += d * ((comb(s0, r, n) - g0[2]) * g0[3] + (comb(s1, r, n) - g1[2]) * g1[3]);
             }
         }
@@ -615,8 +625,8 @@ template <int NC, int R, int TS>
 struct Compute<Q5_K, NC, R, TS> {
     // As Q4_K, with the fifth bit of weight l from qh byte l: bit 2g for the
     // low nibbles (sub-block 2g), bit 2g + 1 for the high ones.
-    __device__ __forceinline__ static void run(const Unit<Q5_K, R> &w, const uint32_t *xp, uint32_t ss, uint32_t cs,
-                                               const floatx4 *gp, uint32_t gcs, uint32_t u,
+    template <class XA>
+    __device__ __forceinline__ static void run(const Unit<Q5_K, R> &w, const XA &xa, uint32_t u,
                                                float (&acc)[R][NC], const u32x4 *) {
         const uint32_t g = u & 3;
         int s0[3][R][NC], s1[3][R][NC];
@@ -626,11 +636,11 @@ struct Compute<Q5_K, NC, R, TS> {
         auto high = [&](int r, int i) { return (i < 4 ? w.h0[r][i] : w.h1[r][i - 4]) >> (2 * g); };
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-            dot_half<NC, R>(xp, ss, cs, 0, h, [&](int r, int k) {
+            dot_half<NC, R>(xa, 0, h, [&](int r, int k) {
                 const int i = 4 * h + k;
                 return (code(r, i) & 0x0F0F0F0Fu) | ((high(r, i) & 0x01010101u) << 4);
             }, s0);
-            dot_half<NC, R>(xp, ss, cs, 1, h, [&](int r, int k) {
+            dot_half<NC, R>(xa, 1, h, [&](int r, int k) {
                 const int i = 4 * h + k;
                 return ((code(r, i) >> 4) & 0x0F0F0F0Fu) | ((high(r, i) & 0x02020202u) << 3);
             }, s1);
@@ -645,7 +655,7 @@ struct Compute<Q5_K, NC, R, TS> {
             const float b0 = dmin * (float)mn0, b1 = dmin * (float)mn1;
 #pragma unroll
             for (int n = 0; n < NC; n++) {
-                const floatx4 g0 = gp[n * gcs], g1 = gp[n * gcs + 1];
+                const floatx4 g0 = xa.gd(n, 0), g1 = xa.gd(n, 1);
                 acc[r][n] += g0[3] * (a0 * comb(s0, r, n) - b0 * g0[2]) + g1[3] * (a1 * comb(s1, r, n) - b1 * g1[2]);
             }
         }
@@ -661,8 +671,8 @@ struct Compute<Q6_K, NC, R, TS> {
     // with bits 2 grp, 2 grp + 1 of qh byte l on top, a 6-bit q;
     // sum((q - 32) X) = sum(q X) - 32 sum(X) over the 16, scaled by
     // d * scales[8 n + is + 2 grp].  The unit reads exactly its 48 code bytes.
-    __device__ __forceinline__ static void run(const Unit<Q6_K, R> &w, const uint32_t *xp, uint32_t ss, uint32_t cs,
-                                               const floatx4 *gp, uint32_t gcs, uint32_t u, float (&acc)[R][NC],
+    template <class XA>
+    __device__ __forceinline__ static void run(const Unit<Q6_K, R> &w, const XA &xa, uint32_t u, float (&acc)[R][NC],
                                                const u32x4 *) {
         const uint32_t is = u & 1;
         float sg[4][R][NC];
@@ -670,7 +680,7 @@ struct Compute<Q6_K, NC, R, TS> {
         for (int grp = 0; grp < 4; grp++) {
             int s[3][R][NC];
             zero3(s);
-            dot_half<NC, R>(xp, ss, cs, grp >> 1, grp & 1, [&](int r, int k) {
+            dot_half<NC, R>(xa, grp >> 1, grp & 1, [&](int r, int k) {
                 const uint32_t v = (grp & 1) ? w.qb[r][k] : w.qa[r][k];
                 return ((v >> (4 * (grp >> 1))) & 0x0F0F0F0Fu) | (((w.qh[r][k] >> (2 * grp)) & 0x03030303u) << 4);
             }, s);
@@ -678,7 +688,7 @@ struct Compute<Q6_K, NC, R, TS> {
             for (int r = 0; r < R; r++)
 #pragma unroll
                 for (int n = 0; n < NC; n++) {
-                    const floatx4 gd = gp[n * gcs + (grp >> 1)];
+                    const floatx4 gd = xa.gd(n, grp >> 1);
                     sg[grp][r][n] = comb(s, r, n) - 32.0f * ((grp & 1) ? gd[1] : gd[0]);
                 }
         }
@@ -692,8 +702,8 @@ struct Compute<Q6_K, NC, R, TS> {
             for (int gq = 0; gq < 4; gq++) dg[gq] = d * (float)(int8_t)((s4 >> (8 * gq)) & 0xFF);
 #pragma unroll
             for (int n = 0; n < NC; n++)
-                acc[r][n] += gp[n * gcs][3] * (dg[0] * sg[0][r][n] + dg[1] * sg[1][r][n]) +
-                             gp[n * gcs + 1][3] * (dg[2] * sg[2][r][n] + dg[3] * sg[3][r][n]);
+                acc[r][n] += xa.gd(n, 0)[3] * (dg[0] * sg[0][r][n] + dg[1] * sg[1][r][n]) +
+                             xa.gd(n, 1)[3] * (dg[2] * sg[2][r][n] + dg[3] * sg[3][r][n]);
         }
     }
 };
@@ -703,20 +713,20 @@ struct Compute<IQ4_XS, NC, R, TS> {
     // Two IQ4_NL-shaped sub-blocks (16 code bytes each, one group each) with
     // their own 6-bit scales: dl = d (ls - 32), ls = nibble of scales_l byte
     // g | 2 bits of scales_h << 4.
-    __device__ __forceinline__ static void run(const Unit<IQ4_XS, R> &w, const uint32_t *xp, uint32_t ss, uint32_t cs,
-                                               const floatx4 *gp, uint32_t gcs, uint32_t u,
+    template <class XA>
+    __device__ __forceinline__ static void run(const Unit<IQ4_XS, R> &w, const XA &xa, uint32_t u,
                                                float (&acc)[R][NC], const u32x4 *) {
         const uint32_t g = u & 3;
         int s0[3][R][NC], s1[3][R][NC];
         zero3(s0);
         zero3(s1);
-        dot_half<NC, R>(xp, ss, cs, 0, 0,
+        dot_half<NC, R>(xa, 0, 0,
                         [&](int r, int k) { return IQ4Levels::levels(w.q0[r][k] & 0x0F0F0F0Fu); }, s0);
-        dot_half<NC, R>(xp, ss, cs, 0, 1,
+        dot_half<NC, R>(xa, 0, 1,
                         [&](int r, int k) { return IQ4Levels::levels((w.q0[r][k] >> 4) & 0x0F0F0F0Fu); }, s0);
-        dot_half<NC, R>(xp, ss, cs, 1, 0,
+        dot_half<NC, R>(xa, 1, 0,
                         [&](int r, int k) { return IQ4Levels::levels(w.q1[r][k] & 0x0F0F0F0Fu); }, s1);
-        dot_half<NC, R>(xp, ss, cs, 1, 1,
+        dot_half<NC, R>(xa, 1, 1,
                         [&](int r, int k) { return IQ4Levels::levels((w.q1[r][k] >> 4) & 0x0F0F0F0Fu); }, s1);
 #pragma unroll
         for (int r = 0; r < R; r++) {
@@ -726,7 +736,7 @@ struct Compute<IQ4_XS, NC, R, TS> {
             const float dl1 = d * (float)((int)((sl >> 4) | (((sh >> (4 * g + 2)) & 3) << 4)) - 32);
 #pragma unroll
             for (int n = 0; n < NC; n++)
-                acc[r][n] += dl0 * (comb(s0, r, n) * gp[n * gcs][3]) + dl1 * (comb(s1, r, n) * gp[n * gcs + 1][3]);
+                acc[r][n] += dl0 * (comb(s0, r, n) * xa.gd(n, 0)[3]) + dl1 * (comb(s1, r, n) * xa.gd(n, 1)[3]);
         }
     }
 };
@@ -896,8 +906,8 @@ __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ W, uint64_
             for (int j = 0; j < D; j++) {
                 const uint32_t u = i + L * (part + S * (t + j));
                 if (u < cn)
-                    Compute<F, NC, R>::run(buf[j], xs + xs_index<F, L>(u, 0), 4 * L, cs,
-                                           gdp + u * UG, gcs, c0 + u, acc, grid_fmt(F) ? tab_g : tab);
+                    Compute<F, NC, R>::run(buf[j], XLds{xs + xs_index<F, L>(u, 0), 4 * L, cs, gdp + u * UG, gcs},
+                                           c0 + u, acc, grid_fmt(F) ? tab_g : tab);
                 load_unit<F, R>(rows, c0 + min(u + L * S * D, last), buf[j]);
             }
         }
@@ -905,8 +915,8 @@ __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ W, uint64_
         for (int j = 0; j < D; j++) {
             const uint32_t u = i + L * (part + S * (t + j));
             if (u < cn)
-                Compute<F, NC, R>::run(buf[j], xs + xs_index<F, L>(u, 0), 4 * L, cs,
-                                       gdp + u * UG, gcs, c0 + u, acc, grid_fmt(F) ? tab_g : tab);
+                Compute<F, NC, R>::run(buf[j], XLds{xs + xs_index<F, L>(u, 0), 4 * L, cs, gdp + u * UG, gcs},
+                                       c0 + u, acc, grid_fmt(F) ? tab_g : tab);
         }
     }
     // reduce: over the slot's lanes, then (S > 1) over the parts in LDS

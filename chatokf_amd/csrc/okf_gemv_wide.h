@@ -133,7 +133,7 @@ __global__ __launch_bounds__(GW_THREADS) void gemv_wide_kernel(const uint8_t *__
                 const uint32_t u = su * L + i;
                 if (u < units)
                     Compute<F, NC, 1, (F == IQ2_XXS ? L : 1)>::run(
-                        buf[j], xs + xs_index<F, L>(u, 0), 4 * L, cs, gdp + u * UG, gcs, u, acc,
+                        buf[j], XLds{xs + xs_index<F, L>(u, 0), 4 * L, cs, gdp + u * UG, gcs}, u, acc,
                         tab + i);
                 if (++su == P && t + j + 1 < s1) {  // next step starts a row
                     flush();

@@ -117,10 +117,18 @@ inline bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 // Raises a kernel's dynamic LDS limit once per device (done: one bit per
 // device, shared by every context and thread; a repeated call is harmless).
+// The limit is the workgroup's LDS less the kernel's static LDS; a failure
+// (which leaves the launch at the default limit) is cleared so that it is
+// not reported as the launch's error.
 inline void set_lds_attr(const okf_ctx *c, const void *fn, std::atomic<uint64_t> &done) {
     const uint64_t bit = 1ull << (c->device & 63);
     if (done.load(std::memory_order_acquire) & bit) return;
-    (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)c->max_lds);
+    hipFuncAttributes fa{};
+    size_t stat = 0;
+    if (hipFuncGetAttributes(&fa, fn) == hipSuccess) stat = fa.sharedSizeBytes;
+    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(c->max_lds - stat)) !=
+        hipSuccess)
+        (void)hipGetLastError();
     done.fetch_or(bit, std::memory_order_acq_rel);
 }
 

@@ -118,6 +118,16 @@ int okf_gemv(okf_ctx *ctx, const okf_weight *w, const float *x, float *y);
  * Unlike the reference's in-place siluMul, gate is left unchanged. */
 int okf_gemv_silu(okf_ctx *ctx, const okf_weight *w, const float *gate, const float *up, float *y);
 
+/* The FFN block of the reference's engines (LLM/Qwen/QwenMetalEngine.swift:
+ * 918-929: MetalEnc.parallel { gemv(gate); gemv(up) }, siluMul, gemv(down)):
+ * g = W_gate x, u = W_up x, y = W_down (silu(g) * u), as two launches (gate
+ * and up in one grid; the SiLU folded into the down projection's staging).
+ * g and u (gate->M values each) are written as the gate and up outputs;
+ * unlike the reference's in-place siluMul, g is left as the gate output.
+ * down->K must equal gate->M; x, g, u 16-byte aligned. */
+int okf_ffn(okf_ctx *ctx, const okf_weight *gate, const okf_weight *up, const okf_weight *down, const float *x,
+            float *g, float *u, float *y);
+
 /* MetalEnc.siluMul (MetalEnc.swift:921): a[i] = silu(a[i]) * b[i], n values. */
 int okf_silu_mul(okf_ctx *ctx, float *a, const float *b, uint32_t n);
 

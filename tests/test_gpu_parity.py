@@ -416,6 +416,35 @@ def test_gemv_silu_matches_silu_mul_then_matvec(enc, t, M, K, seed):
     assert rel(got, host(y2).astype(np.float64)) <= 1e-5
 
 
+# ------------------------------------------------------------ FFN block
+# okf_ffn: gate and up on x (one grid), then down on silu(gate) * up
+# (QwenMetalEngine.swift:918-929); against the oracle's three matvecs.
+FFN = [(Q2_0, Q2_0, Q2_0, 6144, 2048, 1002), (Q4_K, Q4_K, Q4_K, 768, 512, 31), (IQ2_XXS, IQ2_XXS, IQ2_XXS, 512, 1280, 32),
+       (Q8_0, Q8_0, Q8_0, 320, 2080, 33), (Q2_0, Q2_0, Q2_0, 256, 1024, 34),
+       (Q4_K, Q4_K, Q8_0, 512, 768, 35)]  # (formats differ)
+
+
+@pytest.mark.parametrize("tg,tu,td,H,D,seed", FFN)
+def test_ffn_matches_oracle(enc, tg, tu, td, H, D, seed):
+    say("ffn", NAMES[tg], NAMES[td], H, D)
+    wg, wu, wd = weights(tg, H, D, seed), weights(tu, H, D, seed + 1), weights(td, D, H, seed + 2)
+    qg, qu, qd = (ok.QuantTensor(dev(w), k, m, t) for w, k, m, t in ((wg, D, H, tg), (wu, D, H, tu), (wd, H, D, td)))
+    for rep in range(2):
+        x = acts(1, D, seed + 10 + rep)[0]
+        g, u = (torch.full((H,), float("nan"), device="cuda") for _ in range(2))
+        y = torch.full((D,), float("nan"), device="cuda")
+        enc.ffn(qg, qu, qd, dev(x), g, u, y)
+        enc.sync()
+        rg = oracle.matvec(tg, wg, D, H, x)
+        ru = oracle.matvec(tu, wu, D, H, x)
+        ry = oracle.matvec(td, wd, H, D, oracle.silu_mul(rg, ru)).astype(np.float64)
+        assert rel(host(g), rg.astype(np.float64)) <= TOL_MV
+        assert rel(host(u), ru.astype(np.float64)) <= TOL_MV
+        r = rel(host(y), ry)
+        say("  rel", r)
+        assert r <= TOL_MV
+
+
 # ------------------------------------------------------------ parallel group
 def test_parallel_group_matches_single_calls(enc):
     # MetalEnc.parallel { gate; up } (QwenMetalEngine.swift:918-923) plus more
