@@ -124,6 +124,50 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
+    rd_buf = torch.empty(ROTATE_BYTES + (64 << 20), dtype=torch.uint8, device="cuda")
+    rd_out = torch.zeros(1, dtype=torch.int32, device="cuda")
+
+    def hbm_read_time(nbytes):
+        """Seconds per okf_stream_read of nbytes, rotated over rd_buf."""
+        nb = nbytes // 16 * 16
+        nrot = max(2, ROTATE_BYTES // nb)
+        step = (ROTATE_BYTES // nrot) // 256 * 256
+        base = rd_buf.data_ptr()
+        fn, h, op = enc._lib.okf_stream_read, enc.h, rd_out.data_ptr()
+
+        def call(i):
+            fn(h, base + (i % nrot) * step, nb, op)
+        return time_calls(call, args.steps, 5)[0]
+
+    cpu_cores = None
+
+    def cpu_config(name, t, M, K, N, ws_np, Xn, xs):
+        """The reference's CPU path (oracle restatement of GQ.matvec / GQ.matmul,
+        LLM/Gemma/Gemma4Quant.swift:89-170; Q2_0.matvec, LLM/Base/Quant.swift:28-65)
+        on this host's cores for one call of the config: median of >= 5 runs
+        (one run for the pp512 GEMM)."""
+        import oracle  # the CPU baseline leg only
+
+        nonlocal cpu_cores
+        if cpu_cores is None:
+            cpu_cores = oracle.usable_cores()
+        if "silu" in name:
+            U = synth.activations(N, K, xs + 100)[0]
+            run = lambda: oracle.matvec(t, ws_np[0], K, M, oracle.silu_mul(Xn[0], U), threads=cpu_cores)
+        elif len(ws_np) > 1:
+            run = lambda: [oracle.matvec(t, w, K, M, Xn[0], threads=cpu_cores) for w in ws_np]
+        elif N == 1:
+            run = lambda: oracle.matvec(t, ws_np[0], K, M, Xn[0], threads=cpu_cores)
+        else:
+            run = lambda: oracle.matmul(t, ws_np[0], K, M, Xn, threads=cpu_cores)
+        reps = 1 if N >= 512 else 5
+        ts = []
+        for _ in range(reps):
+            s0 = time.perf_counter()
+            run()
+            ts.append(time.perf_counter() - s0)
+        return {"cpu_us": round(float(np.median(ts)) * 1e6, 1), "cpu_runs": reps, "cpu_cores": cpu_cores}
+
     # ----------------------------------------------------------- headline
     t0 = time.time()
     value, step_s, roofline = None, None, None
@@ -228,8 +272,8 @@ def main():
             torch.cuda.empty_cache()
             log(f"bench: generating {name}")
             ws_np = [synth.weights(t, M, K, sd) for sd in seeds]
-            wcache[key] = (sum(w.nbytes for w in ws_np), [rotated(w) for w in ws_np])
-        wbytes, copies_l = wcache[key]
+            wcache[key] = (sum(w.nbytes for w in ws_np), [rotated(w) for w in ws_np], ws_np)
+        wbytes, copies_l, ws_np = wcache[key]
         X = torch.from_numpy(synth.activations(N, K, xs)).cuda()
         Ys = [torch.empty((N, M), device="cuda") for _ in seeds]
         nr = len(copies_l[0])
@@ -262,6 +306,13 @@ def main():
             rec["bound"], rec["frac"] = "mfma_fp16", round(flops / mean_s / FP16_PEAK, 4)
         else:
             rec["bound"], rec["frac"] = "hbm", round(wbytes / mean_s / HBM_PEAK, 4)
+            # the attainable single-launch ceiling: a plain streaming read of
+            # the same number of bytes, rotated over the same >= 1 GiB
+            rd_s = hbm_read_time(wbytes)
+            rec["hbm_read_us"] = round(rd_s * 1e6, 3)
+            rec["hbm_read_frac"] = round(wbytes / rd_s / HBM_PEAK, 4)
+        if not args.no_cpu:
+            rec.update(cpu_config(name, t, M, K, N, ws_np, X.cpu().numpy(), xs))
         log("bench:", json.dumps(rec))
         suite.append(rec)
         del X, Ys
@@ -336,7 +387,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16 x f16 products, f32 accumulate (weights dequantized exactly to f16)",
+        "dtype": "f32 activations (exact 23-bit integers per 32-weight group) x integer weight codes "
+                 "(int8 dot4, exact per group), f32 scales and accumulation",
         "data": "synthetic (reference LCG, BASELINE.json distributions); weights rotated over >= 1 GiB",
         "config": {"workload": "BASELINE configs[1]: Bonsai-1.7B ternary FFN decode step, one token: "
                                "gate+up Q2_0 W 6144x2048 (one parallel group, as the reference "

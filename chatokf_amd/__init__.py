@@ -29,7 +29,7 @@ EXPORTS = (
     "okf_ctx_create", "okf_ctx_destroy", "okf_ctx_stream", "okf_ctx_reserve", "okf_row_bytes",
     "okf_gemv", "okf_gemv_silu", "okf_ffn", "okf_silu_mul", "okf_gemm", "okf_gemm_tile", "okf_dequant_row",
     "okf_embed_batch", "okf_add_rmsnorm_batch", "okf_argmax_rows", "okf_argmax_rows_noalloc",
-    "okf_parallel_begin",
+    "okf_stream_read", "okf_parallel_begin",
     "okf_parallel_end", "okf_sync", "okf_set_fault_rate", "okf_last_hip_error", "okf_strerror",
     "okf_gguf_open", "okf_gguf_close", "okf_gguf_tensor_count", "okf_gguf_tensor_at", "okf_gguf_find",
     "okf_gguf_kv_int", "okf_gguf_kv_double", "okf_gguf_kv_string", "okf_gguf_data", "okf_gguf_upload",
@@ -96,6 +96,7 @@ def _lib():
             "okf_add_rmsnorm_batch": [vp, vp, vp, vp, vp, u32, u32, ctypes.c_float],
             "okf_argmax_rows": [vp, vp, u32, u32, vp],
             "okf_argmax_rows_noalloc": [vp, vp, u32, u32, vp],
+            "okf_stream_read": [vp, vp, ctypes.c_uint64, vp],
             "okf_parallel_begin": [vp],
             "okf_parallel_end": [vp],
             "okf_sync": [vp],
@@ -280,6 +281,10 @@ class Enc:
         """okf_argmax_rows on the library's fixed device scratch (allocates nothing)."""
         self._check(self._lib.okf_argmax_rows_noalloc(self.h, _ptr(x), int(n), int(rows), _ptr(out)),
                     "okf_argmax_rows_noalloc")
+
+    def stream_read(self, p, nbytes: int, out):
+        """okf_stream_read: out[0] ^= xor of the nbytes at p (a measurement kernel)."""
+        self._check(self._lib.okf_stream_read(self.h, _ptr(p), int(nbytes), _ptr(out)), "okf_stream_read")
 
     def reserve(self, gemm_nk: int, argmax_n: int, argmax_rows: int):
         """okf_ctx_reserve: allocate the scratch now; later calls allocate nothing."""

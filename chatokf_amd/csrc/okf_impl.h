@@ -21,6 +21,7 @@
 #include "okf_gemm.h"
 #include "okf_gemv.h"
 #include "okf_gemv_wide.h"
+#include "okf_gemv_sb.h"
 
 // one matvec y = W x of a launch group (with X2: x = silu(X) * X2)
 struct GemvCall {
@@ -43,6 +44,10 @@ struct okf_ctx {
     // variables override them for measurements)
     int gemv_s = 0;      // K split across a workgroup's wavefronts (0 = auto)
     int gemv_wide = -1;  // one-workgroup-per-CU matvec: -1 auto, 0 never, 1 where it fits
+    int gemv_sb = -1;    // superblock-per-lane matvec: -1 auto, 0 never, 1 where it fits
+    int gemv_sb_rw = 0;  // its rows per workgroup (0 = auto)
+    int gemv_sb_t = 0;   // its threads per workgroup (0 = auto)
+    int gemv_sb_r = 0;   // its rows per lane (0 = auto)
     int gemm_ks = 0;     // wide-tile GEMM: K ranges per remainder tile (0 = auto)
     int gemm_thin = 0;   // leftover-tile kernel variant (A/B switch)
     int gemm_ng = 4;     // wide-tile GEMM: N tiles that share an XCD's row blocks
@@ -263,8 +268,76 @@ bool launch_gemv_wide(okf_ctx *c, const GemvCall &call, uint64_t rb, uint32_t K)
     return true;
 }
 
+template <int F, int NC, int R, int T, bool SILU>
+void launch_sb_t(okf_ctx *c, const GemvGroup &g, uint32_t total, uint64_t rb, uint32_t K, uint32_t RW, size_t lds,
+                 uint32_t sr) {
+    auto go = [&](auto src) {
+        constexpr int SR = decltype(src)::value;
+        const void *fn = (const void *)gemv_sb_kernel<F, NC, R, T, SR, SILU>;
+        static std::atomic<uint64_t> attr{0};  // devices that have the attribute set
+        set_lds_attr(c, fn, attr);
+        hipLaunchKernelGGL((gemv_sb_kernel<F, NC, R, T, SR, SILU>), dim3(total), dim3(T), lds, c->stream, g, rb, K,
+                           RW);
+    };
+    switch (sr) {
+        case 1: go(std::integral_constant<int, 1>{}); break;
+        case 2: go(std::integral_constant<int, 2>{}); break;
+        case 3: go(std::integral_constant<int, 3>{}); break;
+        default: go(std::integral_constant<int, 5>{}); break;
+    }
+}
+
+// Superblock-per-lane matvec (gemv_sb_kernel): true when launched.  A
+// workgroup of T = 256 lanes takes RW = T / nsb rows, one superblock per
+// lane.  Measured on MI355X (A/B in one process): Q4_K 17408 x 5120 from
+// 14.8-16.5 us (gemv_kernel) to 13.4-13.9 us; rows of more than 32
+// superblocks stay on the other kernels (5120 x 17408: no gain, and with
+// several superblocks per lane a second item's loads wait for the first
+// item's compute).
+template <int F, int NC, bool SILU>
+bool launch_gemv_sb(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32_t K) {
+    if constexpr (!sb_fmt<F>() || NC > 2) {
+        return false;
+    } else {
+        const uint32_t nsb = K / 256;
+        if (c->gemv_sb == 0 || (c->gemv_sb < 0 && (nsb > 32 || NC > 1))) return false;
+        uint32_t T = c->gemv_sb_t ? (uint32_t)c->gemv_sb_t : 256;
+        if (T != 256 && T != 512) T = 256;
+        const uint32_t sr = (K / 8 + T - 1) / T;  // staging rounds
+        if (sr > 5 || (NC > 1 && sr > 3)) return false;
+        // two rows per lane only on request (each staged activation read then
+        // serves both; measured no faster)
+        const uint32_t R = c->gemv_sb_r == 2 && NC == 1 ? 2 : 1;
+        uint32_t RW = c->gemv_sb_rw ? (uint32_t)c->gemv_sb_rw : std::max(1u, T / nsb) * R;
+        RW = std::max(R, RW / R * R);
+        const size_t lds = ((size_t)NC * nsb * SB_CHUNKS * 16) + (size_t)RW * nsb * NC * sizeof(float);
+        if (lds > c->max_lds) return false;
+        GemvGroup g{};
+        uint32_t total = 0;
+        for (int i = 0; i < n; i++) {
+            g.W[i] = calls[i].W;
+            g.X[i] = calls[i].X;
+            g.X2[i] = calls[i].X2;
+            g.Y[i] = calls[i].Y;
+            g.M[i] = calls[i].M;
+            total += (calls[i].M + RW - 1) / RW;
+            g.end[i] = total;
+        }
+        g.n = (uint32_t)n;
+        if (R == 2 && NC == 1) {
+            if (T == 256) launch_sb_t<F, NC, 2, 256, SILU>(c, g, total, rb, K, RW, lds, sr);
+            else launch_sb_t<F, NC, 2, 512, SILU>(c, g, total, rb, K, RW, lds, sr);
+        } else {
+            if (T == 256) launch_sb_t<F, NC, 1, 256, SILU>(c, g, total, rb, K, RW, lds, sr);
+            else launch_sb_t<F, NC, 1, 512, SILU>(c, g, total, rb, K, RW, lds, sr);
+        }
+        return true;
+    }
+}
+
 template <int F, int NC, bool SILU = false>
 void launch_gemv_nc(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32_t K) {
+    if (launch_gemv_sb<F, NC, SILU>(c, calls, n, rb, K)) return;
     // (Q4_K and Q8_0 units are too large for a deep ring at N > 1; the
     // formats added after the measurements take the many-workgroup kernel)
     if constexpr (!SILU && !((F == Q4_K || F == Q8_0) && NC > 1) && F != Q5_K && F != Q6_K && F != IQ4_XS &&

@@ -174,3 +174,35 @@ __global__ __launch_bounds__(NORM_THREADS) void argmax_kernel(const float *__res
 }
 
 }  // namespace okf
+
+namespace okf {
+
+// Streaming read of a byte range: the attainable single-launch HBM read rate
+// that the matvec rows are compared with (no reference counterpart; it is a
+// measurement of the machine).  1024-thread workgroups, one to four per CU
+// (the launch picks by size); each owns a contiguous range of 16-byte chunks and keeps four loads per thread
+// in flight.  The xor of every dword is folded into *out (one atomic per
+// wavefront), so the read cannot be elided and its result can be checked.
+constexpr int SR_THREADS = 1024, SR_U = 4;
+static __global__ __launch_bounds__(SR_THREADS) void stream_read_kernel(const u32x4 *__restrict__ p, uint64_t n16,
+                                                                      uint64_t per_wg, uint32_t *out) {
+    const uint64_t b = (uint64_t)blockIdx.x * per_wg, e = min(b + per_wg, n16);
+    uint32_t acc = 0;
+    uint64_t i = b + threadIdx.x;
+    for (; i + (SR_U - 1) * SR_THREADS < e; i += SR_U * SR_THREADS) {
+        u32x4 v[SR_U];
+#pragma unroll
+        for (int u = 0; u < SR_U; u++) v[u] = p[i + u * SR_THREADS];
+#pragma unroll
+        for (int u = 0; u < SR_U; u++) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+    }
+    for (; i < e; i += SR_THREADS) {
+        const u32x4 v = p[i];
+        acc ^= v[0] ^ v[1] ^ v[2] ^ v[3];
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) acc ^= __shfl_xor(acc, o);
+    if ((threadIdx.x & 63) == 0 && acc) atomicXor(out, acc);
+}
+
+}  // namespace okf

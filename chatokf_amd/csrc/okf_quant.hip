@@ -248,6 +248,10 @@ int okf_ctx_create(int device, okf_ctx **out) {
             c->cus = (uint32_t)v;
         if (const char *e = getenv("OKF_GEMV_S")) c->gemv_s = atoi(e);
         if (const char *e = getenv("OKF_GEMV_WIDE")) c->gemv_wide = atoi(e);
+        if (const char *e = getenv("OKF_GEMV_SB")) c->gemv_sb = atoi(e);
+        if (const char *e = getenv("OKF_GEMV_SB_RW")) c->gemv_sb_rw = atoi(e);
+        if (const char *e = getenv("OKF_GEMV_SB_T")) c->gemv_sb_t = atoi(e);
+        if (const char *e = getenv("OKF_GEMV_SB_R")) c->gemv_sb_r = atoi(e);
         if (const char *e = getenv("OKF_GEMM_KS")) c->gemm_ks = atoi(e);
         if (const char *e = getenv("OKF_GEMM_NG")) c->gemm_ng = atoi(e);
         if (const char *e = getenv("OKF_GEMM_THIN")) c->gemm_thin = atoi(e);
@@ -403,6 +407,21 @@ int okf_argmax_rows_noalloc(okf_ctx *c, const float *x, uint32_t n, uint32_t row
     ArgPair *pairs = (ArgPair *)c->scratch;
     uint32_t *cnt = (uint32_t *)(c->scratch + SCRATCH_CNT_OFF);
     hipLaunchKernelGGL(argmax_kernel, dim3(chunks, rows), dim3(NORM_THREADS), 0, c->stream, x, n, pairs, cnt,
+                       out);
+    return finish(c);
+}
+
+int okf_stream_read(okf_ctx *c, const void *p, uint64_t bytes, uint32_t *out) {
+    if (!p || !out) return OKF_E_ARG;
+    if (bytes == 0 || bytes % 16 || !aligned16(p)) return OKF_E_SHAPE;
+    int st = begin(c);
+    if (st) return st;
+    const uint64_t n16 = bytes / 16;
+    // one workgroup per 48 KB, between one and four per CU (measured best
+    // on MI355X for 3 MB and 50 MB reads)
+    const uint32_t wgs = (uint32_t)std::min<uint64_t>(4 * c->cus, std::max<uint64_t>(c->cus, bytes / (48 << 10)));
+    const uint64_t per = (n16 + wgs - 1) / wgs;
+    hipLaunchKernelGGL(stream_read_kernel, dim3(wgs), dim3(SR_THREADS), 0, c->stream, (const u32x4 *)p, n16, per,
                        out);
     return finish(c);
 }

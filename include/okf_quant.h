@@ -184,6 +184,12 @@ int okf_argmax_rows(okf_ctx *ctx, const float *x, uint32_t n, uint32_t rows, int
 #define OKF_NOALLOC_ARGMAX_ROWS 4096
 int okf_argmax_rows_noalloc(okf_ctx *ctx, const float *x, uint32_t n, uint32_t rows, int32_t *out);
 
+/* A plain streaming read of bytes (a multiple of 16) at the 16-byte-aligned
+ * device address p: *out ^= the xor of all its 32-bit words.  No counterpart
+ * in the reference: it measures the attainable single-launch HBM read rate
+ * that the matvec kernels are compared with (bench.py's hbm_read rows). */
+int okf_stream_read(okf_ctx *ctx, const void *p, uint64_t bytes, uint32_t *out);
+
 /* MetalEnc.embedBatch (MetalEnc.swift:1096-1146; kernels embed_batch,
  * q4_k_embed_batch, iq_embed_batch, LLM/metal/Kernels.metal:1444-1482):
  * out[n][K] = row ids[n] of w dequantized to fp32, n < N, bit-identical to

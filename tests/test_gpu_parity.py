@@ -134,7 +134,7 @@ def test_gemv_full_config(enc, name, t, M, K, seed):
 # Shapes that exercise tails: M not a multiple of the rows per workgroup, a
 # single block per row, K not a multiple of 64 units.
 EDGE = [(Q8_0, 1, 32), (Q8_0, 3, 96), (Q8_0, 4099, 2080), (Q2_0, 5, 128), (Q2_0, 4097, 384),
-        (Q4_K, 1, 256), (Q4_K, 7, 768), (Q4_K, 4101, 2304), (IQ2_XXS, 2, 256), (IQ2_XXS, 4103, 1280),
+        (Q4_K, 1, 256), (Q4_K, 7, 768), (Q4_K, 4101, 2304), (Q4_K, 1000, 8192), (Q4_K, 13, 8448), (IQ2_XXS, 2, 256), (IQ2_XXS, 4103, 1280),
         (Q4_0, 1, 32), (Q4_0, 4099, 2080), (Q4_0, 2048, 4096), (IQ4_NL, 3, 96), (IQ4_NL, 4099, 2080),
         (IQ4_NL, 2048, 4096), (Q5_K, 1, 256), (Q5_K, 4101, 2304), (Q6_K, 3, 256), (Q6_K, 4099, 1280),
         (IQ4_XS, 2, 512), (IQ4_XS, 4103, 2304)] + \
@@ -340,6 +340,18 @@ def test_argmax_repeated_calls_reset_counters(enc):
         out = torch.full((rows,), -7, dtype=torch.int32, device="cuda")
         enc.argmax_rows(dev(x), n, rows, out)
         assert np.array_equal(host(out), oracle.argmax_rows(x))
+
+
+@pytest.mark.parametrize("nbytes", [16, 16 * 1000 + 16 * 7, 50135040])
+def test_stream_read_xor(enc, nbytes):
+    # the calibration read touches every byte exactly once: its xor of all
+    # 32-bit words equals numpy's, folded into the value already in out
+    rng = np.random.default_rng(nbytes)
+    a = rng.integers(0, 2**32, size=nbytes // 4, dtype=np.uint32)
+    out = torch.tensor([0x5A5A5A5A], dtype=torch.int32, device="cuda")
+    enc.stream_read(dev(a.view(np.int32)), nbytes, out)
+    want = np.bitwise_xor.reduce(a) ^ np.uint32(0x5A5A5A5A)
+    assert int(host(out)[0]) & 0xFFFFFFFF == int(want)
 
 
 # ------------------------------------------------------------ reserve
