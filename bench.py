@@ -194,20 +194,18 @@ def main():
         xp, hp, h2p, yp = (t.data_ptr() for t in (x, h, h2, y))
 
         # gate and up in one parallel group, as the reference's FFN encodes
-        # them (LLM/Qwen/QwenMetalEngine.swift:918-923, MetalEnc.parallel)
+        # them (LLM/Qwen/QwenMetalEngine.swift:918-923, MetalEnc.parallel),
+        # then down on silu(gate) * up (siluMul + gemv, :924-928): one
+        # okf_ffn call per step (two launches)
         pbegin, pend, hctx = enc._lib.okf_parallel_begin, enc._lib.okf_parallel_end, enc.h
-
-        # then down on silu(gate) * up (siluMul + gemv, :924-928) as one call
         silu_c = enc.raw_gemv_silu
+        ffn_c = enc._lib.okf_ffn
+        refs = [(ctypes.byref(g), ctypes.byref(u), ctypes.byref(d)) for g, u, d in zip(gw, uw, dw)]
 
         def ffn_step(i):
-            j = i % nrot
-            pbegin(hctx)
-            gemv_c(gw[j], xp, hp)
-            gemv_c(uw[j], xp, h2p)
-            if pend(hctx):
-                raise RuntimeError("okf_parallel_end failed")
-            silu_c(dw[j], hp, h2p, yp)
+            gr, ur, dr = refs[i % nrot]
+            if ffn_c(hctx, gr, ur, dr, xp, hp, h2p, yp):
+                raise RuntimeError("okf_ffn failed")
 
         for i in range(args.warmup):
             ffn_step(i)
@@ -227,6 +225,7 @@ def main():
             gemv_c(uw[j], xp, h2p)
             pend(hctx)
 
+        step_gpu_t, _ = time_calls(ffn_step, args.steps, 5)
         gate_t, _ = time_calls(gate_up, args.steps, 5)
         down_t, _ = time_calls(lambda i: silu_c(dw[i % nrot], hp, h2p, yp), args.steps, 5)
         if gate_t >= down_t:
@@ -238,7 +237,8 @@ def main():
                     "unit": "GB/s", "frac": round(dom[1] / dom[2] / HBM_PEAK, 4),
                     "traffic": load_traffic(dom[0]), "us_per_launch": round(dom[2] * 1e6, 3),
                     "algorithmic_bytes_per_launch": dom[1]}
-        log(f"bench: ffn step {step_s*1e6:.2f} us, {value:.1f} GB/s; gate+up {gate_t*1e6:.2f} us, "
+        log(f"bench: ffn step {step_s*1e6:.2f} us wall ({step_gpu_t*1e6:.2f} us queued), {value:.1f} GB/s; "
+            f"gate+up {gate_t*1e6:.2f} us, "
             f"down {down_t*1e6:.2f} us")
         del gates, ups, downs
         torch.cuda.empty_cache()

@@ -92,7 +92,9 @@ __global__ __launch_bounds__(NORM_THREADS) void add_rmsnorm_kernel(float *X,
 // (value, index) pair, and the last workgroup of a row to finish (counted
 // in cnt[row]) reduces the row's pairs in chunk order and sets cnt[row]
 // back to 0 for the next call.
-constexpr uint32_t ARGMAX_CHUNK = NORM_THREADS * 4;  // one float4 per thread: ~240 workgroups per row
+// two float4 per thread: ~120 workgroups for a 248320-wide row (measured
+// on MI355X: 7.2 us with one float4, 6.2 with two, 6.5 with four)
+constexpr uint32_t ARGMAX_CHUNK = NORM_THREADS * 8;
 
 struct ArgPair {
     float v;
@@ -149,21 +151,29 @@ __global__ __launch_bounds__(NORM_THREADS) void argmax_kernel(const float *__res
     }
     block_argmax(bv, bi, red);
     ArgPair *p = pairs + (uint64_t)row * chunks;
+    // Cross-workgroup hand-off without fences.  The pair is stored and the
+    // row's counter incremented as agent-scope relaxed atomics (on gfx950
+    // these are issued with the sc1 bit: coherent across the XCDs' L2s);
+    // s_waitcnt vmcnt(0) between them makes the pair's store complete at
+    // the coherence point before the count that announces it is issued.
+    // The last workgroup reads the pairs with agent-scope atomic loads.
+    // (An acquire-release counter costs an L2 write-back and invalidate per
+    // workgroup: measured 9.7 us for a 248320-wide row, against 5.6 us with
+    // this scheme.)
     if (threadIdx.x == 0) {
-        p[c] = ArgPair{bv, bi};
-        // release: the pair is visible device-wide before the count says so
-        const uint32_t prev = __hip_atomic_fetch_add(cnt + row, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t pk = (uint64_t)__float_as_uint(bv) | ((uint64_t)(uint32_t)bi << 32);
+        __hip_atomic_store((uint64_t *)(p + c), pk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        const uint32_t prev = __hip_atomic_fetch_add(cnt + row, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         last = prev == chunks - 1;
     }
     __syncthreads();
     if (!last) return;
-    // acquire for every thread of the last workgroup: the other pairs are visible
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     bv = -__builtin_inff();
     bi = 0;
     for (uint32_t k = threadIdx.x; k < chunks; k += NORM_THREADS) {
-        const ArgPair q = p[k];
-        arg_take(bv, bi, q.v, q.i);
+        const uint64_t q = __hip_atomic_load((const uint64_t *)(p + k), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        arg_take(bv, bi, __uint_as_float((uint32_t)q), (int32_t)(q >> 32));
     }
     __syncthreads();  // (red is reused)
     block_argmax(bv, bi, red);

@@ -398,8 +398,11 @@ int okf_argmax_rows(okf_ctx *c, const float *x, uint32_t n, uint32_t rows, int32
 int okf_argmax_rows_noalloc(okf_ctx *c, const float *x, uint32_t n, uint32_t rows, int32_t *out) {
     if (!x || !out) return OKF_E_ARG;
     if (n == 0 || rows == 0 || n > 0x7FFFFFFFu || rows > OKF_NOALLOC_ARGMAX_ROWS) return OKF_E_SHAPE;
+    // the documented limit counts 1024-value chunks (the kernel's chunks are
+    // larger, so it uses at most that many pairs)
+    static_assert(ARGMAX_CHUNK % 1024 == 0, "argmax chunks are whole 1024-value pieces");
+    if ((uint64_t)((n + 1023) / 1024) * rows > OKF_NOALLOC_ARGMAX_PAIRS) return OKF_E_SHAPE;
     const uint32_t chunks = (n + ARGMAX_CHUNK - 1) / ARGMAX_CHUNK;
-    if ((uint64_t)chunks * rows > OKF_NOALLOC_ARGMAX_PAIRS) return OKF_E_SHAPE;
     int st = begin(c);
     if (st) return st;
     // the device's scratch array through its device address (c->scratch,
