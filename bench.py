@@ -155,7 +155,7 @@ def main():
             U = synth.activations(N, K, xs + 100)[0]
             run = lambda: oracle.matvec(t, ws_np[0], K, M, oracle.silu_mul(Xn[0], U), threads=cpu_cores)
         elif len(ws_np) > 1:
-            run = lambda: [oracle.matvec(t, w, K, M, Xn[0], threads=cpu_cores) for w in ws_np]
+            run = lambda: oracle.silu_mul(*[oracle.matvec(t, w, K, M, Xn[0], threads=cpu_cores) for w in ws_np])
         elif N == 1:
             run = lambda: oracle.matvec(t, ws_np[0], K, M, Xn[0], threads=cpu_cores)
         else:
@@ -198,7 +198,6 @@ def main():
         # then down on silu(gate) * up (siluMul + gemv, :924-928): one
         # okf_ffn call per step (two launches)
         pbegin, pend, hctx = enc._lib.okf_parallel_begin, enc._lib.okf_parallel_end, enc.h
-        silu_c = enc.raw_gemv_silu
         ffn_c = enc._lib.okf_ffn
         refs = [(ctypes.byref(g), ctypes.byref(u), ctypes.byref(d)) for g, u, d in zip(gw, uw, dw)]
 
@@ -217,21 +216,21 @@ def main():
         step_s = (time.perf_counter() - w0) / args.steps
         value = step_bytes / step_s / 1e9
 
-        # dominant kernel of the step: HIP events around batches of its launches
+        # the step's two launches, each timed alone: gate and up with the SiLU
+        # (okf_gemv_gate_up, one grid), then down on g (okf_gemv)
+        gu_c = enc._lib.okf_gemv_gate_up
+
         def gate_up(i):
-            j = i % nrot
-            pbegin(hctx)
-            gemv_c(gw[j], xp, hp)
-            gemv_c(uw[j], xp, h2p)
-            pend(hctx)
+            gr, ur, _ = refs[i % nrot]
+            gu_c(hctx, gr, ur, xp, hp, h2p)
 
         step_gpu_t, _ = time_calls(ffn_step, args.steps, 5)
         gate_t, _ = time_calls(gate_up, args.steps, 5)
-        down_t, _ = time_calls(lambda i: silu_c(dw[i % nrot], hp, h2p, yp), args.steps, 5)
+        down_t, _ = time_calls(lambda i: gemv_c(dw[i % nrot], hp, yp), args.steps, 5)
         if gate_t >= down_t:
             dom = ("q2_0_matvec_gate_up_2x6144x2048", gate_np.nbytes + up_np.nbytes, gate_t)
         else:
-            dom = ("q2_0_matvec_silu_2048x6144", down_np.nbytes, down_t)
+            dom = ("q2_0_matvec_2048x6144", down_np.nbytes, down_t)
         roofline = {"kernel": f"okf::gemv_kernel<Q2_0> ({dom[0]})", "bound": "hbm",
                     "achieved": round(dom[1] / dom[2] / 1e9, 1), "peak": HBM_PEAK / 1e9,
                     "unit": "GB/s", "frac": round(dom[1] / dom[2] / HBM_PEAK, 4),
@@ -251,7 +250,7 @@ def main():
         ("q2_0_matvec_2048x6144", ok.Q2_0, 2048, 6144, 1, 1102, 2102),
         # down on silu(gate) * up (okf_gemv_silu)
         ("q2_0_matvec_silu_2048x6144", ok.Q2_0, 2048, 6144, 1, 1102, 2102),
-        # gate and up as one parallel group (two weight seeds, one x)
+        # gate and up in one grid with the SiLU (two weight seeds, one x)
         ("q2_0_matvec_gate_up_2x6144x2048", ok.Q2_0, 6144, 2048, 1, (1002, 1202), 2002),
         ("q4_k_matvec_17408x5120", ok.Q4_K, 17408, 5120, 1, 1003, 2003),
         ("q4_k_matvec_5120x17408", ok.Q4_K, 5120, 17408, 1, 1103, 2103),
@@ -288,13 +287,13 @@ def main():
         elif len(seeds) == 1:
             def call(i, wcs=wcs_l[0], N=N, xp_=xp_, yp_=yps[0], nr=nr):
                 enc.raw_gemm(wcs[i % nr], xp_, N, yp_)
-        else:
-            def call(i, wcs_l=wcs_l, xp_=xp_, yps=yps, nr=nr):
-                enc._lib.okf_parallel_begin(enc.h)
-                for wcs, yp_ in zip(wcs_l, yps):
-                    enc.raw_gemv(wcs[i % nr], xp_, yp_)
-                if enc._lib.okf_parallel_end(enc.h):
-                    raise RuntimeError("okf_parallel_end failed")
+        else:  # gate and up in one grid with the SiLU (okf_gemv_gate_up)
+            grefs = [(ctypes.byref(a), ctypes.byref(b)) for a, b in zip(*wcs_l)]
+
+            def call(i, grefs=grefs, xp_=xp_, yps=yps, nr=nr):
+                gr, ur = grefs[i % nr]
+                if enc._lib.okf_gemv_gate_up(enc.h, gr, ur, xp_, yps[0], yps[1]):
+                    raise RuntimeError("okf_gemv_gate_up failed")
 
         n_calls = args.steps if N < 512 else max(10, args.steps // 10)
         mean_s, med_s = time_calls(call, n_calls, max(3, args.warmup // 2))  # (mean, best batch)
@@ -390,10 +389,10 @@ def main():
         "dtype": "f32 activations (exact 23-bit integers per 32-weight group) x integer weight codes "
                  "(int8 dot4, exact per group), f32 scales and accumulation",
         "data": "synthetic (reference LCG, BASELINE.json distributions); weights rotated over >= 1 GiB",
-        "config": {"workload": "BASELINE configs[1]: Bonsai-1.7B ternary FFN decode step, one token: "
-                               "gate+up Q2_0 W 6144x2048 (one parallel group, as the reference "
-                               "encodes them), then down Q2_0 W 2048x6144 on silu(gate)*up "
-                               "(siluMul fused into the down matvec)",
+        "config": {"workload": "BASELINE configs[1]: Bonsai-1.7B ternary FFN decode step, one token "
+                               "(okf_ffn): gate+up Q2_0 W 6144x2048 in one grid with the siluMul "
+                               "(as the reference's parallel group + in-place siluMul), then down "
+                               "Q2_0 W 2048x6144 on silu(gate)*up",
                    "weight_bytes_per_step": step_bytes, "parallelism": "single GPU"},
         "roofline": roofline,
         "cpu_baseline": cpu,

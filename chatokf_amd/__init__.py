@@ -27,7 +27,7 @@ LIB_PATH = os.environ.get("OKF_LIB") or os.path.join(HERE, "libokf_quant.so")
 # Every symbol include/okf_quant.h declares.
 EXPORTS = (
     "okf_ctx_create", "okf_ctx_destroy", "okf_ctx_stream", "okf_ctx_reserve", "okf_row_bytes",
-    "okf_gemv", "okf_gemv_silu", "okf_ffn", "okf_silu_mul", "okf_gemm", "okf_gemm_tile", "okf_dequant_row",
+    "okf_gemv", "okf_gemv_silu", "okf_gemv_gate_up", "okf_ffn", "okf_silu_mul", "okf_gemm", "okf_gemm_tile", "okf_dequant_row",
     "okf_embed_batch", "okf_add_rmsnorm_batch", "okf_argmax_rows", "okf_argmax_rows_noalloc",
     "okf_stream_read", "okf_parallel_begin",
     "okf_parallel_end", "okf_sync", "okf_set_fault_rate", "okf_last_hip_error", "okf_strerror",
@@ -88,6 +88,7 @@ def _lib():
             "okf_gemv": [vp, W, vp, vp],
             "okf_gemv_silu": [vp, W, vp, vp, vp],
             "okf_ffn": [vp, W, W, W, vp, vp, vp, vp],
+            "okf_gemv_gate_up": [vp, W, W, vp, vp, vp],
             "okf_silu_mul": [vp, vp, vp, u32],
             "okf_gemm": [vp, W, vp, u32, vp],
             "okf_gemm_tile": [vp, W, vp, u32, vp],
@@ -202,10 +203,17 @@ class Enc:
                     "okf_gemv_silu")
 
     def ffn(self, gate: QuantTensor, up: QuantTensor, down: QuantTensor, x, g, u, y):
-        """okf_ffn: g = W_gate x, u = W_up x, y = W_down (silu(g) * u)."""
+        """okf_ffn: u = W_up x, g = silu(W_gate x) * u (in place, as the reference's
+        siluMul), y = W_down g."""
         gc, uc, dc = gate.c(), up.c(), down.c()
         self._check(self._lib.okf_ffn(self.h, ctypes.byref(gc), ctypes.byref(uc), ctypes.byref(dc), _ptr(x),
                                       _ptr(g), _ptr(u), _ptr(y)), "okf_ffn")
+
+    def gemv_gate_up(self, gate: QuantTensor, up: QuantTensor, x, g, u):
+        """okf_gemv_gate_up: u = W_up x, g = silu(W_gate x) * u."""
+        gc, uc = gate.c(), up.c()
+        self._check(self._lib.okf_gemv_gate_up(self.h, ctypes.byref(gc), ctypes.byref(uc), _ptr(x), _ptr(g),
+                                               _ptr(u)), "okf_gemv_gate_up")
 
     def raw_ffn(self, gc: OkfWeight, uc: OkfWeight, dc: OkfWeight, x: int, g: int, u: int, y: int):
         """okf_ffn on prebuilt descriptors and raw device pointers."""

@@ -830,12 +830,18 @@ __device__ __forceinline__ void stage_x(const float *__restrict__ X, const float
     }
 }
 
+// Paired mode (W2 != nullptr; one column, S = 1, no SiLU staging): the
+// FFN's gate (W) and up (W2) share x, and the workgroup's first half of row
+// slots takes rows of W, the second half the same rows of W2.  The outputs
+// are Y = silu(W x) * (W2 x) (the reference's in-place siluMul leaves that
+// in its gate buffer) and Y2 = W2 x.
 template <int F, int NC, int R, int D, int S, bool SILU>
 __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ W, uint64_t row_bytes, uint32_t K,
                                           uint32_t M, const float *__restrict__ X,
                                           const float *__restrict__ X2, float *__restrict__ Y,
                                           const u32x4 *__restrict__ tab_g, uint32_t cunits,
-                                          uint32_t blk) {
+                                          uint32_t blk, const uint8_t *__restrict__ W2 = nullptr,
+                                          float *__restrict__ Y2 = nullptr) {
     constexpr int L = GV_L;
     extern __shared__ u32x4 lds[];
     constexpr uint32_t TAB = F == IQ2_XXS ? 384 : 0;
@@ -848,10 +854,15 @@ __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ W, uint64_
     if constexpr (F == IQ2_XXS)
         for (uint32_t e = tid; e < TAB; e += nthr) tab[e] = tab_g[e];
 
-    const uint32_t m0 = ((blk * groups + group) * GV_SLOTS + slot) * R;
+    // row slot q of the workgroup; paired: q < QH takes W, q >= QH W2
+    const bool pair = W2 != nullptr;
+    const uint32_t q = group * GV_SLOTS + slot, QH = groups * GV_SLOTS / 2;
+    const bool second = pair && q >= QH;
+    const uint32_t m0 = pair ? (blk * QH + (second ? q - QH : q)) * R : ((blk * groups + group) * GV_SLOTS + slot) * R;
+    const uint8_t *Wq = second ? W2 : W;
     const uint8_t *rows[R];
 #pragma unroll
-    for (int r = 0; r < R; r++) rows[r] = W + (uint64_t)min(m0 + r, M - 1) * row_bytes;
+    for (int r = 0; r < R; r++) rows[r] = Wq + (uint64_t)min(m0 + r, M - 1) * row_bytes;
     constexpr uint32_t UW = unit_weights<F>();
     constexpr uint32_t UG = unit_groups<F>();
     const uint32_t units = K / UW, cs = cunits * unit_chunks<F>() * 4, gcs = cunits * UG;
@@ -943,6 +954,24 @@ __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ W, uint64_
                 acc[r][n] = v;
             }
     }
+    if constexpr (NC == 1 && S == 1 && !SILU) {
+        if (pair) {
+            // gate and up values of the workgroup's rows meet in LDS
+            if (i == 0)
+#pragma unroll
+                for (int r = 0; r < R; r++) red[q * R + r] = acc[r][0];
+            __syncthreads();
+            if (tid < QH * R) {
+                const uint32_t m = blk * QH * R + tid;
+                const float gv = red[tid], uv = red[QH * R + tid];
+                if (m < M) {
+                    Y[m] = silu_mul1(gv, uv);
+                    Y2[m] = uv;
+                }
+            }
+            return;
+        }
+    }
 #pragma unroll
     for (int r = 0; r < R; r++)
 #pragma unroll
@@ -963,6 +992,7 @@ struct GemvGroup {
     uint32_t M[GV_GROUP];
     uint32_t end[GV_GROUP];
     uint32_t n;
+    uint32_t pair;  // 1: W[0] (gate) and W[1] (up) paired in each workgroup (gemv_body)
 };
 
 template <int F, int NC, int R, int D, int S, bool SILU>
@@ -972,6 +1002,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvGroup g, uint64_t row_byt
 #pragma unroll
     for (int k = 0; k + 1 < GV_GROUP; k++)
         if (k + 1 < (int)g.n && blockIdx.x >= g.end[k]) i = k + 1;
+    if constexpr (NC == 1 && S == 1 && !SILU)
+        if (g.pair) {
+            gemv_body<F, NC, R, D, S, SILU>(g.W[0], row_bytes, K, g.M[0], g.X[0], nullptr, g.Y[0], tab_g, cunits,
+                                            blockIdx.x, g.W[1], g.Y[1]);
+            return;
+        }
     const uint32_t blk = blockIdx.x - (i ? g.end[i - 1] : 0);
     gemv_body<F, NC, R, D, S, SILU>(g.W[i], row_bytes, K, g.M[i], g.X[i], g.X2[i], g.Y[i], tab_g, cunits,
                                     blk);

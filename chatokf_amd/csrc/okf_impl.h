@@ -144,14 +144,14 @@ inline int finish(okf_ctx *c) {
 
 template <int F, int NC, int S, bool SILU, int DX = 0>
 void launch_gemv_s(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32_t K,
-                   uint32_t cunits, size_t lds) {
+                   uint32_t cunits, size_t lds, bool pair = false) {
     // Q2_0 and Q8_0 at N = 1: a three-deep ring when a wavefront runs three
     // or more steps (the down projection), so that no step waits for a load
     // issued after the first compute; two otherwise (a third buffer would
     // only re-read).  Measured: Q2_0 2048x6144 4.95 -> 4.75 us.
     if constexpr (DX == 0 && NC == 1 && (F == Q2_0 || F == Q8_0)) {
         const uint32_t steps = (K / unit_weights<F>() + GV_L * S - 1) / (GV_L * S);
-        if (steps >= 3) return launch_gemv_s<F, NC, S, SILU, 3>(c, calls, n, rb, K, cunits, lds);
+        if (steps >= 3) return launch_gemv_s<F, NC, S, SILU, 3>(c, calls, n, rb, K, cunits, lds, pair);
     }
     // two rows per slot (each staged activation read serves both) where
     // measured faster: IQ2_XXS with 2..5 columns, Q4_K and Q2_0 with 5.  (A
@@ -175,6 +175,10 @@ void launch_gemv_s(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32
         g.end[i] = total;
     }
     g.n = (uint32_t)n;
+    if (pair) {  // gate and up rows in the same workgroups: half the row slots each
+        g.pair = 1;
+        total = (calls[0].M + rows_per_wg / 2 - 1) / (rows_per_wg / 2);
+    }
     // the tables the compute reads: IQ2_XXS's LDS rows (copied from c->tab),
     // or the grid formats' device-memory grids
     const u32x4 *tabs = grid_fmt(F) ? (const u32x4 *)c->grids : c->tab8;
@@ -378,6 +382,23 @@ void launch_gemv(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32_t
     }
 }
 
+// The FFN's gate and up (one format, same shape, shared x) in one grid
+// whose workgroups each take the same rows of both: gate <- silu(gate x) *
+// (up x), up <- up x.  The down projection then reads one activation vector
+// with no SiLU in its staging.
+template <int F>
+void launch_gemv_pair(okf_ctx *c, const GemvCall *calls, uint64_t rb, uint32_t K) {
+    constexpr uint32_t UW = unit_weights<F>();
+    const size_t tab = F == IQ2_XXS ? 384 * 16 : 0;
+    const uint32_t units = K / UW;
+    const size_t per_unit = unit_lds_bytes<F>();
+    const size_t red = 4 * GV_SLOTS * 4 * sizeof(float);
+    uint32_t cunits = (units + 63) / 64 * 64;
+    const size_t budget = c->max_lds - tab - red;
+    if (cunits * per_unit > budget) cunits = (uint32_t)(budget / per_unit) / 64 * 64;
+    launch_gemv_s<F, 1, 1, false>(c, calls, 2, rb, K, cunits, tab + cunits * per_unit + red, true);
+}
+
 // The context's scratch (split-tile partial sums, argmax pairs), grown to at
 // least `need` bytes; the stream is drained before an old buffer is freed.
 // After okf_ctx_reserve the sizes are fixed: a call that needs more is an
@@ -526,6 +547,7 @@ void launch_embed(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_
 
 #define OKF_LAUNCHERS(EXT, F)                                                                            \
     EXT template void launch_gemv<F>(okf_ctx *, const GemvCall *, int, uint64_t, uint32_t, uint32_t);    \
+    EXT template void launch_gemv_pair<F>(okf_ctx *, const GemvCall *, uint64_t, uint32_t);               \
     EXT template int launch_gemm<F>(okf_ctx *, const uint8_t *, uint64_t, uint32_t, uint32_t, const float *, \
                                     uint32_t, float *);                                                  \
     EXT template void launch_dequant<F>(okf_ctx *, const uint8_t *, uint32_t, float *);                  \

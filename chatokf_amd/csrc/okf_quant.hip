@@ -328,27 +328,39 @@ int okf_dequant_row(okf_ctx *c, const okf_weight *row, uint32_t n, float *out) {
 // The FFN of the reference's engines (QwenMetalEngine.swift:918-929): gate
 // and up on x as one launch group where their format and K match, then
 // down on silu(gate) * up with the SiLU folded into its activation staging.
-int okf_ffn(okf_ctx *c, const okf_weight *gate, const okf_weight *up, const okf_weight *down, const float *x,
-            float *g, float *u, float *y) {
-    uint64_t rb0 = 0, rb0u = 0, rb1 = 0;
+int okf_gemv_gate_up(okf_ctx *c, const okf_weight *gate, const okf_weight *up, const float *x, float *g,
+                     float *u) {
+    uint64_t rb0 = 0, rb0u = 0;
     int st = check_weight(gate, &rb0);
     if (!st) st = check_weight(up, &rb0u);
-    if (!st) st = check_weight(down, &rb1);
     if (st) return st;
-    if (!x || !g || !u || !y) return OKF_E_ARG;
-    if (gate->K != up->K || gate->M != up->M || down->K != gate->M) return OKF_E_SHAPE;
+    if (!x || !g || !u) return OKF_E_ARG;
+    if (gate->K != up->K || gate->M != up->M) return OKF_E_SHAPE;
     if (!aligned16(x) || !aligned16(g) || !aligned16(u)) return OKF_E_SHAPE;
     if (c && c->grouping) return OKF_E_ARG;
     if ((st = begin(c))) return st;
     const GemvCall gu[2] = {{(const uint8_t *)gate->base + gate->off, x, g, gate->M},
                             {(const uint8_t *)up->base + up->off, x, u, up->M}};
-    const GemvCall dn{(const uint8_t *)down->base + down->off, g, y, down->M, u};
     if (gate->ggml_type == up->ggml_type) {
-        OKF_DISPATCH(gate->ggml_type, launch_gemv, c, gu, 2, rb0, gate->K, 1u);
+        // one grid, each workgroup the same rows of gate and up: g <- silu(g) * u
+        OKF_DISPATCH(gate->ggml_type, launch_gemv_pair, c, gu, rb0, gate->K);
     } else {
         OKF_DISPATCH(gate->ggml_type, launch_gemv, c, &gu[0], 1, rb0, gate->K, 1u);
         OKF_DISPATCH(up->ggml_type, launch_gemv, c, &gu[1], 1, rb0u, up->K, 1u);
+        hipLaunchKernelGGL(silu_mul_kernel, dim3((gate->M + 255) / 256), dim3(256), 0, c->stream, g, u, gate->M);
     }
+    return finish(c);
+}
+
+int okf_ffn(okf_ctx *c, const okf_weight *gate, const okf_weight *up, const okf_weight *down, const float *x,
+            float *g, float *u, float *y) {
+    uint64_t rb1 = 0;
+    int st = check_weight(down, &rb1);
+    if (st) return st;
+    if (!gate || !y) return OKF_E_ARG;
+    if (down->K != gate->M) return OKF_E_SHAPE;
+    if ((st = okf_gemv_gate_up(c, gate, up, x, g, u))) return st;
+    const GemvCall dn{(const uint8_t *)down->base + down->off, g, y, down->M};
     OKF_DISPATCH(down->ggml_type, launch_gemv, c, &dn, 1, rb1, down->K, 1u);
     return finish(c);
 }

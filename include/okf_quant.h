@@ -118,13 +118,23 @@ int okf_gemv(okf_ctx *ctx, const okf_weight *w, const float *x, float *y);
  * Unlike the reference's in-place siluMul, gate is left unchanged. */
 int okf_gemv_silu(okf_ctx *ctx, const okf_weight *w, const float *gate, const float *up, float *y);
 
+/* The gate and up projections of the reference's FFN with its SiLU
+ * (LLM/Qwen/QwenMetalEngine.swift:918-925: MetalEnc.parallel { gemv(gate);
+ * gemv(up) } then the in-place siluMul(gate, up)): u = W_up x,
+ * g = silu(W_gate x) * u.  One launch when gate and up share a format (each
+ * workgroup computes the same rows of both); gate and up have the same K
+ * and M; x, g, u 16-byte aligned. */
+int okf_gemv_gate_up(okf_ctx *ctx, const okf_weight *gate, const okf_weight *up, const float *x, float *g,
+                     float *u);
+
 /* The FFN block of the reference's engines (LLM/Qwen/QwenMetalEngine.swift:
  * 918-929: MetalEnc.parallel { gemv(gate); gemv(up) }, siluMul, gemv(down)):
- * g = W_gate x, u = W_up x, y = W_down (silu(g) * u), as two launches (gate
- * and up in one grid; the SiLU folded into the down projection's staging).
- * g and u (gate->M values each) are written as the gate and up outputs;
- * unlike the reference's in-place siluMul, g is left as the gate output.
- * down->K must equal gate->M; x, g, u 16-byte aligned. */
+ * u = W_up x, g = silu(W_gate x) * u, y = W_down g.  As in the reference,
+ * whose siluMul works in place on the gate buffer, g holds silu(gate) * up
+ * after the call.  Two launches when gate and up share a format: one grid
+ * whose workgroups each compute the same rows of gate and up and form
+ * silu(g) * u there, then the down projection.  down->K must equal gate->M;
+ * x, g, u 16-byte aligned. */
 int okf_ffn(okf_ctx *ctx, const okf_weight *gate, const okf_weight *up, const okf_weight *down, const float *x,
             float *g, float *u, float *y);
 

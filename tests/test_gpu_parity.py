@@ -438,7 +438,9 @@ def test_gemv_silu_matches_silu_mul_then_matvec(enc, t, M, K, seed):
 # (QwenMetalEngine.swift:918-929); against the oracle's three matvecs.
 FFN = [(Q2_0, Q2_0, Q2_0, 6144, 2048, 1002), (Q4_K, Q4_K, Q4_K, 768, 512, 31), (IQ2_XXS, IQ2_XXS, IQ2_XXS, 512, 1280, 32),
        (Q8_0, Q8_0, Q8_0, 320, 2080, 33), (Q2_0, Q2_0, Q2_0, 256, 1024, 34),
-       (Q4_K, Q4_K, Q8_0, 512, 768, 35)]  # (formats differ)
+       (Q4_K, Q4_K, Q8_0, 512, 768, 35),  # (down's format differs)
+       (Q4_K, Q8_0, Q2_0, 256, 512, 36),  # (gate's and up's formats differ: no pairing)
+       (Q2_0, Q2_0, Q8_0, 224, 1024, 37)]
 
 
 @pytest.mark.parametrize("tg,tu,td,H,D,seed", FFN)
@@ -454,12 +456,30 @@ def test_ffn_matches_oracle(enc, tg, tu, td, H, D, seed):
         enc.sync()
         rg = oracle.matvec(tg, wg, D, H, x)
         ru = oracle.matvec(tu, wu, D, H, x)
-        ry = oracle.matvec(td, wd, H, D, oracle.silu_mul(rg, ru)).astype(np.float64)
-        assert rel(host(g), rg.astype(np.float64)) <= TOL_MV
+        rh = oracle.silu_mul(rg, ru)
+        ry = oracle.matvec(td, wd, H, D, rh).astype(np.float64)
+        # g holds silu(gate) * up after the call (the reference's in-place siluMul)
+        assert rel(host(g), rh.astype(np.float64)) <= TOL_MV
         assert rel(host(u), ru.astype(np.float64)) <= TOL_MV
         r = rel(host(y), ry)
         say("  rel", r)
         assert r <= TOL_MV
+
+
+@pytest.mark.parametrize("tg,tu,H,D,seed", [(Q2_0, Q2_0, 6144, 2048, 51), (Q2_0, Q2_0, 40, 1024, 52),
+                                            (Q4_K, Q4_K, 1000, 768, 53), (IQ2_XXS, IQ2_XXS, 72, 512, 54),
+                                            (Q8_0, Q4_0, 96, 256, 55)])
+def test_gemv_gate_up_matches_oracle(enc, tg, tu, H, D, seed):
+    # gate and up in one grid (rows paired per workgroup, any M), g = silu(gate) * up
+    say("gate_up", NAMES[tg], NAMES[tu], H, D)
+    wg, wu = weights(tg, H, D, seed), weights(tu, H, D, seed + 1)
+    qg, qu = ok.QuantTensor(dev(wg), D, H, tg), ok.QuantTensor(dev(wu), D, H, tu)
+    x = acts(1, D, seed + 2)[0]
+    g, u = (torch.full((H,), float("nan"), device="cuda") for _ in range(2))
+    enc.gemv_gate_up(qg, qu, dev(x), g, u)
+    rg, ru = oracle.matvec(tg, wg, D, H, x), oracle.matvec(tu, wu, D, H, x)
+    assert rel(host(u), ru.astype(np.float64)) <= TOL_MV
+    assert rel(host(g), oracle.silu_mul(rg, ru).astype(np.float64)) <= TOL_MV
 
 
 # ------------------------------------------------------------ parallel group
