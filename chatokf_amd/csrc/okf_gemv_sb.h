@@ -213,9 +213,8 @@ __global__ __launch_bounds__(T) void gemv_sb_kernel(GemvGroup g, uint64_t row_by
     // the first item's loads go right behind the staging's activation loads
     sb_stage_x<NC, SR, SILU>(X, X2, K, tid, T, xs, cs, [&]() { load(tid); });
     __syncthreads();
-    // (the launch sizes RW so that a lane has one item; a second one would be
-    // loaded only after the first is computed: measured, a two-deep register
-    // ring spills at these workgroup sizes)
+    // a lane's next item is requested right after its current one is
+    // consumed (one register buffer; other wavefronts cover the latency)
     for (uint32_t it = tid; it < items; it += T) {
         float o[R][NC];
         const uint32_t row = it / nsb, sb = it - row * nsb;

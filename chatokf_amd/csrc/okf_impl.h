@@ -47,7 +47,6 @@ struct okf_ctx {
     int gemv_sb = -1;    // superblock-per-lane matvec: -1 auto, 0 never, 1 where it fits
     int gemv_sb_rw = 0;  // its rows per workgroup (0 = auto)
     int gemv_sb_t = 0;   // its threads per workgroup (0 = auto)
-    int gemv_sb_r = 0;   // its rows per lane (0 = auto)
     int gemm_ks = 0;     // wide-tile GEMM: K ranges per remainder tile (0 = auto)
     int gemm_thin = 0;   // leftover-tile kernel variant (A/B switch)
     int gemm_ng = 4;     // wide-tile GEMM: N tiles that share an XCD's row blocks
@@ -272,48 +271,53 @@ bool launch_gemv_wide(okf_ctx *c, const GemvCall &call, uint64_t rb, uint32_t K)
     return true;
 }
 
-template <int F, int NC, int R, int T, bool SILU>
+template <int F, int NC, int T, bool SILU>
 void launch_sb_t(okf_ctx *c, const GemvGroup &g, uint32_t total, uint64_t rb, uint32_t K, uint32_t RW, size_t lds,
                  uint32_t sr) {
     auto go = [&](auto src) {
         constexpr int SR = decltype(src)::value;
-        const void *fn = (const void *)gemv_sb_kernel<F, NC, R, T, SR, SILU>;
+        const void *fn = (const void *)gemv_sb_kernel<F, NC, 1, T, SR, SILU>;
         static std::atomic<uint64_t> attr{0};  // devices that have the attribute set
         set_lds_attr(c, fn, attr);
-        hipLaunchKernelGGL((gemv_sb_kernel<F, NC, R, T, SR, SILU>), dim3(total), dim3(T), lds, c->stream, g, rb, K,
+        hipLaunchKernelGGL((gemv_sb_kernel<F, NC, 1, T, SR, SILU>), dim3(total), dim3(T), lds, c->stream, g, rb, K,
                            RW);
     };
+    // (one register buffer: a two-deep ring measured slower at every
+    // workgroup size tried, 15.5 against 13.6 us at 17408 x 5120)
     switch (sr) {
         case 1: go(std::integral_constant<int, 1>{}); break;
         case 2: go(std::integral_constant<int, 2>{}); break;
         case 3: go(std::integral_constant<int, 3>{}); break;
-        default: go(std::integral_constant<int, 5>{}); break;
+        case 4:
+        case 5: go(std::integral_constant<int, 5>{}); break;
+        default: go(std::integral_constant<int, 9>{}); break;
     }
 }
 
-// Superblock-per-lane matvec (gemv_sb_kernel): true when launched.  A
-// workgroup of T = 256 lanes takes RW = T / nsb rows, one superblock per
-// lane.  Measured on MI355X (A/B in one process): Q4_K 17408 x 5120 from
-// 14.8-16.5 us (gemv_kernel) to 13.4-13.9 us; rows of more than 32
-// superblocks stay on the other kernels (5120 x 17408: no gain, and with
-// several superblocks per lane a second item's loads wait for the first
-// item's compute).
+// Superblock-per-lane matvec (gemv_sb_kernel): true when launched.  Short
+// rows (<= 32 superblocks): T = 256 lanes and RW = T / nsb rows, one
+// superblock per lane.  Long rows: T = 512 and RW = M / CUs (one workgroup
+// per CU, each lane a few superblocks), so that the per-workgroup staging of
+// x is shared by more rows.  Measured on MI355X (A/B in one process):
+// Q4_K 17408 x 5120 from 15.7 us (gemv_kernel) to 13.6 us; 5120 x 17408
+// from 17.6 us (gemv_wide_kernel) to 16.4 us.
 template <int F, int NC, bool SILU>
 bool launch_gemv_sb(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32_t K) {
-    if constexpr (!sb_fmt<F>() || NC > 2) {
+    if constexpr (!sb_fmt<F>() || NC > 1) {
         return false;
     } else {
         const uint32_t nsb = K / 256;
-        if (c->gemv_sb == 0 || (c->gemv_sb < 0 && (nsb > 32 || NC > 1))) return false;
-        uint32_t T = c->gemv_sb_t ? (uint32_t)c->gemv_sb_t : 256;
+        if (c->gemv_sb == 0) return false;
+        const bool lng = nsb > 32;
+        uint32_t T = c->gemv_sb_t ? (uint32_t)c->gemv_sb_t : lng ? 512 : 256;
         if (T != 256 && T != 512) T = 256;
         const uint32_t sr = (K / 8 + T - 1) / T;  // staging rounds
-        if (sr > 5 || (NC > 1 && sr > 3)) return false;
-        // two rows per lane only on request (each staged activation read then
-        // serves both; measured no faster)
-        const uint32_t R = c->gemv_sb_r == 2 && NC == 1 ? 2 : 1;
-        uint32_t RW = c->gemv_sb_rw ? (uint32_t)c->gemv_sb_rw : std::max(1u, T / nsb) * R;
-        RW = std::max(R, RW / R * R);
+        if (sr > 9) return false;
+        uint32_t M = 0;
+        for (int i = 0; i < n; i++) M += calls[i].M;
+        const uint32_t RW = c->gemv_sb_rw ? (uint32_t)c->gemv_sb_rw
+                            : lng       ? std::min(32u, std::max(4u, (M + c->cus - 1) / c->cus))
+                                        : std::max(1u, T / nsb);
         const size_t lds = ((size_t)NC * nsb * SB_CHUNKS * 16) + (size_t)RW * nsb * NC * sizeof(float);
         if (lds > c->max_lds) return false;
         GemvGroup g{};
@@ -328,13 +332,8 @@ bool launch_gemv_sb(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint3
             g.end[i] = total;
         }
         g.n = (uint32_t)n;
-        if (R == 2 && NC == 1) {
-            if (T == 256) launch_sb_t<F, NC, 2, 256, SILU>(c, g, total, rb, K, RW, lds, sr);
-            else launch_sb_t<F, NC, 2, 512, SILU>(c, g, total, rb, K, RW, lds, sr);
-        } else {
-            if (T == 256) launch_sb_t<F, NC, 1, 256, SILU>(c, g, total, rb, K, RW, lds, sr);
-            else launch_sb_t<F, NC, 1, 512, SILU>(c, g, total, rb, K, RW, lds, sr);
-        }
+        if (T == 256) launch_sb_t<F, NC, 256, SILU>(c, g, total, rb, K, RW, lds, sr);
+        else launch_sb_t<F, NC, 512, SILU>(c, g, total, rb, K, RW, lds, sr);
         return true;
     }
 }
