@@ -467,6 +467,7 @@ def test_ffn_matches_oracle(enc, tg, tu, td, H, D, seed):
 
 
 @pytest.mark.parametrize("tg,tu,H,D,seed", [(Q2_0, Q2_0, 6144, 2048, 51), (Q2_0, Q2_0, 40, 1024, 52),
+                                            (Q2_0, Q2_0, 45, 384, 56), (Q4_K, Q4_K, 7, 256, 57),
                                             (Q4_K, Q4_K, 1000, 768, 53), (IQ2_XXS, IQ2_XXS, 72, 512, 54),
                                             (Q8_0, Q4_0, 96, 256, 55)])
 def test_gemv_gate_up_matches_oracle(enc, tg, tu, H, D, seed):
@@ -489,7 +490,7 @@ def test_parallel_group_matches_single_calls(enc):
     # equals its single okf_gemv within float reassociation.
     cases = [(Q2_0, 6144, 2048, 1002), (Q2_0, 6144, 2048, 1202), (Q8_0, 300, 2048, 61),
              (Q2_0, 200, 2048, 62), (Q2_0, 130, 1024, 63), (Q2_0, 64, 2048, 64), (Q2_0, 96, 2048, 65),
-             (Q8_0, 40, 2048, 66)]
+             (Q8_0, 40, 2048, 66), (Q4_K, 1000, 2048, 67), (Q4_K, 37, 2048, 68), (Q4_K, 300, 1024, 69)]
     xs = {K: dev(acts(1, K, 70 + K)) for K in (1024, 2048)}
     ws, ys, singles = [], [], []
     for t, M, K, seed in cases:
