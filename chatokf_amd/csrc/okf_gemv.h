@@ -472,12 +472,13 @@ struct Compute<Q4_K, NC, R, TS> {
 
 template <int NC, int R, int TS>
 struct Compute<IQ2_XXS, NC, R, TS> {
-    // tab: [0, 256) grid entries (8 unsigned bytes, .x .y), [256, 384) sign
-    // entries {M.x, M.y, (M & 0x01010101).x, .y} with M = 0xFF per negative
-    // weight (the eighth sign from the parity rule); a weight byte is
-    // (g ^ M) + (M & 1) = +-g, no carry between bytes (g <= 43).  Entry e at
-    // tab[e * TS] (TS = 16: the replicated, conflict-free layout of
-    // gemv_wide_kernel, tab offset by the lane's copy).
+    // tab: [0, 256) grid entries {g.x, g.y, (-g).x, (-g).y} (the 8 values
+    // as bytes, then negated), [256, 384) sign entries {S.x, S.y} of v_perm
+    // selectors: byte j of weight dword k selects j (+g) or j + 4 (-g) by
+    // its sign (the eighth from the parity rule), so one v_perm makes four
+    // signed weight bytes.  Entry e at tab[e * TS] (TS = 16: the
+    // replicated, conflict-free layout of gemv_wide_kernel, tab offset by
+    // the lane's copy).
     template <class XA>
     __device__ __forceinline__ static void run(const Unit<IQ2_XXS, R> &w, const XA &xa, uint32_t,
                                                float (&acc)[R][NC], const u32x4 *tab) {
@@ -494,10 +495,10 @@ struct Compute<IQ2_XXS, NC, R, TS> {
 #pragma unroll
                     for (int e = 0; e < 2; e++) {
                         const int l = 2 * h + e;
-                        const uint2 gv = *(const uint2 *)&tab[((a0 >> (8 * l)) & 0xFF) * TS];
-                        const u32x4 sg = tab[(256 + ((a1 >> (7 * l)) & 127)) * TS];
-                        wv[r][2 * e] = (gv.x ^ sg[0]) + sg[2];
-                        wv[r][2 * e + 1] = (gv.y ^ sg[1]) + sg[3];
+                        const u32x4 gv = tab[((a0 >> (8 * l)) & 0xFF) * TS];
+                        const uint2 sg = *(const uint2 *)&tab[(256 + ((a1 >> (7 * l)) & 127)) * TS];
+                        wv[r][2 * e] = perm(gv[2], gv[0], sg.x);
+                        wv[r][2 * e + 1] = perm(gv[3], gv[1], sg.y);
                     }
                 }
                 dot_half<NC, R>(xa, sb, h, [&](int r, int k) { return wv[r][k]; }, s);

@@ -60,21 +60,27 @@ void build_iq2_tables(uint32_t *t) {
 // negative weight) and M & 0x01010101, {M.lo, M.hi, M1.lo, M1.hi}, so that a
 // signed weight byte is (g ^ M) + M1.
 void build_iq2_tables8(uint32_t *t) {
+    // grid entry e: its 8 values as bytes, then their negations (the dot4
+    // kernels pick each weight's byte from one or the other with v_perm)
     for (int e = 0; e < 256; e++) {
         const uint64_t g = okf_iq2xxs_grid_host[e];
+        uint64_t ng = 0;
+        for (int j = 0; j < 8; j++) ng |= (uint64_t)(uint8_t)(-(int)((g >> (8 * j)) & 0xFF)) << (8 * j);
         t[e * 4 + 0] = (uint32_t)g;
         t[e * 4 + 1] = (uint32_t)(g >> 32);
-        t[e * 4 + 2] = t[e * 4 + 3] = 0;
+        t[e * 4 + 2] = (uint32_t)ng;
+        t[e * 4 + 3] = (uint32_t)(ng >> 32);
     }
+    // sign entry s7: v_perm selectors, byte j of weight dword k is j (the
+    // positive value) or j + 4 (the negated one) for the eighth sign from the
+    // parity rule (ksigns, LLM/Quantize/IQ2Grid.swift:73)
     for (int s7 = 0; s7 < 128; s7++) {
         const uint32_t s = s7 | ((__builtin_popcount(s7) & 1u) << 7);
         uint32_t m[2] = {0, 0};
-        for (int j = 0; j < 8; j++)
-            if ((s >> j) & 1) m[j >> 2] |= 0xFFu << (8 * (j & 3));
+        for (int j = 0; j < 8; j++) m[j >> 2] |= (uint32_t)((j & 3) + 4 * ((s >> j) & 1)) << (8 * (j & 3));
         t[(256 + s7) * 4 + 0] = m[0];
         t[(256 + s7) * 4 + 1] = m[1];
-        t[(256 + s7) * 4 + 2] = m[0] & 0x01010101u;
-        t[(256 + s7) * 4 + 3] = m[1] & 0x01010101u;
+        t[(256 + s7) * 4 + 2] = t[(256 + s7) * 4 + 3] = 0;
     }
 }
 
