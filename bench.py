@@ -310,6 +310,10 @@ def main():
             rd_s = hbm_read_time(wbytes)
             rec["hbm_read_us"] = round(rd_s * 1e6, 3)
             rec["hbm_read_frac"] = round(wbytes / rd_s / HBM_PEAK, 4)
+            # warm: the same call on one weight copy (L2 / MALL resident after the
+            # first call; reported beside, not the measurement)
+            warm_s, _ = time_calls(lambda i: call(0), n_calls, 3)
+            rec["us_warm"] = round(warm_s * 1e6, 3)
         if not args.no_cpu:
             rec.update(cpu_config(name, t, M, K, N, ws_np, X.cpu().numpy(), xs))
         log("bench:", json.dumps(rec))
