@@ -41,20 +41,21 @@ __host__ __device__ constexpr uint32_t unit_weights() {
     return (F == Q8_0 || F == Q4_0 || F == IQ4_NL || grid_fmt(F)) ? 32 : 64;
 }
 // 32-weight groups per unit, and 16-byte LDS chunks per unit (per group:
-// three digit planes of 32 bytes)
+// three digit planes of 32 bytes; for the generic formats, whose weights are
+// fp32 values, the 32 activations as fp32)
 template <int F>
 __host__ __device__ constexpr uint32_t unit_groups() {
     return unit_weights<F>() / 32;
 }
 template <int F>
 __host__ __device__ constexpr uint32_t unit_chunks() {
-    return unit_groups<F>() * 6;
+    return unit_groups<F>() * (grid_fmt(F) ? 8 : 6);
 }
-// bytes of LDS one unit of one column takes: the digit planes and one
-// float4 of group data per group
+// bytes of LDS one unit of one column takes: the chunks and one float4 of
+// group data per group
 template <int F>
 __host__ __device__ constexpr uint32_t unit_lds_bytes() {
-    return unit_groups<F>() * (96 + 16);
+    return unit_groups<F>() * (unit_chunks<F>() / unit_groups<F>() * 16 + 16);
 }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -326,6 +327,20 @@ __device__ __forceinline__ void stage_slot(const float (&v)[NC][8], uint32_t u, 
                                            uint32_t *xs, uint32_t cs, floatx4 *gdp, uint32_t gcs) {
     constexpr uint32_t UG = unit_groups<F>();
     const uint32_t gi = sidx >> 2, k = sidx & 3;
+    if constexpr (grid_fmt(F)) {
+        // the 8 values as they are: chunks 2k, 2k + 1 of group gi hold
+        // values 8k .. 8k + 7 (no group data)
+        if (store)
+#pragma unroll
+            for (int n = 0; n < NC; n++) {
+                uint32_t *d = xs + n * cs;
+                *(floatx4 *)(d + xs_index<F, L>(u, gi * 8 + 2 * k)) = floatx4{v[n][0], v[n][1], v[n][2], v[n][3]};
+                *(floatx4 *)(d + xs_index<F, L>(u, gi * 8 + 2 * k + 1)) = floatx4{v[n][4], v[n][5], v[n][6], v[n][7]};
+            }
+        (void)gdp;
+        (void)gcs;
+        return;
+    }
 #pragma unroll
     for (int n = 0; n < NC; n++) {
         uint2 pl[3];
@@ -401,8 +416,9 @@ struct Compute {
     // The grid formats (IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M), the
     // small K-quants and the plain weights: the 32-weight sub-block is
     // decoded to fp32 with the bit-exact decoder (grid tables from device
-    // memory, tab) and multiplied in fp32 into the staged activations
-    // rebuilt as integers (exact in fp32), scaled once per group.
+    // memory, tab) and multiplied in fp32 into the activations, staged as
+    // fp32 (chunk c of the unit = values 4c .. 4c + 3): one fma a weight,
+    // in order, as the reference's fp32 dot.
     static_assert(grid_fmt(F), "no matvec compute for this format");
     template <class XA>
     __device__ __forceinline__ static void run(const Unit<F, R> &w, const XA &xa, uint32_t u, float (&acc)[R][NC],
@@ -415,21 +431,12 @@ struct Compute {
             for (int n = 0; n < NC; n++) {
                 float a = 0;
 #pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    const u32x4 p0 = xa.chunk(n, chunk_of(0, 0, h));
-                    const u32x4 p1 = xa.chunk(n, chunk_of(0, 1, h));
-                    const u32x4 p2 = xa.chunk(n, chunk_of(0, 2, h));
+                for (int c = 0; c < 8; c++) {
+                    const floatx4 xv = __builtin_bit_cast(floatx4, xa.chunk(n, c));
 #pragma unroll
-                    for (int k = 0; k < 4; k++)
-#pragma unroll
-                        for (int b = 0; b < 4; b++) {
-                            const int X = (__builtin_amdgcn_sbfe((int)p2[k], 8 * b, 8) << 16) +
-                                          (__builtin_amdgcn_sbfe((int)p1[k], 8 * b, 8) << 8) +
-                                          __builtin_amdgcn_sbfe((int)p0[k], 8 * b, 8);
-                            a = fmaf(wv[16 * h + 4 * k + b], (float)X, a);
-                        }
+                    for (int e = 0; e < 4; e++) a = fmaf(wv[4 * c + e], xv[e], a);
                 }
-                acc[r][n] += a * xa.gd(n, 0)[3];
+                acc[r][n] += a;
             }
         }
     }
