@@ -21,6 +21,15 @@ __host__ __device__ constexpr bool grid_fmt(int f) {
 }
 constexpr uint32_t GT_IQ2XS = 0, GT_IQ2S = 4096, GT_IQ3XXS = 12288, GT_IQ3S = 13312, GT_IQ1S = 15360,
                    GT_BYTES = 23552;
+// a grid format's own grid: its offset in that buffer and its size (IQ1_M
+// shares IQ1_S's); 0, 0 for the other formats
+__host__ __device__ constexpr uint32_t gt_off(int f) {
+    return f == IQ2_S ? GT_IQ2S : f == IQ3_XXS ? GT_IQ3XXS : f == IQ3_S ? GT_IQ3S : (f == IQ1_S || f == IQ1_M) ? GT_IQ1S : 0;
+}
+__host__ __device__ constexpr uint32_t gt_bytes(int f) {
+    return f == IQ2_XS ? GT_IQ2S - GT_IQ2XS : f == IQ2_S ? GT_IQ3XXS - GT_IQ2S : f == IQ3_XXS ? GT_IQ3S - GT_IQ3XXS
+         : f == IQ3_S ? GT_IQ1S - GT_IQ3S : (f == IQ1_S || f == IQ1_M) ? GT_BYTES - GT_IQ1S : 0;
+}
 
 // Bytes of one 256-weight span (Q8_0: 8 blocks, Q2_0: 2 blocks), matching the
 // reference's IQArgs.blk (LLM/Base/MetalEnc.swift:162-167).

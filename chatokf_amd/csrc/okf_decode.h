@@ -215,13 +215,13 @@ __device__ __forceinline__ float iq_sign(uint32_t signs, int j, float v) { retur
 // w = sign(db * grid byte j).
 template <bool S>
 __device__ __forceinline__ void decode_unit_iq2_xs_s(const uint8_t *row, uint32_t u, float *w,
-                                                     const uint8_t *gt) {
+                                                     const uint8_t *fg) {
     const uint8_t *b = row + (uint64_t)(u >> 3) * (S ? 82 : 74);
     const uint32_t ib = u & 7;
     const float d = h2f(ldu<uint16_t>(b));
     const uint32_t sc = b[(S ? 74 : 66) + ib];
     const float db0 = d * (0.5f + (float)(sc & 0xF)) * 0.25f, db1 = d * (0.5f + (float)(sc >> 4)) * 0.25f;
-    const uint64_t *grid = (const uint64_t *)(gt + (S ? GT_IQ2S : GT_IQ2XS));
+    const uint64_t *grid = (const uint64_t *)fg;
 #pragma unroll
     for (int l = 0; l < 4; l++) {
         uint64_t e;
@@ -243,11 +243,11 @@ __device__ __forceinline__ void decode_unit_iq2_xs_s(const uint8_t *row, uint32_
 
 // IQX.iq3XXS / IQX.iq3S (LLM/Quantize/IQ3.swift:60-115), sub-block ib = u & 7.
 template <bool S>
-__device__ __forceinline__ void decode_unit_iq3(const uint8_t *row, uint32_t u, float *w, const uint8_t *gt) {
+__device__ __forceinline__ void decode_unit_iq3(const uint8_t *row, uint32_t u, float *w, const uint8_t *fg) {
     const uint8_t *b = row + (uint64_t)(u >> 3) * (S ? 110 : 98);
     const uint32_t ib = u & 7;
     const float d = h2f(ldu<uint16_t>(b));
-    const uint32_t *grid = (const uint32_t *)(gt + (S ? GT_IQ3S : GT_IQ3XXS));
+    const uint32_t *grid = (const uint32_t *)fg;
     float db;
     uint32_t aux = 0, qh = 0;
     if constexpr (S) {
@@ -283,10 +283,10 @@ __device__ __forceinline__ void decode_unit_iq3(const uint8_t *row, uint32_t u, 
 // (LLM/Quantize/IQ2XXS.swift:63-98), sub-block ib = u & 7: w = dl (n - 1 +
 // delta) with the grid's ternary digit n at bit 8 (j % 4) + 4 (j / 4).
 template <bool M>
-__device__ __forceinline__ void decode_unit_iq1(const uint8_t *row, uint32_t u, float *w, const uint8_t *gt) {
+__device__ __forceinline__ void decode_unit_iq1(const uint8_t *row, uint32_t u, float *w, const uint8_t *fg) {
     const uint8_t *b = row + (uint64_t)(u >> 3) * (M ? 56 : 50);
     const uint32_t ib = u & 7;
-    const uint32_t *grid = (const uint32_t *)(gt + GT_IQ1S);
+    const uint32_t *grid = (const uint32_t *)fg;
     float dls[2];
     uint32_t hb[4], neg[4];
     const uint8_t *qs;
@@ -402,6 +402,15 @@ __device__ __forceinline__ void decode_unit_dense(const uint8_t *row, uint32_t u
     }
 }
 
+// The grid formats' decoders take fg, the format's own grid (gt_off<F>()
+// bytes into the buffer of all the grids, or a copy of it in LDS).
+template <int F>
+__device__ __forceinline__ void decode_unit_fg(const uint8_t *row, uint32_t u, float *w, const uint8_t *fg) {
+    if constexpr (F == IQ2_XS || F == IQ2_S) decode_unit_iq2_xs_s<F == IQ2_S>(row, u, w, fg);
+    else if constexpr (F == IQ3_XXS || F == IQ3_S) decode_unit_iq3<F == IQ3_S>(row, u, w, fg);
+    else if constexpr (F == IQ1_S || F == IQ1_M) decode_unit_iq1<F == IQ1_M>(row, u, w, fg);
+}
+
 // gt: the grid tables of the grid formats (GT_* offsets), in device memory
 template <int F>
 __device__ __forceinline__ void decode_unit(const uint8_t *row, uint32_t u, float *w,
@@ -414,9 +423,8 @@ __device__ __forceinline__ void decode_unit(const uint8_t *row, uint32_t u, floa
     else if constexpr (F == Q5_K) decode_unit_q5_k(row, u, w);
     else if constexpr (F == Q6_K) decode_unit_q6_k(row, u, w);
     else if constexpr (F == IQ4_XS) decode_unit_iq4_xs(row, u, w);
-    else if constexpr (F == IQ2_XS || F == IQ2_S) decode_unit_iq2_xs_s<F == IQ2_S>(row, u, w, gt);
-    else if constexpr (F == IQ3_XXS || F == IQ3_S) decode_unit_iq3<F == IQ3_S>(row, u, w, gt);
-    else if constexpr (F == IQ1_S || F == IQ1_M) decode_unit_iq1<F == IQ1_M>(row, u, w, gt);
+    else if constexpr (F == IQ2_XS || F == IQ2_S || F == IQ3_XXS || F == IQ3_S || F == IQ1_S || F == IQ1_M)
+        decode_unit_fg<F>(row, u, w, gt + gt_off(F));
     else if constexpr (F == Q2_K) decode_unit_q2_k(row, u, w);
     else if constexpr (F == Q3_K) decode_unit_q3_k(row, u, w);
     else if constexpr (F == F32 || F == F16 || F == BF16) decode_unit_dense<F>(row, u, w);

@@ -58,6 +58,15 @@ __host__ __device__ constexpr uint32_t unit_lds_bytes() {
     return unit_groups<F>() * (unit_chunks<F>() / unit_groups<F>() * 16 + 16);
 }
 
+// 16-byte LDS rows of tables gemv_kernel copies per workgroup: IQ2_XXS's
+// int8 grid and sign rows, a grid format's own grid (IQ1_S / IQ1_M read
+// their 8 KB grid from device memory: the copy measured 1-2 us slower at
+// 17408 x 5120, where it took IQ3_XXS from 31.6 to 24.6 us)
+template <int F>
+__host__ __device__ constexpr uint32_t gemv_tab_rows() {
+    return F == IQ2_XXS ? 384 : (F == IQ1_S || F == IQ1_M) ? 0 : gt_bytes(F) / 16;
+}
+
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // v_perm_b32: byte k of the result is byte sel_k of the 8-byte value {hi, lo}
@@ -415,8 +424,9 @@ template <int F, int NC, int R, int TS = 1>
 struct Compute {
     // The grid formats (IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M), the
     // small K-quants and the plain weights: the 32-weight sub-block is
-    // decoded to fp32 with the bit-exact decoder (grid tables from device
-    // memory, tab) and multiplied in fp32 into the activations, staged as
+    // decoded to fp32 with the bit-exact decoder (the format's grid from its
+    // copy in LDS, or for IQ1_S / IQ1_M all the grids in device memory: tab)
+    // and multiplied in fp32 into the activations, staged as
     // fp32 (chunk c of the unit = values 4c .. 4c + 3): one fma a weight,
     // in order, as the reference's fp32 dot.
     static_assert(grid_fmt(F), "no matvec compute for this format");
@@ -426,7 +436,8 @@ struct Compute {
 #pragma unroll
         for (int r = 0; r < R; r++) {
             float wv[32];
-            decode_unit<F>(w.row[r], u, wv, nullptr, (const uint8_t *)tab);
+            if constexpr (gemv_tab_rows<F>() > 0) decode_unit_fg<F>(w.row[r], u, wv, (const uint8_t *)tab);
+            else decode_unit<F>(w.row[r], u, wv, nullptr, (const uint8_t *)tab);
 #pragma unroll
             for (int n = 0; n < NC; n++) {
                 float a = 0;
@@ -852,15 +863,15 @@ __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ W, uint64_
                                           float *__restrict__ Y2 = nullptr) {
     constexpr int L = GV_L;
     extern __shared__ u32x4 lds[];
-    constexpr uint32_t TAB = F == IQ2_XXS ? 384 : 0;
+    constexpr uint32_t TAB = gemv_tab_rows<F>();
     u32x4 *tab = lds;
     uint32_t *xs = (uint32_t *)(lds + TAB);
     const uint32_t tid = threadIdx.x, nthr = blockDim.x;
     const uint32_t lane = tid & 63, i = lane % L, slot = lane / L;
     const uint32_t wave = tid >> 6, waves = nthr >> 6;
     const uint32_t part = wave % S, group = wave / S, groups = waves / S;
-    if constexpr (F == IQ2_XXS)
-        for (uint32_t e = tid; e < TAB; e += nthr) tab[e] = tab_g[e];
+    if constexpr (TAB > 0)
+        for (uint32_t e = tid; e < TAB; e += nthr) tab[e] = tab_g[gt_off(F) / 16 + e];
 
     // row slot q of the workgroup; paired: q < QH takes W, q >= QH W2
     const bool pair = W2 != nullptr;
@@ -926,7 +937,7 @@ __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ W, uint64_
                 const uint32_t u = i + L * (part + S * (t + j));
                 if (u < cn)
                     Compute<F, NC, R>::run(buf[j], XLds{xs + xs_index<F, L>(u, 0), 4 * L, cs, gdp + u * UG, gcs},
-                                           c0 + u, acc, grid_fmt(F) ? tab_g : tab);
+                                           c0 + u, acc, TAB > 0 ? tab : tab_g);
                 load_unit<F, R>(rows, c0 + min(u + L * S * D, last), buf[j]);
             }
         }
@@ -935,7 +946,7 @@ __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ W, uint64_
             const uint32_t u = i + L * (part + S * (t + j));
             if (u < cn)
                 Compute<F, NC, R>::run(buf[j], XLds{xs + xs_index<F, L>(u, 0), 4 * L, cs, gdp + u * UG, gcs},
-                                       c0 + u, acc, grid_fmt(F) ? tab_g : tab);
+                                       c0 + u, acc, TAB > 0 ? tab : tab_g);
         }
     }
     // reduce: over the slot's lanes, then (S > 1) over the parts in LDS

@@ -348,7 +348,7 @@ void launch_gemv_nc(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint3
                   !grid_fmt(F))
         if (n == 1 && launch_gemv_wide<F, NC>(c, calls[0], rb, K)) return;
     constexpr uint32_t UW = unit_weights<F>();
-    const size_t tab = F == IQ2_XXS ? 384 * 16 : 0;
+    const size_t tab = gemv_tab_rows<F>() * 16;
     const uint32_t units = K / UW;
     // stage all of x when it fits, else in chunks of 64-unit groups (per
     // 32 weights: three 32-byte digit planes and a float4 of group data)
@@ -389,7 +389,7 @@ void launch_gemv(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32_t
 template <int F>
 void launch_gemv_pair(okf_ctx *c, const GemvCall *calls, uint64_t rb, uint32_t K) {
     constexpr uint32_t UW = unit_weights<F>();
-    const size_t tab = F == IQ2_XXS ? 384 * 16 : 0;
+    const size_t tab = gemv_tab_rows<F>() * 16;
     const uint32_t units = K / UW;
     const size_t per_unit = unit_lds_bytes<F>();
     const size_t red = 4 * GV_SLOTS * 4 * sizeof(float);
