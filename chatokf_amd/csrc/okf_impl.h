@@ -153,11 +153,13 @@ void launch_gemv_s(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32
         if (steps >= 3) return launch_gemv_s<F, NC, S, SILU, 3>(c, calls, n, rb, K, cunits, lds, pair);
     }
     // two rows per slot (each staged activation read serves both) where
-    // measured faster: IQ2_XXS with 1..5 columns (16.9 -> 16.4 us at one), Q4_K
-    // and Q2_0 with 5.  (A
+    // measured faster: IQ2_XXS with 1..5 columns (16.9 -> 16.4 us at one), the
+    // generic formats with 2..5 (17408 x 5120, N = 4: 15-18 % faster; at one
+    // column 10-25 % slower), Q4_K and Q2_0 with 5.  (A
     // three-deep ring for the Q4_K matvec measured 3-4 % slower than two
     // once the weight loads were issued behind the staging's.)
-    constexpr int R = ((F == IQ2_XXS && NC >= 1) || (NC == 5 && F != Q8_0 && F != Q5_K && F != Q6_K && F != IQ4_XS && !grid_fmt(F))) ? 2 : 1,
+    constexpr int R = ((F == IQ2_XXS && NC >= 1) || (grid_fmt(F) && NC >= 2) ||
+                       (NC == 5 && F != Q8_0 && F != Q5_K && F != Q6_K && F != IQ4_XS)) ? 2 : 1,
                   D = DX ? DX : 2, WAVES = 4;
     const void *fn = (const void *)gemv_kernel<F, NC, R, D, S, SILU>;
     static std::atomic<uint64_t> attr{0};  // devices that have the attribute set
