@@ -19,6 +19,9 @@ __host__ __device__ constexpr bool grid_fmt(int f) {
     return f == IQ2_XS || f == IQ2_S || f == IQ3_XXS || f == IQ3_S || f == IQ1_S || f == IQ1_M || f == Q2_K ||
            f == Q3_K || f == F32 || f == F16 || f == BF16;
 }
+// The formats the matvec takes through that generic compute: all of them but
+// IQ3_XXS, which has an integer compute of its own
+__host__ __device__ constexpr bool gen_fmt(int f) { return grid_fmt(f) && f != IQ3_XXS; }
 constexpr uint32_t GT_IQ2XS = 0, GT_IQ2S = 4096, GT_IQ3XXS = 12288, GT_IQ3S = 13312, GT_IQ1S = 15360,
                    GT_BYTES = 23552;
 // a grid format's own grid: its offset in that buffer and its size (IQ1_M

@@ -38,7 +38,7 @@ namespace okf {
 // any K that is a whole number of blocks works).
 template <int F>
 __host__ __device__ constexpr uint32_t unit_weights() {
-    return (F == Q8_0 || F == Q4_0 || F == IQ4_NL || grid_fmt(F)) ? 32 : 64;
+    return (F == Q8_0 || F == Q4_0 || F == IQ4_NL || gen_fmt(F)) ? 32 : 64;
 }
 // 32-weight groups per unit, and 16-byte LDS chunks per unit (per group:
 // three digit planes of 32 bytes; for the generic formats, whose weights are
@@ -49,7 +49,7 @@ __host__ __device__ constexpr uint32_t unit_groups() {
 }
 template <int F>
 __host__ __device__ constexpr uint32_t unit_chunks() {
-    return unit_groups<F>() * (grid_fmt(F) ? 8 : 6);
+    return unit_groups<F>() * (gen_fmt(F) ? 8 : 6);
 }
 // bytes of LDS one unit of one column takes: the chunks and one float4 of
 // group data per group
@@ -64,7 +64,7 @@ __host__ __device__ constexpr uint32_t unit_lds_bytes() {
 // 17408 x 5120, where it took IQ3_XXS from 31.6 to 24.6 us)
 template <int F>
 __host__ __device__ constexpr uint32_t gemv_tab_rows() {
-    return F == IQ2_XXS ? 384 : (F == IQ1_S || F == IQ1_M) ? 0 : gt_bytes(F) / 16;
+    return F == IQ2_XXS ? 384 : F == IQ3_XXS ? 192 : (F == IQ1_S || F == IQ1_M) ? 0 : gt_bytes(F) / 16;
 }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -82,7 +82,7 @@ __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
 
 // ---------------------------------------------------------------- units --
 // Raw bytes of one unit for R rows (native vector types keep them in VGPRs).
-// The grid formats (grid_fmt) keep only the row: their compute decodes a
+// The generic formats (gen_fmt) keep only the row: their compute decodes a
 // 32-weight sub-block with the bit-exact decoder.
 template <int F, int R>
 struct Unit {
@@ -96,6 +96,12 @@ template <int R>
 struct Unit<IQ2_XXS, R> {  // d + two sub-blocks (a0, a1, a0', a1')
     uint32_t d[R];
     u32x4 a[R];
+};
+template <int R>
+struct Unit<IQ3_XXS, R> {  // d, the two sub-blocks' 16 grid indices and their two scale-and-sign words
+    uint32_t d[R];
+    u32x4 q[R];
+    uint2 aux[R];
 };
 template <int R>
 struct Unit<Q8_0, R> {  // one block: d + 32 code bytes (2-byte aligned)
@@ -175,7 +181,13 @@ __device__ __forceinline__ void load_unit(const uint8_t *const rows[R], uint32_t
             w.hdr[r] = ldu<uint2>(b);
             w.q0[r] = ldu<u32x4>(b + 8 + g * 32);
             w.q1[r] = ldu<u32x4>(b + 24 + g * 32);
-        } else if constexpr (grid_fmt(F)) {
+        } else if constexpr (F == IQ3_XXS) {  // unit = sub-blocks 2g, 2g + 1 of superblock u >> 2
+            const uint8_t *b = rows[r] + (uint64_t)(u >> 2) * 98;
+            const uint32_t g = u & 3;
+            w.d[r] = ldu<uint16_t>(b);
+            w.q[r] = ldu<u32x4>(b + 2 + g * 16);
+            w.aux[r] = ldu<uint2>(b + 66 + g * 8);
+        } else if constexpr (gen_fmt(F)) {
             w.row[r] = rows[r];
         } else if constexpr (F == Q4_0 || F == IQ4_NL) {
             const uint8_t *b = rows[r] + (uint64_t)u * 18;
@@ -336,7 +348,7 @@ __device__ __forceinline__ void stage_slot(const float (&v)[NC][8], uint32_t u, 
                                            uint32_t *xs, uint32_t cs, floatx4 *gdp, uint32_t gcs) {
     constexpr uint32_t UG = unit_groups<F>();
     const uint32_t gi = sidx >> 2, k = sidx & 3;
-    if constexpr (grid_fmt(F)) {
+    if constexpr (gen_fmt(F)) {
         // the 8 values as they are: chunks 2k, 2k + 1 of group gi hold
         // values 8k .. 8k + 7 (no group data)
         if (store)
@@ -429,15 +441,15 @@ struct Compute {
     // and multiplied in fp32 into the activations, staged as
     // fp32 (chunk c of the unit = values 4c .. 4c + 3): one fma a weight,
     // in order, as the reference's fp32 dot.
-    static_assert(grid_fmt(F), "no matvec compute for this format");
+    static_assert(gen_fmt(F), "no matvec compute for this format");
     template <class XA>
     __device__ __forceinline__ static void run(const Unit<F, R> &w, const XA &xa, uint32_t u, float (&acc)[R][NC],
                                                const u32x4 *tab) {
 #pragma unroll
         for (int r = 0; r < R; r++) {
             float wv[32];
-            if constexpr (gemv_tab_rows<F>() > 0) decode_unit_fg<F>(w.row[r], u, wv, (const uint8_t *)tab);
-            else decode_unit<F>(w.row[r], u, wv, nullptr, (const uint8_t *)tab);
+            if constexpr (gt_bytes(F) > 0) decode_unit_fg<F>(w.row[r], u, wv, (const uint8_t *)tab);
+            else decode_unit<F>(w.row[r], u, wv, nullptr);
 #pragma unroll
             for (int n = 0; n < NC; n++) {
                 float a = 0;
@@ -525,6 +537,51 @@ struct Compute<IQ2_XXS, NC, R, TS> {
             for (int r = 0; r < R; r++) {
                 const uint32_t a1 = w.a[r][2 * sb + 1];
                 const float db = h2f(w.d[r]) * (0.5f + (float)(a1 >> 28)) * 0.25f;
+#pragma unroll
+                for (int n = 0; n < NC; n++) acc[r][n] += db * (comb(s, r, n) * xa.gd(n, sb)[3]);
+            }
+        }
+    }
+};
+
+template <int NC, int R, int TS>
+struct Compute<IQ3_XXS, NC, R, TS> {
+    // IQX.iq3XXS (LLM/Quantize/IQ3.swift:60-86) as integer dot products:
+    // weight = db * sign * grid byte, db = d (0.5 + aux >> 28) / 2 per
+    // 32-weight sub-block, where the grid bytes (4..62) and their signs fit
+    // int8.  tab (as 8-byte entries): [0, 256) grid entry e's 4 bytes, then
+    // their negations; [256, 384) the v_perm selectors of a 7-bit sign
+    // index (byte j selects the positive or the negated byte, eighth sign
+    // from the parity rule).
+    template <class XA>
+    __device__ __forceinline__ static void run(const Unit<IQ3_XXS, R> &w, const XA &xa, uint32_t,
+                                               float (&acc)[R][NC], const u32x4 *tab) {
+        const uint2 *t2 = (const uint2 *)tab;
+#pragma unroll
+        for (int sb = 0; sb < 2; sb++) {
+            int s[3][R][NC];
+            zero3(s);
+#pragma unroll
+            for (int h = 0; h < 2; h++) {  // index pairs 2h, 2h + 1 = plane dwords 4h .. 4h + 3
+                uint32_t wv[R][4];
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const uint32_t qd = w.q[r][2 * sb + h], aux = sb ? w.aux[r].y : w.aux[r].x;
+#pragma unroll
+                    for (int e = 0; e < 2; e++) {
+                        const int l = 2 * h + e;
+                        const uint2 g1 = t2[(qd >> (16 * e)) & 0xFF], g2 = t2[(qd >> (16 * e + 8)) & 0xFF];
+                        const uint2 sg = t2[256 + ((aux >> (7 * l)) & 127)];
+                        wv[r][2 * e] = perm(g1.y, g1.x, sg.x);
+                        wv[r][2 * e + 1] = perm(g2.y, g2.x, sg.y);
+                    }
+                }
+                dot_half<NC, R>(xa, sb, h, [&](int r, int k) { return wv[r][k]; }, s);
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const uint32_t aux = sb ? w.aux[r].y : w.aux[r].x;
+                const float db = h2f(w.d[r]) * (0.5f + (float)(aux >> 28)) * 0.5f;
 #pragma unroll
                 for (int n = 0; n < NC; n++) acc[r][n] += db * (comb(s, r, n) * xa.gd(n, sb)[3]);
             }
@@ -871,7 +928,7 @@ __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ W, uint64_
     const uint32_t wave = tid >> 6, waves = nthr >> 6;
     const uint32_t part = wave % S, group = wave / S, groups = waves / S;
     if constexpr (TAB > 0)
-        for (uint32_t e = tid; e < TAB; e += nthr) tab[e] = tab_g[gt_off(F) / 16 + e];
+        for (uint32_t e = tid; e < TAB; e += nthr) tab[e] = tab_g[e];
 
     // row slot q of the workgroup; paired: q < QH takes W, q >= QH W2
     const bool pair = W2 != nullptr;

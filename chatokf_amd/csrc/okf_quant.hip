@@ -84,6 +84,24 @@ void build_iq2_tables8(uint32_t *t) {
     }
 }
 
+// IQ3_XXS's tables for its integer matvec, 8-byte entries: [0, 256) grid
+// entry e's 4 bytes (LLM/Quantize/IQ3Grid.swift), then their negations;
+// [256, 384) the first 8 bytes of IQ2_XXS's sign selector rows (sel8, 16
+// bytes a row): a 7-bit sign index gives the same 8 signs.
+void build_iq3_xxs_tables8(uint32_t *t, const uint32_t *sel8) {
+    for (int e = 0; e < 256; e++) {
+        const uint32_t g = okf_host_iq3xxs_grid[e];
+        uint32_t ng = 0;
+        for (int j = 0; j < 4; j++) ng |= (uint32_t)(uint8_t)(-(int)((g >> (8 * j)) & 0xFF)) << (8 * j);
+        t[2 * e] = g;
+        t[2 * e + 1] = ng;
+    }
+    for (int s7 = 0; s7 < 128; s7++) {
+        t[2 * (256 + s7)] = sel8[4 * s7];
+        t[2 * (256 + s7) + 1] = sel8[4 * s7 + 1];
+    }
+}
+
 #define OKF_DISPATCH(type, fn, ...)                         \
     switch (type) {                                         \
     case Q8_0: fn<Q8_0>(__VA_ARGS__); break;                \
@@ -223,9 +241,11 @@ int okf_ctx_create(int device, okf_ctx **out) {
         build_iq2_tables(tabh);
         if (e == hipSuccess) e = hipMalloc((void **)&c->tab, sizeof(tabh));
         if (e == hipSuccess) e = hipMemcpy(c->tab, tabh, sizeof(tabh), hipMemcpyHostToDevice);
-        build_iq2_tables8(tabh);
-        if (e == hipSuccess) e = hipMalloc((void **)&c->tab8, sizeof(tabh));
-        if (e == hipSuccess) e = hipMemcpy(c->tab8, tabh, sizeof(tabh), hipMemcpyHostToDevice);
+        uint32_t tab8h[(384 + 192) * 4];
+        build_iq2_tables8(tab8h);
+        build_iq3_xxs_tables8(tab8h + 384 * 4, tab8h + 256 * 4);
+        if (e == hipSuccess) e = hipMalloc((void **)&c->tab8, sizeof(tab8h));
+        if (e == hipSuccess) e = hipMemcpy(c->tab8, tab8h, sizeof(tab8h), hipMemcpyHostToDevice);
         if (e != hipSuccess) {
             if (c->grid) (void)hipFree(c->grid);
             if (c->grids) (void)hipFree(c->grids);
