@@ -64,7 +64,7 @@ __host__ __device__ constexpr uint32_t unit_lds_bytes() {
 // 17408 x 5120, where it took IQ3_XXS from 31.6 to 24.6 us)
 template <int F>
 __host__ __device__ constexpr uint32_t gemv_tab_rows() {
-    return F == IQ2_XXS ? 384 : F == IQ3_XXS ? 192 : (F == IQ1_S || F == IQ1_M) ? 0 : gt_bytes(F) / 16;
+    return F == IQ2_XXS ? 384 : itab_rows(F) ? itab_rows(F) : (F == IQ1_S || F == IQ1_M) ? 0 : gt_bytes(F) / 16;
 }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -96,6 +96,22 @@ template <int R>
 struct Unit<IQ2_XXS, R> {  // d + two sub-blocks (a0, a1, a0', a1')
     uint32_t d[R];
     u32x4 a[R];
+};
+template <int R>
+struct Unit<IQ3_S, R> {  // d, 16 grid index bytes, their high bits, 8 sign bytes, the scale byte
+    uint32_t d[R], qh[R], sc[R];
+    u32x4 q[R];
+    uint2 sg[R];
+};
+template <int R>
+struct Unit<IQ2_XS, R> {  // d, 8 16-bit index+sign words, 2 scale bytes
+    uint32_t d[R], sc[R];
+    u32x4 q[R];
+};
+template <int R>
+struct Unit<IQ2_S, R> {  // d, 8 index bytes, 8 sign bytes, 2 high-bit bytes, 2 scale bytes
+    uint32_t d[R], qh[R], sc[R];
+    uint2 q[R], sg[R];
 };
 template <int R>
 struct Unit<IQ3_XXS, R> {  // d, the two sub-blocks' 16 grid indices and their two scale-and-sign words
@@ -187,6 +203,28 @@ __device__ __forceinline__ void load_unit(const uint8_t *const rows[R], uint32_t
             w.d[r] = ldu<uint16_t>(b);
             w.q[r] = ldu<u32x4>(b + 2 + g * 16);
             w.aux[r] = ldu<uint2>(b + 66 + g * 8);
+        } else if constexpr (F == IQ3_S) {  // unit = sub-blocks 2g, 2g + 1
+            const uint8_t *b = rows[r] + (uint64_t)(u >> 2) * 110;
+            const uint32_t g = u & 3;
+            w.d[r] = ldu<uint16_t>(b);
+            w.q[r] = ldu<u32x4>(b + 2 + g * 16);
+            w.qh[r] = ldu<uint16_t>(b + 66 + g * 2);
+            w.sg[r] = ldu<uint2>(b + 74 + g * 8);
+            w.sc[r] = b[106 + g];
+        } else if constexpr (F == IQ2_XS) {
+            const uint8_t *b = rows[r] + (uint64_t)(u >> 2) * 74;
+            const uint32_t g = u & 3;
+            w.d[r] = ldu<uint16_t>(b);
+            w.q[r] = ldu<u32x4>(b + 2 + g * 16);
+            w.sc[r] = ldu<uint16_t>(b + 66 + g * 2);
+        } else if constexpr (F == IQ2_S) {
+            const uint8_t *b = rows[r] + (uint64_t)(u >> 2) * 82;
+            const uint32_t g = u & 3;
+            w.d[r] = ldu<uint16_t>(b);
+            w.q[r] = ldu<uint2>(b + 2 + g * 8);
+            w.sg[r] = ldu<uint2>(b + 34 + g * 8);
+            w.qh[r] = ldu<uint16_t>(b + 66 + g * 2);
+            w.sc[r] = ldu<uint16_t>(b + 74 + g * 2);
         } else if constexpr (gen_fmt(F)) {
             w.row[r] = rows[r];
         } else if constexpr (F == Q4_0 || F == IQ4_NL) {
@@ -586,6 +624,118 @@ struct Compute<IQ3_XXS, NC, R, TS> {
                 for (int n = 0; n < NC; n++) acc[r][n] += db * (comb(s, r, n) * xa.gd(n, sb)[3]);
             }
         }
+    }
+};
+
+template <int NC, int R, int TS>
+struct Compute<IQ3_S, NC, R, TS> {
+    // IQX.iq3S (LLM/Quantize/IQ3.swift:88-115) as integer dot products:
+    // weight = d (1 + 2 sc) * sign * grid byte (1..15) per 32-weight
+    // sub-block.  tab (8-byte entries): [0, 512) grid entry e's 4 bytes and
+    // their negations; [512, 768) the v_perm selectors of a sign byte.
+    template <class XA>
+    __device__ __forceinline__ static void run(const Unit<IQ3_S, R> &w, const XA &xa, uint32_t,
+                                               float (&acc)[R][NC], const u32x4 *tab) {
+        const uint2 *t2 = (const uint2 *)tab;
+#pragma unroll
+        for (int sb = 0; sb < 2; sb++) {
+            int s[3][R][NC];
+            zero3(s);
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                uint32_t wv[R][4];
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const uint32_t qd = w.q[r][2 * sb + h], qh = (w.qh[r] >> (8 * sb)) & 0xFF;
+                    const uint32_t sgd = sb ? w.sg[r].y : w.sg[r].x;
+#pragma unroll
+                    for (int e = 0; e < 2; e++) {
+                        const int l = 2 * h + e;
+                        const uint32_t i1 = ((qd >> (16 * e)) & 0xFF) | ((qh << (8 - 2 * l)) & 256);
+                        const uint32_t i2 = ((qd >> (16 * e + 8)) & 0xFF) | ((qh << (7 - 2 * l)) & 256);
+                        const uint2 g1 = t2[i1], g2 = t2[i2], sg = t2[512 + ((sgd >> (8 * l)) & 0xFF)];
+                        wv[r][2 * e] = perm(g1.y, g1.x, sg.x);
+                        wv[r][2 * e + 1] = perm(g2.y, g2.x, sg.y);
+                    }
+                }
+                dot_half<NC, R>(xa, sb, h, [&](int r, int k) { return wv[r][k]; }, s);
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const float db = h2f(w.d[r]) * (float)(1 + 2 * ((w.sc[r] >> (4 * sb)) & 0xF));
+#pragma unroll
+                for (int n = 0; n < NC; n++) acc[r][n] += db * (comb(s, r, n) * xa.gd(n, sb)[3]);
+            }
+        }
+    }
+};
+
+// IQX.iq2XS / IQX.iq2S (LLM/Quantize/IQ3.swift:14-57) as integer dot
+// products: weight = d (0.5 + nibble) / 4 * sign * grid byte (8, 25, 43),
+// one scale nibble per 16 weights.  tab: [0, G) grid entry e as 16 bytes (8
+// values, then their negations), then 8-byte v_perm selectors: of a 7-bit
+// sign index (IQ2_XS, eighth sign from the parity rule) or of a sign byte
+// (IQ2_S).
+template <int F, int NC, int R, int TS>
+struct ComputeIQ2XS {
+    static constexpr uint32_t G = F == IQ2_S ? 1024 : 512;
+    template <class XA>
+    __device__ __forceinline__ static void run(const Unit<F, R> &w, const XA &xa, float (&acc)[R][NC],
+                                               const u32x4 *tab) {
+        const uint2 *sel = (const uint2 *)(tab + G);
+#pragma unroll
+        for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {  // 16 weights, one scale nibble
+                int s[3][R][NC];
+                zero3(s);
+                uint32_t wv[R][4];
+#pragma unroll
+                for (int r = 0; r < R; r++)
+#pragma unroll
+                    for (int e = 0; e < 2; e++) {
+                        const int l = 2 * h + e;
+                        uint32_t idx, sv;
+                        if constexpr (F == IQ2_S) {
+                            const uint32_t qd = sb ? w.q[r].y : w.q[r].x, sgd = sb ? w.sg[r].y : w.sg[r].x;
+                            const uint32_t qh = (w.qh[r] >> (8 * sb)) & 0xFF;
+                            idx = ((qd >> (8 * l)) & 0xFF) | ((qh << (8 - 2 * l)) & 0x300);
+                            sv = (sgd >> (8 * l)) & 0xFF;
+                        } else {
+                            const uint32_t q16 = (w.q[r][2 * sb + h] >> (16 * e)) & 0xFFFF;
+                            idx = q16 & 511;
+                            sv = q16 >> 9;
+                        }
+                        const u32x4 gv = tab[idx];
+                        const uint2 sg = sel[sv];
+                        wv[r][2 * e] = perm(gv[2], gv[0], sg.x);
+                        wv[r][2 * e + 1] = perm(gv[3], gv[1], sg.y);
+                    }
+                dot_half<NC, R>(xa, sb, h, [&](int r, int k) { return wv[r][k]; }, s);
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const uint32_t nib = (w.sc[r] >> (8 * sb + 4 * h)) & 0xF;
+                    const float db = h2f(w.d[r]) * (0.5f + (float)nib) * 0.25f;
+#pragma unroll
+                    for (int n = 0; n < NC; n++) acc[r][n] += db * (comb(s, r, n) * xa.gd(n, sb)[3]);
+                }
+            }
+    }
+};
+template <int NC, int R, int TS>
+struct Compute<IQ2_XS, NC, R, TS> {
+    template <class XA>
+    __device__ __forceinline__ static void run(const Unit<IQ2_XS, R> &w, const XA &xa, uint32_t,
+                                               float (&acc)[R][NC], const u32x4 *tab) {
+        ComputeIQ2XS<IQ2_XS, NC, R, TS>::run(w, xa, acc, tab);
+    }
+};
+template <int NC, int R, int TS>
+struct Compute<IQ2_S, NC, R, TS> {
+    template <class XA>
+    __device__ __forceinline__ static void run(const Unit<IQ2_S, R> &w, const XA &xa, uint32_t,
+                                               float (&acc)[R][NC], const u32x4 *tab) {
+        ComputeIQ2XS<IQ2_S, NC, R, TS>::run(w, xa, acc, tab);
     }
 };
 

@@ -102,6 +102,51 @@ void build_iq3_xxs_tables8(uint32_t *t, const uint32_t *sel8) {
     }
 }
 
+// v_perm selectors of an 8-bit sign byte (bit j negates weight j): byte j of
+// dword j / 4 is j % 4 or j % 4 + 4
+static void sign_byte_selectors(uint32_t s, uint32_t *m) {
+    m[0] = m[1] = 0;
+    for (int j = 0; j < 8; j++) m[j >> 2] |= (uint32_t)((j & 3) + 4 * ((s >> j) & 1)) << (8 * (j & 3));
+}
+
+// IQ3_S's tables, 8-byte entries: [0, 512) grid entry e's 4 bytes
+// (LLM/Quantize/IQ3Grid.swift), then their negations; [512, 768) the
+// selectors of a sign byte.
+void build_iq3_s_tables8(uint32_t *t) {
+    for (int e = 0; e < 512; e++) {
+        const uint32_t g = okf_host_iq3s_grid[e];
+        uint32_t ng = 0;
+        for (int j = 0; j < 4; j++) ng |= (uint32_t)(uint8_t)(-(int)((g >> (8 * j)) & 0xFF)) << (8 * j);
+        t[2 * e] = g;
+        t[2 * e + 1] = ng;
+    }
+    for (int s = 0; s < 256; s++) sign_byte_selectors((uint32_t)s, t + 2 * (512 + s));
+}
+
+// IQ2_XS's / IQ2_S's tables: [0, n) grid entry e as its 8 bytes, then their
+// negations (16 bytes); then 8-byte selectors: of a 7-bit sign index (the
+// first 8 bytes of IQ2_XXS's selector rows, sel7, 16 bytes a row) or, with
+// sel7 null, of a sign byte.
+void build_iq2_xs_s_tables8(uint32_t *t, const uint64_t *grid, int n, const uint32_t *sel7) {
+    for (int e = 0; e < n; e++) {
+        const uint64_t g = grid[e];
+        uint64_t ng = 0;
+        for (int j = 0; j < 8; j++) ng |= (uint64_t)(uint8_t)(-(int)((g >> (8 * j)) & 0xFF)) << (8 * j);
+        t[e * 4 + 0] = (uint32_t)g;
+        t[e * 4 + 1] = (uint32_t)(g >> 32);
+        t[e * 4 + 2] = (uint32_t)ng;
+        t[e * 4 + 3] = (uint32_t)(ng >> 32);
+    }
+    uint32_t *s2 = t + n * 4;
+    if (sel7)
+        for (int s = 0; s < 128; s++) {
+            s2[2 * s] = sel7[4 * s];
+            s2[2 * s + 1] = sel7[4 * s + 1];
+        }
+    else
+        for (int s = 0; s < 256; s++) sign_byte_selectors((uint32_t)s, s2 + 2 * s);
+}
+
 #define OKF_DISPATCH(type, fn, ...)                         \
     switch (type) {                                         \
     case Q8_0: fn<Q8_0>(__VA_ARGS__); break;                \
@@ -241,11 +286,15 @@ int okf_ctx_create(int device, okf_ctx **out) {
         build_iq2_tables(tabh);
         if (e == hipSuccess) e = hipMalloc((void **)&c->tab, sizeof(tabh));
         if (e == hipSuccess) e = hipMemcpy(c->tab, tabh, sizeof(tabh), hipMemcpyHostToDevice);
-        uint32_t tab8h[(384 + 192) * 4];
+        std::vector<uint32_t> tab8v(ITAB_ROWS * 4);
+        uint32_t *tab8h = tab8v.data();
         build_iq2_tables8(tab8h);
-        build_iq3_xxs_tables8(tab8h + 384 * 4, tab8h + 256 * 4);
-        if (e == hipSuccess) e = hipMalloc((void **)&c->tab8, sizeof(tab8h));
-        if (e == hipSuccess) e = hipMemcpy(c->tab8, tab8h, sizeof(tab8h), hipMemcpyHostToDevice);
+        build_iq3_xxs_tables8(tab8h + itab_at(IQ3_XXS) * 4, tab8h + 256 * 4);
+        build_iq3_s_tables8(tab8h + itab_at(IQ3_S) * 4);
+        build_iq2_xs_s_tables8(tab8h + itab_at(IQ2_XS) * 4, okf_host_iq2xs_grid, 512, tab8h + 256 * 4);
+        build_iq2_xs_s_tables8(tab8h + itab_at(IQ2_S) * 4, okf_host_iq2s_grid, 1024, nullptr);
+        if (e == hipSuccess) e = hipMalloc((void **)&c->tab8, tab8v.size() * 4);
+        if (e == hipSuccess) e = hipMemcpy(c->tab8, tab8h, tab8v.size() * 4, hipMemcpyHostToDevice);
         if (e != hipSuccess) {
             if (c->grid) (void)hipFree(c->grid);
             if (c->grids) (void)hipFree(c->grids);
