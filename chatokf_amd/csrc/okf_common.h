@@ -20,9 +20,9 @@ __host__ __device__ constexpr bool grid_fmt(int f) {
            f == Q3_K || f == F32 || f == F16 || f == BF16;
 }
 // The formats the matvec takes through that generic compute: all of them but
-// IQ3_XXS, IQ3_S, IQ2_XS and IQ2_S, which have integer computes of their own
+// the grid formats, which have integer computes of their own
 __host__ __device__ constexpr bool gen_fmt(int f) {
-    return grid_fmt(f) && f != IQ3_XXS && f != IQ3_S && f != IQ2_XS && f != IQ2_S;
+    return grid_fmt(f) && f != IQ3_XXS && f != IQ3_S && f != IQ2_XS && f != IQ2_S && f != IQ1_S && f != IQ1_M;
 }
 // 16-byte rows of those computes' tables, and where they start in the
 // context's table buffer (after IQ2_XXS's 384 rows)

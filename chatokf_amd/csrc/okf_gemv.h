@@ -59,12 +59,11 @@ __host__ __device__ constexpr uint32_t unit_lds_bytes() {
 }
 
 // 16-byte LDS rows of tables gemv_kernel copies per workgroup: IQ2_XXS's
-// int8 grid and sign rows, a grid format's own grid (IQ1_S / IQ1_M read
-// their 8 KB grid from device memory: the copy measured 1-2 us slower at
-// 17408 x 5120, where it took IQ3_XXS from 31.6 to 24.6 us)
+// int8 grid and sign rows, the other grid formats' integer tables (IQ1_S /
+// IQ1_M: their grid as it is)
 template <int F>
 __host__ __device__ constexpr uint32_t gemv_tab_rows() {
-    return F == IQ2_XXS ? 384 : itab_rows(F) ? itab_rows(F) : (F == IQ1_S || F == IQ1_M) ? 0 : gt_bytes(F) / 16;
+    return F == IQ2_XXS ? 384 : itab_rows(F) ? itab_rows(F) : gt_bytes(F) / 16;
 }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -112,6 +111,16 @@ template <int R>
 struct Unit<IQ2_S, R> {  // d, 8 index bytes, 8 sign bytes, 2 high-bit bytes, 2 scale bytes
     uint32_t d[R], qh[R], sc[R];
     uint2 q[R], sg[R];
+};
+template <int R>
+struct Unit<IQ1_S, R> {  // d, 8 index bytes, 2 high-bits words
+    uint32_t d[R], qh[R];
+    uint2 q[R];
+};
+template <int R>
+struct Unit<IQ1_M, R> {  // 8 index bytes, 4 high-bit bytes, the block's 4 scale words, the unit's one
+    uint32_t qh[R], sw[R];
+    uint2 q[R], sc[R];
 };
 template <int R>
 struct Unit<IQ3_XXS, R> {  // d, the two sub-blocks' 16 grid indices and their two scale-and-sign words
@@ -225,6 +234,19 @@ __device__ __forceinline__ void load_unit(const uint8_t *const rows[R], uint32_t
             w.sg[r] = ldu<uint2>(b + 34 + g * 8);
             w.qh[r] = ldu<uint16_t>(b + 66 + g * 2);
             w.sc[r] = ldu<uint16_t>(b + 74 + g * 2);
+        } else if constexpr (F == IQ1_S) {
+            const uint8_t *b = rows[r] + (uint64_t)(u >> 2) * 50;
+            const uint32_t g = u & 3;
+            w.d[r] = ldu<uint16_t>(b);
+            w.q[r] = ldu<uint2>(b + 2 + g * 8);
+            w.qh[r] = ldu<uint32_t>(b + 34 + g * 4);
+        } else if constexpr (F == IQ1_M) {
+            const uint8_t *b = rows[r] + (uint64_t)(u >> 2) * 56;
+            const uint32_t g = u & 3;
+            w.q[r] = ldu<uint2>(b + g * 8);
+            w.qh[r] = ldu<uint32_t>(b + 32 + g * 4);
+            w.sc[r] = ldu<uint2>(b + 48);
+            w.sw[r] = ldu<uint16_t>(b + 48 + g * 2);  // sub-blocks 2g, 2g + 1: scale word g
         } else if constexpr (gen_fmt(F)) {
             w.row[r] = rows[r];
         } else if constexpr (F == Q4_0 || F == IQ4_NL) {
@@ -736,6 +758,90 @@ struct Compute<IQ2_S, NC, R, TS> {
     __device__ __forceinline__ static void run(const Unit<IQ2_S, R> &w, const XA &xa, uint32_t,
                                                float (&acc)[R][NC], const u32x4 *tab) {
         ComputeIQ2XS<IQ2_S, NC, R, TS>::run(w, xa, acc, tab);
+    }
+};
+
+// IQ1.dequant / IQ1M.dequant (LLM/Quantize/IQ1.swift:44-66,
+// LLM/Quantize/IQ2XXS.swift:63-98) as integer dot products: weight =
+// dl (n - 1 + delta), delta = +-1/8, n the grid's ternary digit, so 8 w / dl
+// = 8 n - 8 +- 1 fits int8; one v_perm picks it per byte from the six
+// values {-7, 1, 9 | -9, -1, 7} by n + 4 (delta < 0).  tab: the 2048-entry
+// grid (4 bytes an entry: weight j's digit at bit 8 (j % 4) + 4 (j / 4)).
+// IQ1_S has one dl and delta per 32 weights; IQ1_M one dl per 16 and a
+// delta per 8.
+template <int F, int NC, int R, int TS>
+struct ComputeIQ1 {
+    template <class XA>
+    __device__ __forceinline__ static void run(const Unit<F, R> &w, const XA &xa, float (&acc)[R][NC],
+                                               const u32x4 *tab) {
+        const uint32_t *grid = (const uint32_t *)tab;
+        constexpr uint32_t POS = 0x000901F9u, NEG = 0x0007FFF7u;  // {-7, 1, 9, 0}, {-9, -1, 7, 0}
+#pragma unroll
+        for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                int s[3][R][NC];
+                zero3(s);
+                uint32_t wv[R][4];
+#pragma unroll
+                for (int r = 0; r < R; r++)
+#pragma unroll
+                    for (int e = 0; e < 2; e++) {
+                        const int l = 2 * h + e;
+                        const uint32_t qd = sb ? w.q[r].y : w.q[r].x;
+                        uint32_t hb, neg;
+                        if constexpr (F == IQ1_S) {
+                            const uint32_t qh = (w.qh[r] >> (16 * sb)) & 0xFFFF;
+                            hb = (qh >> (3 * l)) & 7;
+                            neg = qh >> 15;
+                        } else {
+                            const uint32_t hq = (w.qh[r] >> (16 * sb + 8 * h)) & 0xFF;
+                            hb = (hq >> (4 * e)) & 7;
+                            neg = (hq >> (4 * e + 3)) & 1;
+                        }
+                        const uint32_t gv = grid[((qd >> (8 * l)) & 0xFF) | (hb << 8)];
+                        const uint32_t nm = neg ? 0x04040404u : 0u;
+                        wv[r][2 * e] = perm(NEG, POS, (gv & 0x0F0F0F0Fu) | nm);
+                        wv[r][2 * e + 1] = perm(NEG, POS, ((gv >> 4) & 0x0F0F0F0Fu) | nm);
+                    }
+                dot_half<NC, R>(xa, sb, h, [&](int r, int k) { return wv[r][k]; }, s);
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    float dl;
+                    if constexpr (F == IQ1_S) {
+                        const uint32_t qh = (w.qh[r] >> (16 * sb)) & 0xFFFF;
+                        dl = h2f(w.d[r]) * (float)(2 * ((qh >> 12) & 7) + 1);
+                    } else {
+                        // d from the tops of the block's four scale words; the
+                        // sub-block's 3-bit scales (one per 16 weights) at
+                        // bit 6 sb of the unit's word
+                        const uint32_t a = w.sc[r].x, b = w.sc[r].y;
+                        const uint32_t bits = ((a & 0xFFFF) >> 12) | ((a >> 24) & 0x00f0) |
+                                              (((b & 0xFFFF) >> 4) & 0x0f00) | ((b >> 16) & 0xf000);
+                        const uint32_t sv = w.sw[r] >> (6 * sb);
+                        dl = h2f((uint16_t)bits) * (float)(2 * ((sv >> (3 * h)) & 7) + 1);
+                    }
+                    const float db = dl * 0.125f;
+#pragma unroll
+                    for (int n = 0; n < NC; n++) acc[r][n] += db * (comb(s, r, n) * xa.gd(n, sb)[3]);
+                }
+            }
+    }
+};
+template <int NC, int R, int TS>
+struct Compute<IQ1_S, NC, R, TS> {
+    template <class XA>
+    __device__ __forceinline__ static void run(const Unit<IQ1_S, R> &w, const XA &xa, uint32_t,
+                                               float (&acc)[R][NC], const u32x4 *tab) {
+        ComputeIQ1<IQ1_S, NC, R, TS>::run(w, xa, acc, tab);
+    }
+};
+template <int NC, int R, int TS>
+struct Compute<IQ1_M, NC, R, TS> {
+    template <class XA>
+    __device__ __forceinline__ static void run(const Unit<IQ1_M, R> &w, const XA &xa, uint32_t,
+                                               float (&acc)[R][NC], const u32x4 *tab) {
+        ComputeIQ1<IQ1_M, NC, R, TS>::run(w, xa, acc, tab);
     }
 };
 
