@@ -19,10 +19,11 @@ __host__ __device__ constexpr bool grid_fmt(int f) {
     return f == IQ2_XS || f == IQ2_S || f == IQ3_XXS || f == IQ3_S || f == IQ1_S || f == IQ1_M || f == Q2_K ||
            f == Q3_K || f == F32 || f == F16 || f == BF16;
 }
-// The formats the matvec takes through that generic compute: all of them but
-// the grid formats, which have integer computes of their own
+// The formats the matvec takes through that generic compute: the plain
+// weights (the grid formats and Q2_K / Q3_K have integer computes of their
+// own)
 __host__ __device__ constexpr bool gen_fmt(int f) {
-    return grid_fmt(f) && f != IQ3_XXS && f != IQ3_S && f != IQ2_XS && f != IQ2_S && f != IQ1_S && f != IQ1_M;
+    return f == F32 || f == F16 || f == BF16;
 }
 // 16-byte rows of those computes' tables, and where they start in the
 // context's table buffer (after IQ2_XXS's 384 rows)

@@ -38,7 +38,7 @@ namespace okf {
 // any K that is a whole number of blocks works).
 template <int F>
 __host__ __device__ constexpr uint32_t unit_weights() {
-    return (F == Q8_0 || F == Q4_0 || F == IQ4_NL || gen_fmt(F)) ? 32 : 64;
+    return (F == Q8_0 || F == Q4_0 || F == IQ4_NL || F == Q2_K || F == Q3_K || gen_fmt(F)) ? 32 : 64;
 }
 // 32-weight groups per unit, and 16-byte LDS chunks per unit (per group:
 // three digit planes of 32 bytes; for the generic formats, whose weights are
@@ -121,6 +121,17 @@ template <int R>
 struct Unit<IQ1_M, R> {  // 8 index bytes, 4 high-bit bytes, the block's 4 scale words, the unit's one
     uint32_t qh[R], sw[R];
     uint2 q[R], sc[R];
+};
+template <int R>
+struct Unit<Q2_K, R> {  // the group's 32 code bytes, its two scale bytes, d and dmin
+    u32x4 q0[R], q1[R];
+    uint32_t sc[R], dd[R];
+};
+template <int R>
+struct Unit<Q3_K, R> {  // the group's 32 code bytes, the 32 hmask bytes, the 12 scale bytes, d
+    u32x4 q0[R], q1[R], h0[R], h1[R];
+    uint2 s8[R];
+    uint32_t s4[R], d[R];
 };
 template <int R>
 struct Unit<IQ3_XXS, R> {  // d, the two sub-blocks' 16 grid indices and their two scale-and-sign words
@@ -247,6 +258,23 @@ __device__ __forceinline__ void load_unit(const uint8_t *const rows[R], uint32_t
             w.qh[r] = ldu<uint32_t>(b + 32 + g * 4);
             w.sc[r] = ldu<uint2>(b + 48);
             w.sw[r] = ldu<uint16_t>(b + 48 + g * 2);  // sub-blocks 2g, 2g + 1: scale word g
+        } else if constexpr (F == Q2_K) {  // unit = group j = u & 7 of superblock u >> 3
+            const uint8_t *b = rows[r] + (uint64_t)(u >> 3) * 84;
+            const uint32_t j = u & 7, n = j >> 2;
+            w.q0[r] = ldu<u32x4>(b + 16 + 32 * n);
+            w.q1[r] = ldu<u32x4>(b + 32 + 32 * n);
+            w.sc[r] = ldu<uint16_t>(b + 2 * j);
+            w.dd[r] = ldu<uint32_t>(b + 80);
+        } else if constexpr (F == Q3_K) {
+            const uint8_t *b = rows[r] + (uint64_t)(u >> 3) * 110;
+            const uint32_t n = (u & 7) >> 2;
+            w.q0[r] = ldu<u32x4>(b + 32 + 32 * n);
+            w.q1[r] = ldu<u32x4>(b + 48 + 32 * n);
+            w.h0[r] = ldu<u32x4>(b);
+            w.h1[r] = ldu<u32x4>(b + 16);
+            w.s8[r] = ldu<uint2>(b + 96);
+            w.s4[r] = ldu<uint32_t>(b + 104);
+            w.d[r] = ldu<uint16_t>(b + 108);
         } else if constexpr (gen_fmt(F)) {
             w.row[r] = rows[r];
         } else if constexpr (F == Q4_0 || F == IQ4_NL) {
@@ -842,6 +870,72 @@ struct Compute<IQ1_M, NC, R, TS> {
     __device__ __forceinline__ static void run(const Unit<IQ1_M, R> &w, const XA &xa, uint32_t,
                                                float (&acc)[R][NC], const u32x4 *tab) {
         ComputeIQ1<IQ1_M, NC, R, TS>::run(w, xa, acc, tab);
+    }
+};
+
+template <int NC, int R, int TS>
+struct Compute<Q2_K, NC, R, TS> {
+    // KQuant.q2K (LLM/Quantize/KQuants.swift:9-36) as integer dot products:
+    // per 16 weights, w = d (sc & 15) q - dmin (sc >> 4), q = the 2-bit
+    // field 2 (j % 4) of the group's code bytes, so sum w x = d (sc & 15)
+    // sum q X f - dmin (sc >> 4) sum X f, both sums exact per half group.
+    template <class XA>
+    __device__ __forceinline__ static void run(const Unit<Q2_K, R> &w, const XA &xa, uint32_t u,
+                                               float (&acc)[R][NC], const u32x4 *) {
+        const uint32_t sh = 2 * (u & 3);
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            int s[3][R][NC];
+            zero3(s);
+            dot_half<NC, R>(xa, 0, h, [&](int r, int k) {
+                return ((h ? w.q1[r][k] : w.q0[r][k]) >> sh) & 0x03030303u;
+            }, s);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const uint32_t sc = (w.sc[r] >> (8 * h)) & 0xFF;
+                const float dl = h2f(w.dd[r] & 0xFFFF) * (float)(sc & 0xF), ml = h2f(w.dd[r] >> 16) * (float)(sc >> 4);
+#pragma unroll
+                for (int n = 0; n < NC; n++) {
+                    const floatx4 g = xa.gd(n, 0);
+                    acc[r][n] += g[3] * (dl * comb(s, r, n) - ml * g[h]);
+                }
+            }
+        }
+    }
+};
+
+template <int NC, int R, int TS>
+struct Compute<Q3_K, NC, R, TS> {
+    // KQuant.q3K (LLM/Quantize/KQuants.swift:38-83) as integer dot products:
+    // w = dl (q + 4 hbit - 4), q + 4 hbit (0..7) a byte, so sum w x =
+    // dl (sum (q + 4 hbit) X - 4 sum X) f per 16 weights.
+    template <class XA>
+    __device__ __forceinline__ static void run(const Unit<Q3_K, R> &w, const XA &xa, uint32_t u,
+                                               float (&acc)[R][NC], const u32x4 *) {
+        const uint32_t j = u & 7, n8 = j >> 2, sh = 2 * (j & 3), hb = 4 * n8 + (j & 3);
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            int s[3][R][NC];
+            zero3(s);
+            dot_half<NC, R>(xa, 0, h, [&](int r, int k) {
+                const uint32_t q = ((h ? w.q1[r][k] : w.q0[r][k]) >> sh) & 0x03030303u;
+                const uint32_t hm = ((h ? w.h1[r][k] : w.h0[r][k]) >> hb) & 0x01010101u;
+                return q | (hm << 2);
+            }, s);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const uint32_t i = n8 * 8 + (j & 3) * 2 + h;
+                const uint32_t lo8 = (i & 7) < 4 ? w.s8[r].x : w.s8[r].y;
+                const uint32_t lo = (lo8 >> (8 * (i & 3) + 4 * (i >> 3))) & 0xF;
+                const uint32_t hi = (w.s4[r] >> (8 * (i & 3) + 2 * (i >> 2))) & 3;
+                const float dl = h2f(w.d[r]) * (float)((int)(lo | (hi << 4)) - 32);
+#pragma unroll
+                for (int n = 0; n < NC; n++) {
+                    const floatx4 g = xa.gd(n, 0);
+                    acc[r][n] += g[3] * (dl * (comb(s, r, n) - 4.0f * g[h]));
+                }
+            }
+        }
     }
 };
 

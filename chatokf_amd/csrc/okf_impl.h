@@ -158,7 +158,7 @@ void launch_gemv_s(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32
     // column 10-25 % slower), Q4_K and Q2_0 with 5.  (A
     // three-deep ring for the Q4_K matvec measured 3-4 % slower than two
     // once the weight loads were issued behind the staging's.)
-    constexpr int R = ((F == IQ2_XXS && NC >= 1) || ((itab_rows(F) || F == IQ1_S || F == IQ1_M) && NC >= 2) || (gen_fmt(F) && NC >= 2) ||
+    constexpr int R = ((F == IQ2_XXS && NC >= 1) || (grid_fmt(F) && NC >= 2) ||
                        (NC == 5 && F != Q8_0 && F != Q5_K && F != Q6_K && F != IQ4_XS)) ? 2 : 1,
                   D = DX ? DX : 2, WAVES = 4;
     const void *fn = (const void *)gemv_kernel<F, NC, R, D, S, SILU>;
