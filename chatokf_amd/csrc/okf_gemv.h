@@ -522,11 +522,8 @@ __device__ __forceinline__ float comb(const int (&s)[3][R][NC], int r, int n) {
 
 template <int F, int NC, int R, int TS = 1>
 struct Compute {
-    // The grid formats (IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M), the
-    // small K-quants and the plain weights: the 32-weight sub-block is
-    // decoded to fp32 with the bit-exact decoder (the format's grid from its
-    // copy in LDS, or for IQ1_S / IQ1_M all the grids in device memory: tab)
-    // and multiplied in fp32 into the activations, staged as
+    // The plain f32 / f16 / bf16 weights: the 32 weights of a unit are
+    // decoded to fp32 and multiplied in fp32 into the activations, staged as
     // fp32 (chunk c of the unit = values 4c .. 4c + 3): one fma a weight,
     // in order, as the reference's fp32 dot.
     static_assert(gen_fmt(F), "no matvec compute for this format");
@@ -536,8 +533,7 @@ struct Compute {
 #pragma unroll
         for (int r = 0; r < R; r++) {
             float wv[32];
-            if constexpr (gt_bytes(F) > 0) decode_unit_fg<F>(w.row[r], u, wv, (const uint8_t *)tab);
-            else decode_unit<F>(w.row[r], u, wv, nullptr);
+            decode_unit<F>(w.row[r], u, wv, nullptr);
 #pragma unroll
             for (int n = 0; n < NC; n++) {
                 float a = 0;
