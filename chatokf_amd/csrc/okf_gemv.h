@@ -38,7 +38,7 @@ namespace okf {
 // any K that is a whole number of blocks works).
 template <int F>
 __host__ __device__ constexpr uint32_t unit_weights() {
-    return (F == Q8_0 || F == Q4_0 || F == IQ4_NL || F == Q2_K || F == Q3_K || gen_fmt(F)) ? 32 : 64;
+    return (F == Q8_0 || F == Q4_0 || F == IQ4_NL || gen_fmt(F)) ? 32 : 64;
 }
 // 32-weight groups per unit, and 16-byte LDS chunks per unit (per group:
 // three digit planes of 32 bytes; for the generic formats, whose weights are
@@ -123,12 +123,12 @@ struct Unit<IQ1_M, R> {  // 8 index bytes, 4 high-bit bytes, the block's 4 scale
     uint2 q[R], sc[R];
 };
 template <int R>
-struct Unit<Q2_K, R> {  // the group's 32 code bytes, its two scale bytes, d and dmin
+struct Unit<Q2_K, R> {  // groups 2g, 2g + 1: their 32 code bytes, four scale bytes, d and dmin
     u32x4 q0[R], q1[R];
     uint32_t sc[R], dd[R];
 };
 template <int R>
-struct Unit<Q3_K, R> {  // the group's 32 code bytes, the 32 hmask bytes, the 12 scale bytes, d
+struct Unit<Q3_K, R> {  // groups 2g, 2g + 1: their 32 code bytes, the 32 hmask bytes, the 12 scale bytes, d
     u32x4 q0[R], q1[R], h0[R], h1[R];
     uint2 s8[R];
     uint32_t s4[R], d[R];
@@ -258,16 +258,16 @@ __device__ __forceinline__ void load_unit(const uint8_t *const rows[R], uint32_t
             w.qh[r] = ldu<uint32_t>(b + 32 + g * 4);
             w.sc[r] = ldu<uint2>(b + 48);
             w.sw[r] = ldu<uint16_t>(b + 48 + g * 2);  // sub-blocks 2g, 2g + 1: scale word g
-        } else if constexpr (F == Q2_K) {  // unit = group j = u & 7 of superblock u >> 3
-            const uint8_t *b = rows[r] + (uint64_t)(u >> 3) * 84;
-            const uint32_t j = u & 7, n = j >> 2;
+        } else if constexpr (F == Q2_K) {  // unit = groups 2g, 2g + 1 (g = u & 3) of superblock u >> 2
+            const uint8_t *b = rows[r] + (uint64_t)(u >> 2) * 84;
+            const uint32_t g = u & 3, n = g >> 1;  // (both groups read the same code bytes)
             w.q0[r] = ldu<u32x4>(b + 16 + 32 * n);
             w.q1[r] = ldu<u32x4>(b + 32 + 32 * n);
-            w.sc[r] = ldu<uint16_t>(b + 2 * j);
+            w.sc[r] = ldu<uint32_t>(b + 4 * g);
             w.dd[r] = ldu<uint32_t>(b + 80);
         } else if constexpr (F == Q3_K) {
-            const uint8_t *b = rows[r] + (uint64_t)(u >> 3) * 110;
-            const uint32_t n = (u & 7) >> 2;
+            const uint8_t *b = rows[r] + (uint64_t)(u >> 2) * 110;
+            const uint32_t n = (u & 3) >> 1;
             w.q0[r] = ldu<u32x4>(b + 32 + 32 * n);
             w.q1[r] = ldu<u32x4>(b + 48 + 32 * n);
             w.h0[r] = ldu<u32x4>(b);
@@ -873,27 +873,31 @@ template <int NC, int R, int TS>
 struct Compute<Q2_K, NC, R, TS> {
     // KQuant.q2K (LLM/Quantize/KQuants.swift:9-36) as integer dot products:
     // per 16 weights, w = d (sc & 15) q - dmin (sc >> 4), q = the 2-bit
-    // field 2 (j % 4) of the group's code bytes, so sum w x = d (sc & 15)
+    // field 2 (j % 4) of group j's code bytes, so sum w x = d (sc & 15)
     // sum q X f - dmin (sc >> 4) sum X f, both sums exact per half group.
     template <class XA>
     __device__ __forceinline__ static void run(const Unit<Q2_K, R> &w, const XA &xa, uint32_t u,
                                                float (&acc)[R][NC], const u32x4 *) {
-        const uint32_t sh = 2 * (u & 3);
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            int s[3][R][NC];
-            zero3(s);
-            dot_half<NC, R>(xa, 0, h, [&](int r, int k) {
-                return ((h ? w.q1[r][k] : w.q0[r][k]) >> sh) & 0x03030303u;
-            }, s);
+        for (int gi = 0; gi < 2; gi++) {  // group j = 2 (u % 4) + gi
+            const uint32_t sh = 2 * ((2 * (u & 3) + gi) & 3);
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                const uint32_t sc = (w.sc[r] >> (8 * h)) & 0xFF;
-                const float dl = h2f(w.dd[r] & 0xFFFF) * (float)(sc & 0xF), ml = h2f(w.dd[r] >> 16) * (float)(sc >> 4);
+            for (int h = 0; h < 2; h++) {
+                int s[3][R][NC];
+                zero3(s);
+                dot_half<NC, R>(xa, gi, h, [&](int r, int k) {
+                    return ((h ? w.q1[r][k] : w.q0[r][k]) >> sh) & 0x03030303u;
+                }, s);
 #pragma unroll
-                for (int n = 0; n < NC; n++) {
-                    const floatx4 g = xa.gd(n, 0);
-                    acc[r][n] += g[3] * (dl * comb(s, r, n) - ml * g[h]);
+                for (int r = 0; r < R; r++) {
+                    const uint32_t sc = (w.sc[r] >> (16 * gi + 8 * h)) & 0xFF;
+                    const float dl = h2f(w.dd[r] & 0xFFFF) * (float)(sc & 0xF);
+                    const float ml = h2f(w.dd[r] >> 16) * (float)(sc >> 4);
+#pragma unroll
+                    for (int n = 0; n < NC; n++) {
+                        const floatx4 g = xa.gd(n, gi);
+                        acc[r][n] += g[3] * (dl * comb(s, r, n) - ml * g[h]);
+                    }
                 }
             }
         }
@@ -908,12 +912,14 @@ struct Compute<Q3_K, NC, R, TS> {
     template <class XA>
     __device__ __forceinline__ static void run(const Unit<Q3_K, R> &w, const XA &xa, uint32_t u,
                                                float (&acc)[R][NC], const u32x4 *) {
-        const uint32_t j = u & 7, n8 = j >> 2, sh = 2 * (j & 3), hb = 4 * n8 + (j & 3);
+#pragma unroll
+      for (int gi = 0; gi < 2; gi++) {  // group j = 2 (u % 4) + gi
+        const uint32_t j = 2 * (u & 3) + gi, n8 = j >> 2, sh = 2 * (j & 3), hb = 4 * n8 + (j & 3);
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             int s[3][R][NC];
             zero3(s);
-            dot_half<NC, R>(xa, 0, h, [&](int r, int k) {
+            dot_half<NC, R>(xa, gi, h, [&](int r, int k) {
                 const uint32_t q = ((h ? w.q1[r][k] : w.q0[r][k]) >> sh) & 0x03030303u;
                 const uint32_t hm = ((h ? w.h1[r][k] : w.h0[r][k]) >> hb) & 0x01010101u;
                 return q | (hm << 2);
@@ -927,11 +933,12 @@ struct Compute<Q3_K, NC, R, TS> {
                 const float dl = h2f(w.d[r]) * (float)((int)(lo | (hi << 4)) - 32);
 #pragma unroll
                 for (int n = 0; n < NC; n++) {
-                    const floatx4 g = xa.gd(n, 0);
+                    const floatx4 g = xa.gd(n, gi);
                     acc[r][n] += g[3] * (dl * (comb(s, r, n) - 4.0f * g[h]));
                 }
             }
         }
+      }
     }
 };
 
