@@ -584,13 +584,18 @@ struct Compute<Q4_K, NC, R, TS> {
     }
 };
 
+// the IQ2 grid's three values and their negations, as v_perm sources
+constexpr uint32_t IQ2_POS = 0x002B1908u, IQ2_NEG = 0x00D5E7F8u;  // {8, 25, 43, 0}, {-8, -25, -43, 0}
+
 template <int NC, int R, int TS>
 struct Compute<IQ2_XXS, NC, R, TS> {
-    // tab: [0, 256) grid entries {g.x, g.y, (-g).x, (-g).y} (the 8 values
-    // as bytes, then negated), [256, 384) sign entries {S.x, S.y} of v_perm
-    // selectors: byte j of weight dword k selects j (+g) or j + 4 (-g) by
-    // its sign (the eighth from the parity rule), so one v_perm makes four
-    // signed weight bytes.  Entry e at tab[e * TS] (TS = 16: the
+    // tab: [0, 256) grid entries {I.x, I.y}: per weight the index 0..2 of
+    // its value in {8, 25, 43}; [256, 384) sign entries {S.x, S.y} of
+    // selectors, byte j = j % 4 + 4 (weight j negative; the eighth sign from
+    // the parity rule).  I + S - {0, 1, 2, 3} selects the signed value from
+    // {8, 25, 43 | -8, -25, -43} (no byte carries: each sum is 0..6), so
+    // one add and one v_perm make four signed weight bytes, from 8-byte
+    // table reads.  Entry e at tab[e * TS] (TS = 16: the
     // replicated, conflict-free layout of gemv_wide_kernel, tab offset by
     // the lane's copy).
     template <class XA>
@@ -609,10 +614,10 @@ struct Compute<IQ2_XXS, NC, R, TS> {
 #pragma unroll
                     for (int e = 0; e < 2; e++) {
                         const int l = 2 * h + e;
-                        const u32x4 gv = tab[((a0 >> (8 * l)) & 0xFF) * TS];
+                        const uint2 gv = *(const uint2 *)&tab[((a0 >> (8 * l)) & 0xFF) * TS];
                         const uint2 sg = *(const uint2 *)&tab[(256 + ((a1 >> (7 * l)) & 127)) * TS];
-                        wv[r][2 * e] = perm(gv[2], gv[0], sg.x);
-                        wv[r][2 * e + 1] = perm(gv[3], gv[1], sg.y);
+                        wv[r][2 * e] = perm(IQ2_NEG, IQ2_POS, gv.x + sg.x - 0x03020100u);
+                        wv[r][2 * e + 1] = perm(IQ2_NEG, IQ2_POS, gv.y + sg.y - 0x03020100u);
                     }
                 }
                 dot_half<NC, R>(xa, sb, h, [&](int r, int k) { return wv[r][k]; }, s);

@@ -60,16 +60,19 @@ void build_iq2_tables(uint32_t *t) {
 // negative weight) and M & 0x01010101, {M.lo, M.hi, M1.lo, M1.hi}, so that a
 // signed weight byte is (g ^ M) + M1.
 void build_iq2_tables8(uint32_t *t) {
-    // grid entry e: its 8 values as bytes, then their negations (the dot4
-    // kernels pick each weight's byte from one or the other with v_perm)
+    // grid entry e: per weight the index of its value in {8, 25, 43} (the
+    // grid's only bytes), 8 bytes; the dot4 kernels add 4 for a negative
+    // weight and pick the signed byte with one v_perm
     for (int e = 0; e < 256; e++) {
         const uint64_t g = okf_iq2xxs_grid_host[e];
-        uint64_t ng = 0;
-        for (int j = 0; j < 8; j++) ng |= (uint64_t)(uint8_t)(-(int)((g >> (8 * j)) & 0xFF)) << (8 * j);
-        t[e * 4 + 0] = (uint32_t)g;
-        t[e * 4 + 1] = (uint32_t)(g >> 32);
-        t[e * 4 + 2] = (uint32_t)ng;
-        t[e * 4 + 3] = (uint32_t)(ng >> 32);
+        uint64_t ix = 0;
+        for (int j = 0; j < 8; j++) {
+            const uint32_t v = (uint32_t)((g >> (8 * j)) & 0xFF);
+            ix |= (uint64_t)(v == 8 ? 0 : v == 25 ? 1 : 2) << (8 * j);
+        }
+        t[e * 4 + 0] = (uint32_t)ix;
+        t[e * 4 + 1] = (uint32_t)(ix >> 32);
+        t[e * 4 + 2] = t[e * 4 + 3] = 0;
     }
     // sign entry s7: v_perm selectors, byte j of weight dword k is j (the
     // positive value) or j + 4 (the negated one) for the eighth sign from the
