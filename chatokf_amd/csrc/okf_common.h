@@ -28,12 +28,12 @@ __host__ __device__ constexpr bool gen_fmt(int f) {
 // 16-byte rows of those computes' tables, and where they start in the
 // context's table buffer (after IQ2_XXS's 384 rows)
 __host__ __device__ constexpr uint32_t itab_rows(int f) {
-    return f == IQ3_XXS ? 192 : f == IQ3_S ? 384 : f == IQ2_XS ? 576 : f == IQ2_S ? 1152 : 0;
+    return f == IQ3_XXS ? 192 : f == IQ3_S ? 384 : f == IQ2_XS ? 320 : f == IQ2_S ? 640 : 0;
 }
 __host__ __device__ constexpr uint32_t itab_at(int f) {
-    return f == IQ3_XXS ? 384 : f == IQ3_S ? 576 : f == IQ2_XS ? 960 : f == IQ2_S ? 1536 : 0;
+    return f == IQ3_XXS ? 384 : f == IQ3_S ? 576 : f == IQ2_XS ? 960 : f == IQ2_S ? 1280 : 0;
 }
-constexpr uint32_t ITAB_ROWS = 2688;
+constexpr uint32_t ITAB_ROWS = 1920;
 constexpr uint32_t GT_IQ2XS = 0, GT_IQ2S = 4096, GT_IQ3XXS = 12288, GT_IQ3S = 13312, GT_IQ1S = 15360,
                    GT_BYTES = 23552;
 // a grid format's own grid: its offset in that buffer and its size (IQ1_M

@@ -723,17 +723,17 @@ struct Compute<IQ3_S, NC, R, TS> {
 
 // IQX.iq2XS / IQX.iq2S (LLM/Quantize/IQ3.swift:14-57) as integer dot
 // products: weight = d (0.5 + nibble) / 4 * sign * grid byte (8, 25, 43),
-// one scale nibble per 16 weights.  tab: [0, G) grid entry e as 16 bytes (8
-// values, then their negations), then 8-byte v_perm selectors: of a 7-bit
+// one scale nibble per 16 weights.  tab (8-byte entries): [0, G) grid entry
+// e as its values' indices in {8, 25, 43}, then the selectors of a 7-bit
 // sign index (IQ2_XS, eighth sign from the parity rule) or of a sign byte
-// (IQ2_S).
+// (IQ2_S), combined as IQ2_XXS's.
 template <int F, int NC, int R, int TS>
 struct ComputeIQ2XS {
     static constexpr uint32_t G = F == IQ2_S ? 1024 : 512;
     template <class XA>
     __device__ __forceinline__ static void run(const Unit<F, R> &w, const XA &xa, float (&acc)[R][NC],
                                                const u32x4 *tab) {
-        const uint2 *sel = (const uint2 *)(tab + G);
+        const uint2 *gi = (const uint2 *)tab, *sel = gi + G;
 #pragma unroll
         for (int sb = 0; sb < 2; sb++)
 #pragma unroll
@@ -757,10 +757,9 @@ struct ComputeIQ2XS {
                             idx = q16 & 511;
                             sv = q16 >> 9;
                         }
-                        const u32x4 gv = tab[idx];
-                        const uint2 sg = sel[sv];
-                        wv[r][2 * e] = perm(gv[2], gv[0], sg.x);
-                        wv[r][2 * e + 1] = perm(gv[3], gv[1], sg.y);
+                        const uint2 gv = gi[idx], sg = sel[sv];
+                        wv[r][2 * e] = perm(IQ2_NEG, IQ2_POS, gv.x + sg.x - 0x03020100u);
+                        wv[r][2 * e + 1] = perm(IQ2_NEG, IQ2_POS, gv.y + sg.y - 0x03020100u);
                     }
                 dot_half<NC, R>(xa, sb, h, [&](int r, int k) { return wv[r][k]; }, s);
 #pragma unroll

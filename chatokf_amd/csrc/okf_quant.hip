@@ -126,21 +126,23 @@ void build_iq3_s_tables8(uint32_t *t) {
     for (int s = 0; s < 256; s++) sign_byte_selectors((uint32_t)s, t + 2 * (512 + s));
 }
 
-// IQ2_XS's / IQ2_S's tables: [0, n) grid entry e as its 8 bytes, then their
-// negations (16 bytes); then 8-byte selectors: of a 7-bit sign index (the
-// first 8 bytes of IQ2_XXS's selector rows, sel7, 16 bytes a row) or, with
-// sel7 null, of a sign byte.
+// IQ2_XS's / IQ2_S's tables, 8-byte entries: [0, n) grid entry e as the
+// indices 0..2 of its 8 values in {8, 25, 43} (as IQ2_XXS's); then the
+// selectors (byte j = j % 4 + 4 for a negative weight): of a 7-bit sign
+// index (the first 8 bytes of IQ2_XXS's selector rows, sel7, 16 bytes a
+// row) or, with sel7 null, of a sign byte.
 void build_iq2_xs_s_tables8(uint32_t *t, const uint64_t *grid, int n, const uint32_t *sel7) {
     for (int e = 0; e < n; e++) {
         const uint64_t g = grid[e];
-        uint64_t ng = 0;
-        for (int j = 0; j < 8; j++) ng |= (uint64_t)(uint8_t)(-(int)((g >> (8 * j)) & 0xFF)) << (8 * j);
-        t[e * 4 + 0] = (uint32_t)g;
-        t[e * 4 + 1] = (uint32_t)(g >> 32);
-        t[e * 4 + 2] = (uint32_t)ng;
-        t[e * 4 + 3] = (uint32_t)(ng >> 32);
+        uint64_t ix = 0;
+        for (int j = 0; j < 8; j++) {
+            const uint32_t v = (uint32_t)((g >> (8 * j)) & 0xFF);
+            ix |= (uint64_t)(v == 8 ? 0 : v == 25 ? 1 : 2) << (8 * j);
+        }
+        t[e * 2] = (uint32_t)ix;
+        t[e * 2 + 1] = (uint32_t)(ix >> 32);
     }
-    uint32_t *s2 = t + n * 4;
+    uint32_t *s2 = t + n * 2;
     if (sel7)
         for (int s = 0; s < 128; s++) {
             s2[2 * s] = sel7[4 * s];
