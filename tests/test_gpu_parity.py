@@ -170,7 +170,8 @@ def test_gemv_edges(enc, t, M, K):
 # Activations of any fp32 magnitude: each 32-weight group carries its own
 # power-of-two scale, so tiny, huge and mixed-magnitude vectors keep the
 # reference's fp32 relative precision (no fp16 overflow or underflow).
-@pytest.mark.parametrize("t", [Q8_0, Q2_0, Q4_K, IQ2_XXS], ids=lambda t: NAMES[t])
+@pytest.mark.parametrize("t", [Q8_0, Q2_0, Q4_K, IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M, Q2_K, Q3_K,
+                               F32], ids=lambda t: NAMES[t])
 @pytest.mark.parametrize("scale", ["1e-20", "1e-5", "1e5", "1e20", "mixed"])
 def test_gemv_activation_range(enc, t, scale):
     M, K = 1030, 2048
