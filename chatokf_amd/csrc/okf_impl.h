@@ -232,7 +232,7 @@ bool launch_iq2mm(okf_ctx *c, const GemvCall &call, uint64_t rb, uint32_t K) {
     const size_t lds = GM_TAB * 16 + (size_t)P * GV_L * (GM_UNIT + 2) * 16 + (size_t)GM_WAVES * kmax * 4 * NC * 4;
     const uint32_t sp = (units * 32 + GW_THREADS - 1) / GW_THREADS;
     if (lds > c->max_lds || sp > 3 || nq * P * GM_WAVES >= (1ull << 32)) return false;
-    constexpr int D = 4;
+    constexpr int D = 2;  // weight ring depth (17408 x 5120, N = 4: 1 19.4, 2 19.5, 3 20.2, 4 20.9, 6 21.2, 8 22.9 us)
     auto go = [&](auto spc) {
         constexpr uint32_t SP = decltype(spc)::value;
         const void *fn = (const void *)gemv_wide_iq2mm_kernel<NC, D, SP>;
