@@ -178,6 +178,26 @@ void build_iq2_xs_s_tables8(uint32_t *t, const uint64_t *grid, int n, const uint
 
 enum class Path { Auto, Tile };
 
+// N > 5 as consecutive narrow launches of up to narrow_cols columns, while N
+// <= narrow_max: the tile kernels fill few CUs at small N.  Measured on
+// MI355X at 17408 x 5120 (us): Q4_K narrow 5 columns 56, tile 84-88 at N =
+// 6..8; IQ2_XXS narrow 4 columns 19.4, tile 142-153 at N = 6..32; IQ3_XXS 5
+// columns 53, tile 171-179; Q8_0 64 / 152; Q5_K 68 / 171; Q6_K 65 / 161;
+// Q2_K 53 / 132; Q4_0 4 columns 28 / 125 (and at 2048 x 2048 Q8_0 7.1 / 56,
+// Q2_0 2048 x 6144 11.5 / 123).
+uint32_t narrow_cols(int32_t t) { return t == IQ2_XXS || t == Q4_0 || t == IQ4_NL ? 4 : 5; }
+uint32_t narrow_max(int32_t t) {
+    switch (t) {
+    case Q4_K: return 7;
+    case IQ2_XXS: return 28;
+    case Q4_0: case IQ4_NL: return 16;
+    case Q5_K: case Q2_K: return 12;
+    case Q8_0: case Q6_K: return 11;
+    case F32: case F16: case BF16: return 5;
+    default: return 15;  // the other grid formats, IQ4_XS, Q3_K, Q2_0
+    }
+}
+
 int run_gemm(okf_ctx *c, const okf_weight *w, const float *X, uint32_t N, float *Y, Path path,
              const float *X2 = nullptr) {
     uint64_t rb = 0;
@@ -188,7 +208,17 @@ int run_gemm(okf_ctx *c, const okf_weight *w, const float *X, uint32_t N, float 
     if (!aligned16(X) || (X2 && !aligned16(X2))) return OKF_E_SHAPE;
     if ((st = begin(c))) return st;
     const uint8_t *W = (const uint8_t *)w->base + w->off;
-    if (path == Path::Auto && N <= 5) {
+    // (at M <= 4096 the 128 x 128 tile kernel runs at most 32 workgroups per
+    // 128 columns: chunks win to N = 32, e.g. Q8_0 2048 x 2048 N = 28 about
+    // 39 against 59 us, Q2_0 2048 x 6144 69 against 130)
+    const uint32_t nmax = std::max(narrow_max(w->ggml_type), w->M <= 4096 ? 32u : 0u);
+    if (path == Path::Auto && N > 5 && N <= nmax && !X2) {
+        const uint32_t nc = narrow_cols(w->ggml_type);
+        for (uint32_t c0 = 0; c0 < N; c0 += nc) {
+            const GemvCall call{W, X + (uint64_t)c0 * w->K, Y + (uint64_t)c0 * w->M, w->M, nullptr};
+            OKF_DISPATCH(w->ggml_type, launch_gemv, c, &call, 1, rb, w->K, std::min(nc, N - c0));
+        }
+    } else if (path == Path::Auto && N <= 5) {
         const GemvCall call{W, X, Y, w->M, X2};
         if (c->grouping && N == 1) {
             // inside a parallel group: launched together at okf_parallel_end

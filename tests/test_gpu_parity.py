@@ -539,8 +539,36 @@ def test_tile_gemm_matches_oracle(enc, t, M, K, N):
     ref = oracle.matmul(t, w, K, M, X).astype(np.float64)
     got = run_gemm(enc, t, M, K, w, X, tile=True)
     assert rel(got, ref) <= TOL
-    if N > 5:  # the auto path takes the tile for N > 5
+    if not narrow_chunks(t, M, N):  # the auto path takes the tile past the narrow chunks
         assert np.array_equal(run_gemm(enc, t, M, K, w, X), got)
+
+
+# The auto path for 5 < N <= NARROW_MAX[t]: consecutive narrow launches of
+# up to NARROW_COLS[t] columns (okf_quant.hip's narrow_max / narrow_cols).
+NARROW_MAX = {Q4_K: 7, IQ2_XXS: 28, Q4_0: 16, IQ4_NL: 16, Q5_K: 12, Q2_K: 12, Q8_0: 11, Q6_K: 11, F32: 5,
+              F16: 5, BF16: 5}
+NARROW_COLS = {IQ2_XXS: 4, Q4_0: 4, IQ4_NL: 4}
+
+
+def narrow_chunks(t, M, N):
+    return 5 < N <= max(NARROW_MAX.get(t, 15), 32 if M <= 4096 else 0)
+CHUNKS = [(Q4_K, 260, 2304, 7), (IQ2_XXS, 129, 1536, 6), (IQ2_XXS, 1000, 1280, 28), (Q8_0, 300, 2048, 11),
+          (Q2_0, 130, 1024, 13), (Q4_0, 300, 2048, 9), (IQ3_XXS, 130, 768, 15), (Q2_K, 130, 768, 12),
+          (Q6_K, 129, 768, 8), (Q8_0, 2048, 2048, 32), (F32, 300, 1024, 17), (Q4_K, 4000, 2304, 20)]
+
+
+@pytest.mark.parametrize("t,M,K,N", CHUNKS)
+def test_small_n_narrow_chunks(enc, t, M, K, N):
+    say("chunks", NAMES[t], M, K, N)
+    assert narrow_chunks(t, M, N)
+    w = weights(t, M, K, 19)
+    X = acts(N, K, 20)
+    ref = oracle.matmul(t, w, K, M, X).astype(np.float64)
+    got = run_gemm(enc, t, M, K, w, X)
+    assert rel(got, ref) <= TOL_MV
+    nc = NARROW_COLS.get(t, 5)
+    for c0 in range(0, N, nc):
+        assert np.array_equal(got[c0:c0 + nc], run_gemm(enc, t, M, K, w, X[c0:c0 + nc]))
 
 
 # With OKF_GEMM_KS=k the leftover tiles are split over k K ranges of whole
