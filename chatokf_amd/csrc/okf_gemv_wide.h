@@ -208,13 +208,16 @@ __device__ __forceinline__ uint32_t gm_start(uint32_t z, uint32_t T) {
     return (uint32_t)((uint64_t)z * T / GM_WAVES);
 }
 
-template <int NC, int D, uint32_t SP>
-__global__ __launch_bounds__(GW_THREADS) void gemv_wide_iq2mm_kernel(const uint8_t *__restrict__ W,
-                                                                     uint64_t row_bytes, uint32_t K,
-                                                                     uint32_t M, const float *__restrict__ X,
-                                                                     float *__restrict__ Y,
-                                                                     const u32x4 *__restrict__ tab_g,
-                                                                     uint32_t kmax) {
+// The body of the 2..4-column matrix-core kernels: F = IQ2_XXS (weights from
+// the replicated fp16 tables) or Q4_K (weights sc * q, exact in fp16, from
+// the nibbles; the mins through the per-32 activation sums staged beside the
+// scales).
+template <int F, int NC, int D, uint32_t SP>
+__device__ __forceinline__ void wide_mm_body(const uint8_t *__restrict__ W, uint64_t row_bytes, uint32_t K,
+                                             uint32_t M, const float *__restrict__ X, float *__restrict__ Y,
+                                             const u32x4 *__restrict__ tab_g, uint32_t kmax) {
+    static_assert(F == IQ2_XXS || F == Q4_K, "matrix-core narrow formats");
+    constexpr uint32_t TABR = F == IQ2_XXS ? GM_TAB : 0;
     constexpr int L = GV_L;
     constexpr uint32_t UW = 64;
     extern __shared__ u32x4 lds[];
@@ -226,14 +229,15 @@ __global__ __launch_bounds__(GW_THREADS) void gemv_wide_iq2mm_kernel(const uint8
     const uint32_t units = K / UW, P = (units + L - 1) / L;
     const uint32_t nq = (r1 - r0 + 3) / 4, T = nq * P, s0 = gm_start(z, T), s1 = gm_start(z + 1, T);
     u32x4 *tab = lds;
-    u32x4 *xs = lds + GM_TAB;
+    u32x4 *xs = lds + TABR;
     floatx4 *xf = (floatx4 *)(xs + (size_t)P * L * GM_UNIT);
-    float *part = (float *)(xf + (size_t)P * L * 2);
+    floatx4 *xsum = xf + (size_t)P * L * 2;  // (Q4_K) per-32 sums of x, as xf
+    float *part = (float *)(xsum + (F == Q4_K ? (size_t)P * L * 2 : 0));
 
     // loads: table entries, then activations, then the weight ring
-    constexpr uint32_t TPT = GM_TAB / GW_THREADS;
-    static_assert(GM_TAB % GW_THREADS == 0, "table entries per thread");
-    u32x4 trow[TPT];
+    constexpr uint32_t TPT = TABR / GW_THREADS;
+    static_assert(TABR % GW_THREADS == 0, "table entries per thread");
+    u32x4 trow[TPT > 0 ? TPT : 1];
 #pragma unroll
     for (uint32_t k = 0; k < TPT; k++) trow[k] = tab_g[(tid + k * GW_THREADS) / GM_COPIES];
     const uint32_t nx = units * 8 * 4;  // (unit, k-slot, column) entries, <= SP * 1024
@@ -250,9 +254,9 @@ __global__ __launch_bounds__(GW_THREADS) void gemv_wide_iq2mm_kernel(const uint8
     const uint32_t lrow0 = r0 + (s0 / P) * 4 + t;
     const uint8_t *lrow = W + (uint64_t)min(lrow0, r1 - 1) * row_bytes;
     uint32_t ls = s0, lsu = s0 % P, lr = lrow0;
-    auto load_next = [&](Unit<IQ2_XXS, 1> &w) {
+    auto load_next = [&](Unit<F, 1> &w) {
         const uint8_t *rows[1] = {lrow};
-        load_unit<IQ2_XXS, 1>(rows, min(lsu * L + q, units - 1), w);
+        load_unit<F, 1>(rows, min(lsu * L + q, units - 1), w);
         if (ls + 1 < s1) {
             ls++;
             if (++lsu == P) {
@@ -262,7 +266,7 @@ __global__ __launch_bounds__(GW_THREADS) void gemv_wide_iq2mm_kernel(const uint8
             }
         }
     };
-    Unit<IQ2_XXS, 1> buf[D];
+    Unit<F, 1> buf[D];
 #pragma unroll
     for (int j = 0; j < D; j++) load_next(buf[j]);
     __builtin_amdgcn_sched_barrier(0);
@@ -282,6 +286,15 @@ __global__ __launch_bounds__(GW_THREADS) void gemv_wide_iq2mm_kernel(const uint8
         m = fmaxf(m, __shfl_xor(m, 4, 64));
         m = fmaxf(m, __shfl_xor(m, 8, 64));
         const int ex = min(__builtin_amdgcn_frexp_expf(m), 127);
+        float sx = 0;  // (Q4_K) the group's sum of x, in order within a slot
+        if constexpr (F == Q4_K) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) sx += A[p][k];
+#pragma unroll
+            for (int k = 0; k < 4; k++) sx += B[p][k];
+            sx += __shfl_xor(sx, 4, 64);
+            sx += __shfl_xor(sx, 8, 64);
+        }
         floatx4 Ah, Al, Bh, Bl;
 #pragma unroll
         for (int k = 0; k < 4; k++) {
@@ -296,11 +309,15 @@ __global__ __launch_bounds__(GW_THREADS) void gemv_wide_iq2mm_kernel(const uint8
         if (c >= (uint32_t)NC) {
             hi = lo = u32x4{0, 0, 0, 0};
             f = 0;
+            sx = 0;
         }
         if (e < nx) {
             xs[u * GM_UNIT + sl * 4 + c] = hi;
             xs[u * GM_UNIT + 32 + sl * 4 + c] = lo;
-            if ((sl & 3) == 0) ((float *)xf)[(u * 2 + (sl >> 2)) * 4 + c] = f;
+            if ((sl & 3) == 0) {
+                ((float *)xf)[(u * 2 + (sl >> 2)) * 4 + c] = f;
+                if constexpr (F == Q4_K) ((float *)xsum)[(u * 2 + (sl >> 2)) * 4 + c] = sx;
+            }
         }
     }
     __syncthreads();
@@ -328,19 +345,42 @@ __global__ __launch_bounds__(GW_THREADS) void gemv_wide_iq2mm_kernel(const uint8
         for (int j = 0; j < D; j++) {
             if (st + j < s1) {
                 const uint32_t u = su * L + q;
-                const Unit<IQ2_XXS, 1> &w = buf[j];
+                const Unit<F, 1> &w = buf[j];
                 const bool live = u < units;
                 const u32x4 *xp = xs + min(u, units - 1) * GM_UNIT + t;
+                [[maybe_unused]] uint32_t sc[2], mn[2];
+                if constexpr (F == Q4_K)
+                    q4k_scale_min_pair(make_uint4(w.hdr[0][0], w.hdr[0][1], w.hdr[0][2], w.hdr[0][3]),
+                                       (u & 3), sc[0], mn[0], sc[1], mn[1]);
 #pragma unroll
                 for (int sb = 0; sb < 2; sb++) {
-                    const uint32_t a0 = w.a[0][2 * sb], a1 = w.a[0][2 * sb + 1];
                     floatx4 acc = {0, 0, 0, 0};
 #pragma unroll
                     for (int l = 0; l < 4; l++) {
-                        const u32x4 gv = tl[((a0 >> (8 * l)) & 0xFF) * GM_COPIES];
-                        const u32x4 sg = tl[(256 + ((a1 >> (7 * l)) & 127)) * GM_COPIES];
                         const u32x4 xv = xp[(4 * sb + l) * 4], xl = xp[32 + (4 * sb + l) * 4];
-                        const u32x4 wv = gv ^ sg;
+                        u32x4 wv;
+                        if constexpr (F == IQ2_XXS) {
+                            const uint32_t a0 = w.a[0][2 * sb], a1 = w.a[0][2 * sb + 1];
+                            const u32x4 gv = tl[((a0 >> (8 * l)) & 0xFF) * GM_COPIES];
+                            const u32x4 sg = tl[(256 + ((a1 >> (7 * l)) & 127)) * GM_COPIES];
+                            wv = gv ^ sg;
+                        } else {
+                            // weights 8 l .. 8 l + 7 of sub-block sb: code
+                            // bytes 8 l .. 8 l + 7, low (sb 0) or high nibbles,
+                            // as 1024 + q in fp16, then sc (1024 + q) - 1024 sc
+                            // = sc q, exact (<= 945), in one fma
+                            const uint32_t c0 = l < 2 ? w.q0[0][2 * l] : w.q1[0][2 * l - 4];
+                            const uint32_t c1 = l < 2 ? w.q0[0][2 * l + 1] : w.q1[0][2 * l - 3];
+                            const uint32_t n0 = (c0 >> (4 * sb)) & 0x0F0F0F0Fu, n1 = (c1 >> (4 * sb)) & 0x0F0F0F0Fu;
+                            const _Float16 s = (_Float16)(float)sc[sb], o = (_Float16)(-1024.0f * (float)sc[sb]);
+                            const half2v s2 = {s, s}, o2 = {o, o};
+                            const uint32_t e4[4] = {perm(0x64646464u, n0, 0x04010400u), perm(0x64646464u, n0, 0x04030402u),
+                                                    perm(0x64646464u, n1, 0x04010400u), perm(0x64646464u, n1, 0x04030402u)};
+#pragma unroll
+                            for (int i = 0; i < 4; i++)
+                                wv[i] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(
+                                                                         __builtin_bit_cast(half2v, e4[i]), s2, o2));
+                        }
 #pragma unroll
                         for (int h = 0; h < 2; h++) {
                             const half4v wh = __builtin_bit_cast(half4v, uint2{wv[2 * h], wv[2 * h + 1]});
@@ -350,8 +390,15 @@ __global__ __launch_bounds__(GW_THREADS) void gemv_wide_iq2mm_kernel(const uint8
                                 __builtin_bit_cast(half4v, uint2{xl[2 * h], xl[2 * h + 1]}), wh, acc, 0, 0, 0);
                         }
                     }
-                    const float db = live ? h2f(w.d[0]) * (0.5f + (float)(a1 >> 28)) * 0.25f : 0.0f;
-                    tot += db * (acc * xf[min(u, units - 1) * 2 + sb]);
+                    const uint32_t uc = min(u, units - 1);
+                    if constexpr (F == IQ2_XXS) {
+                        const float db = live ? h2f(w.d[0]) * (0.5f + (float)(w.a[0][2 * sb + 1] >> 28)) * 0.25f : 0.0f;
+                        tot += db * (acc * xf[uc * 2 + sb]);
+                    } else {
+                        const float d = live ? h2f(w.hdr[0][0] & 0xFFFF) : 0.0f;
+                        const float dm = live ? h2f(w.hdr[0][0] >> 16) * (float)mn[sb] : 0.0f;
+                        tot += d * (acc * xf[uc * 2 + sb]) - dm * xsum[uc * 2 + sb];
+                    }
                 }
                 if (++su == P && st + j + 1 < s1) {  // next step starts a row quad
                     flush();
@@ -378,6 +425,24 @@ __global__ __launch_bounds__(GW_THREADS) void gemv_wide_iq2mm_kernel(const uint8
         }
         Y[(uint64_t)n * M + r0 + rho] = v;
     }
+}
+
+template <int NC, int D, uint32_t SP>
+__global__ __launch_bounds__(GW_THREADS) void gemv_wide_iq2mm_kernel(const uint8_t *__restrict__ W,
+                                                                     uint64_t row_bytes, uint32_t K,
+                                                                     uint32_t M, const float *__restrict__ X,
+                                                                     float *__restrict__ Y,
+                                                                     const u32x4 *__restrict__ tab_g,
+                                                                     uint32_t kmax) {
+    wide_mm_body<IQ2_XXS, NC, D, SP>(W, row_bytes, K, M, X, Y, tab_g, kmax);
+}
+
+template <int NC, int D, uint32_t SP>
+__global__ __launch_bounds__(GW_THREADS) void gemv_wide_q4kmm_kernel(const uint8_t *__restrict__ W,
+                                                                     uint64_t row_bytes, uint32_t K,
+                                                                     uint32_t M, const float *__restrict__ X,
+                                                                     float *__restrict__ Y, uint32_t kmax) {
+    wide_mm_body<Q4_K, NC, D, SP>(W, row_bytes, K, M, X, Y, nullptr, kmax);
 }
 
 }  // namespace okf

@@ -48,6 +48,7 @@ struct okf_ctx {
     int gemv_sb_rw = 0;  // its rows per workgroup (0 = auto)
     int gemv_sb_t = 0;   // its threads per workgroup (0 = auto)
     int gemm_ks = 0;     // wide-tile GEMM: K ranges per remainder tile (0 = auto)
+    int q4k_mm = 1;      // Q4_K 2..4 columns on the matrix cores (0: the dot4 kernel)
     int gemm_thin = 0;   // leftover-tile kernel variant (A/B switch)
     int gemm_ng = 4;     // wide-tile GEMM: N tiles that share an XCD's row blocks
     uint32_t cus = 256;  // compute units of the device
@@ -247,6 +248,32 @@ bool launch_iq2mm(okf_ctx *c, const GemvCall &call, uint64_t rb, uint32_t K) {
     return true;
 }
 
+// Q4_K with 2..4 columns on the matrix cores (gemv_wide_q4kmm_kernel): true
+// when launched.
+template <int NC>
+bool launch_q4kmm(okf_ctx *c, const GemvCall &call, uint64_t rb, uint32_t K) {
+    if (!c->q4k_mm) return false;
+    const uint32_t G = std::min(c->cus, call.M), units = K / 64, P = (units + GV_L - 1) / GV_L;
+    const uint64_t nq = ((call.M + G - 1) / G + 3) / 4, lmax = (nq * P + GM_WAVES - 1) / GM_WAVES;
+    const uint32_t kmax = (uint32_t)((lmax + P - 1) / P + 1);
+    const size_t lds = (size_t)P * GV_L * (GM_UNIT + 4) * 16 + (size_t)GM_WAVES * kmax * 4 * NC * 4;
+    const uint32_t sp = (units * 32 + GW_THREADS - 1) / GW_THREADS;
+    if (lds > c->max_lds || sp > 3 || nq * P * GM_WAVES >= (1ull << 32)) return false;
+    constexpr int D = 2;
+    auto go = [&](auto spc) {
+        constexpr uint32_t SP = decltype(spc)::value;
+        const void *fn = (const void *)gemv_wide_q4kmm_kernel<NC, D, SP>;
+        static std::atomic<uint64_t> attr{0};  // devices that have the attribute set
+        set_lds_attr(c, fn, attr);
+        hipLaunchKernelGGL((gemv_wide_q4kmm_kernel<NC, D, SP>), dim3(G), dim3(GW_THREADS), lds, c->stream,
+                           call.W, rb, K, call.M, call.X, call.Y, kmax);
+    };
+    if (sp <= 1) go(std::integral_constant<uint32_t, 1>{});
+    else if (sp == 2) go(std::integral_constant<uint32_t, 2>{});
+    else go(std::integral_constant<uint32_t, 3>{});
+    return true;
+}
+
 // One workgroup per CU (gemv_wide_kernel) for a single matrix: true when
 // launched.
 template <int F, int NC>
@@ -344,6 +371,8 @@ bool launch_gemv_sb(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint3
 template <int F, int NC, bool SILU = false>
 void launch_gemv_nc(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32_t K) {
     if (launch_gemv_sb<F, NC, SILU>(c, calls, n, rb, K)) return;
+    if constexpr (F == Q4_K && !SILU && NC >= 2 && NC <= 4)
+        if (n == 1 && launch_q4kmm<NC>(c, calls[0], rb, K)) return;
     // (Q4_K and Q8_0 units are too large for a deep ring at N > 1; the
     // formats added after the measurements take the many-workgroup kernel)
     if constexpr (!SILU && !((F == Q4_K || F == Q8_0) && NC > 1) && F != Q5_K && F != Q6_K && F != IQ4_XS &&

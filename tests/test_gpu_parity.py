@@ -244,6 +244,18 @@ def test_iq2_xxs_mtp_verify_full_config(enc):
     assert r <= TOL_MV
 
 
+@pytest.mark.parametrize("N", [2, 3, 4])
+def test_q4_k_narrow_full_config(enc, N):
+    # Q4_K 17408 x 5120 with 2..4 columns (the matrix-core narrow kernel)
+    t, M, K = Q4_K, 17408, 5120
+    w = weights(t, M, K, 1003)
+    X = acts(N, K, 2006)
+    ref = oracle.matmul(t, w, K, M, X).astype(np.float64)
+    r = rel(run_gemm(enc, t, M, K, w, X), ref)
+    say("q4_k N", N, "rel", r)
+    assert r <= TOL_MV
+
+
 # ------------------------------------------- one workgroup per CU (wide)
 # With OKF_GEMV_WIDE=1 every single-matrix matvec / narrow call that the
 # one-workgroup-per-CU kernel takes goes through it (the automatic policy
@@ -539,7 +551,7 @@ def test_tile_gemm_matches_oracle(enc, t, M, K, N):
     ref = oracle.matmul(t, w, K, M, X).astype(np.float64)
     got = run_gemm(enc, t, M, K, w, X, tile=True)
     assert rel(got, ref) <= TOL
-    if not narrow_chunks(t, M, N):  # the auto path takes the tile past the narrow chunks
+    if N > 5 and not narrow_chunks(t, M, N, K):  # the auto path takes the tile past the narrow chunks
         assert np.array_equal(run_gemm(enc, t, M, K, w, X), got)
 
 
@@ -550,23 +562,30 @@ NARROW_MAX = {Q4_K: 7, IQ2_XXS: 28, Q4_0: 16, IQ4_NL: 16, Q5_K: 12, Q2_K: 12, Q8
 NARROW_COLS = {IQ2_XXS: 4, Q4_0: 4, IQ4_NL: 4}
 
 
-def narrow_chunks(t, M, N):
-    return 5 < N <= max(NARROW_MAX.get(t, 15), 32 if M <= 4096 else 0)
+def narrow_cols(t, K):
+    return 4 if t in NARROW_COLS or (t == Q4_K and K <= 6144) else 5
+
+
+def narrow_chunks(t, M, N, K=0):
+    nmax = 16 if t == Q4_K and K <= 6144 else NARROW_MAX.get(t, 15)
+    first = 5 if t == IQ2_XXS or (t == Q4_K and K <= 6144) else 6
+    return first <= N <= max(nmax, 32 if M <= 4096 else 0)
 CHUNKS = [(Q4_K, 260, 2304, 7), (IQ2_XXS, 129, 1536, 6), (IQ2_XXS, 1000, 1280, 28), (Q8_0, 300, 2048, 11),
           (Q2_0, 130, 1024, 13), (Q4_0, 300, 2048, 9), (IQ3_XXS, 130, 768, 15), (Q2_K, 130, 768, 12),
-          (Q6_K, 129, 768, 8), (Q8_0, 2048, 2048, 32), (F32, 300, 1024, 17), (Q4_K, 4000, 2304, 20)]
+          (Q6_K, 129, 768, 8), (Q8_0, 2048, 2048, 32), (F32, 300, 1024, 17), (Q4_K, 4000, 2304, 20),
+          (Q4_K, 1030, 2048, 5), (IQ2_XXS, 1030, 2048, 5), (Q4_K, 300, 8192, 7)]
 
 
 @pytest.mark.parametrize("t,M,K,N", CHUNKS)
 def test_small_n_narrow_chunks(enc, t, M, K, N):
     say("chunks", NAMES[t], M, K, N)
-    assert narrow_chunks(t, M, N)
+    assert narrow_chunks(t, M, N, K)
     w = weights(t, M, K, 19)
     X = acts(N, K, 20)
     ref = oracle.matmul(t, w, K, M, X).astype(np.float64)
     got = run_gemm(enc, t, M, K, w, X)
     assert rel(got, ref) <= TOL_MV
-    nc = NARROW_COLS.get(t, 5)
+    nc = narrow_cols(t, K)
     for c0 in range(0, N, nc):
         assert np.array_equal(got[c0:c0 + nc], run_gemm(enc, t, M, K, w, X[c0:c0 + nc]))
 
