@@ -253,6 +253,7 @@ def main():
         # gate and up in one grid with the SiLU (two weight seeds, one x)
         ("q2_0_matvec_gate_up_2x6144x2048", ok.Q2_0, 6144, 2048, 1, (1002, 1202), 2002),
         ("q4_k_matvec_17408x5120", ok.Q4_K, 17408, 5120, 1, 1003, 2003),
+        ("q4_k_matmul_17408x5120_m4", ok.Q4_K, 17408, 5120, 4, 1003, 2006),
         ("q4_k_matvec_5120x17408", ok.Q4_K, 5120, 17408, 1, 1103, 2103),
         ("iq2_xxs_matvec_17408x5120_m1", ok.IQ2_XXS, 17408, 5120, 1, 1004, 2004),
         ("iq2_xxs_matmul_17408x5120_m4", ok.IQ2_XXS, 17408, 5120, 4, 1004, 2004),
