@@ -208,15 +208,40 @@ __device__ __forceinline__ uint32_t gm_start(uint32_t z, uint32_t T) {
     return (uint32_t)((uint64_t)z * T / GM_WAVES);
 }
 
-// The body of the 2..4-column matrix-core kernels: F = IQ2_XXS (weights from
-// the replicated fp16 tables) or Q4_K (weights sc * q, exact in fp16, from
-// the nibbles; the mins through the per-32 activation sums staged beside the
-// scales).
+// int8 bytes b (4) -> two dwords of fp16 pairs of 1152 + b (exact); the
+// caller subtracts 1152 (or folds it into an fma)
+__device__ __forceinline__ void i8_h2(uint32_t b4, uint32_t &lo, uint32_t &hi) {
+    const uint32_t u = b4 ^ 0x80808080u;  // b + 128, 0..255
+    lo = perm(0x64646464u, u, 0x04010400u);
+    hi = perm(0x64646464u, u, 0x04030402u);
+}
+
+// Q8_0's unit here: blocks 2u, 2u + 1 (64 weights)
+struct Q8Pair {
+    uint32_t d[2];
+    u32x4 q[2][2];
+};
+template <int F>
+struct MMUnit {
+    using type = Unit<F, 1>;
+};
+template <>
+struct MMUnit<Q8_0> {
+    using type = Q8Pair;
+};
+
+// The body of the 2..4-column matrix-core kernels, per 64-weight unit (two
+// 32-weight sub-blocks): F = IQ2_XXS (weights from the replicated fp16
+// tables), Q4_K / Q5_K (weights sc * q, exact in fp16, from the nibbles and
+// the fifth bit; the mins through the per-32 activation sums staged beside
+// the scales), IQ4_XS (the levels, scale per sub-block) or Q8_0 (the int8
+// codes, scale per block).
 template <int F, int NC, int D, uint32_t SP>
 __device__ __forceinline__ void wide_mm_body(const uint8_t *__restrict__ W, uint64_t row_bytes, uint32_t K,
                                              uint32_t M, const float *__restrict__ X, float *__restrict__ Y,
                                              const u32x4 *__restrict__ tab_g, uint32_t kmax) {
-    static_assert(F == IQ2_XXS || F == Q4_K, "matrix-core narrow formats");
+    static_assert(F == IQ2_XXS || F == Q4_K || F == Q5_K || F == IQ4_XS || F == Q8_0, "matrix-core narrow formats");
+    constexpr bool MINS = F == Q4_K || F == Q5_K;
     constexpr uint32_t TABR = F == IQ2_XXS ? GM_TAB : 0;
     constexpr int L = GV_L;
     constexpr uint32_t UW = 64;
@@ -231,8 +256,8 @@ __device__ __forceinline__ void wide_mm_body(const uint8_t *__restrict__ W, uint
     u32x4 *tab = lds;
     u32x4 *xs = lds + TABR;
     floatx4 *xf = (floatx4 *)(xs + (size_t)P * L * GM_UNIT);
-    floatx4 *xsum = xf + (size_t)P * L * 2;  // (Q4_K) per-32 sums of x, as xf
-    float *part = (float *)(xsum + (F == Q4_K ? (size_t)P * L * 2 : 0));
+    floatx4 *xsum = xf + (size_t)P * L * 2;  // (Q4_K, Q5_K) per-32 sums of x, as xf
+    float *part = (float *)(xsum + (MINS ? (size_t)P * L * 2 : 0));
 
     // loads: table entries, then activations, then the weight ring
     constexpr uint32_t TPT = TABR / GW_THREADS;
@@ -254,9 +279,21 @@ __device__ __forceinline__ void wide_mm_body(const uint8_t *__restrict__ W, uint
     const uint32_t lrow0 = r0 + (s0 / P) * 4 + t;
     const uint8_t *lrow = W + (uint64_t)min(lrow0, r1 - 1) * row_bytes;
     uint32_t ls = s0, lsu = s0 % P, lr = lrow0;
-    auto load_next = [&](Unit<F, 1> &w) {
-        const uint8_t *rows[1] = {lrow};
-        load_unit<F, 1>(rows, min(lsu * L + q, units - 1), w);
+    using UnitT = typename MMUnit<F>::type;
+    auto load_next = [&](UnitT &w) {
+        const uint32_t uu = min(lsu * L + q, units - 1);
+        if constexpr (F == Q8_0) {
+#pragma unroll
+            for (int b = 0; b < 2; b++) {
+                const uint8_t *bp = lrow + (uint64_t)(2 * uu + b) * 34;
+                w.d[b] = ldu<uint16_t>(bp);
+                w.q[b][0] = ldu<u32x4>(bp + 2);
+                w.q[b][1] = ldu<u32x4>(bp + 18);
+            }
+        } else {
+            const uint8_t *rows[1] = {lrow};
+            load_unit<F, 1>(rows, uu, w);
+        }
         if (ls + 1 < s1) {
             ls++;
             if (++lsu == P) {
@@ -266,7 +303,7 @@ __device__ __forceinline__ void wide_mm_body(const uint8_t *__restrict__ W, uint
             }
         }
     };
-    Unit<F, 1> buf[D];
+    UnitT buf[D];
 #pragma unroll
     for (int j = 0; j < D; j++) load_next(buf[j]);
     __builtin_amdgcn_sched_barrier(0);
@@ -286,8 +323,8 @@ __device__ __forceinline__ void wide_mm_body(const uint8_t *__restrict__ W, uint
         m = fmaxf(m, __shfl_xor(m, 4, 64));
         m = fmaxf(m, __shfl_xor(m, 8, 64));
         const int ex = min(__builtin_amdgcn_frexp_expf(m), 127);
-        float sx = 0;  // (Q4_K) the group's sum of x, in order within a slot
-        if constexpr (F == Q4_K) {
+        float sx = 0;  // (Q4_K, Q5_K) the group's sum of x, in order within a slot
+        if constexpr (MINS) {
 #pragma unroll
             for (int k = 0; k < 4; k++) sx += A[p][k];
 #pragma unroll
@@ -316,7 +353,7 @@ __device__ __forceinline__ void wide_mm_body(const uint8_t *__restrict__ W, uint
             xs[u * GM_UNIT + 32 + sl * 4 + c] = lo;
             if ((sl & 3) == 0) {
                 ((float *)xf)[(u * 2 + (sl >> 2)) * 4 + c] = f;
-                if constexpr (F == Q4_K) ((float *)xsum)[(u * 2 + (sl >> 2)) * 4 + c] = sx;
+                if constexpr (MINS) ((float *)xsum)[(u * 2 + (sl >> 2)) * 4 + c] = sx;
             }
         }
     }
@@ -345,11 +382,11 @@ __device__ __forceinline__ void wide_mm_body(const uint8_t *__restrict__ W, uint
         for (int j = 0; j < D; j++) {
             if (st + j < s1) {
                 const uint32_t u = su * L + q;
-                const Unit<F, 1> &w = buf[j];
+                const UnitT &w = buf[j];
                 const bool live = u < units;
                 const u32x4 *xp = xs + min(u, units - 1) * GM_UNIT + t;
                 [[maybe_unused]] uint32_t sc[2], mn[2];
-                if constexpr (F == Q4_K)
+                if constexpr (MINS)
                     q4k_scale_min_pair(make_uint4(w.hdr[0][0], w.hdr[0][1], w.hdr[0][2], w.hdr[0][3]),
                                        (u & 3), sc[0], mn[0], sc[1], mn[1]);
 #pragma unroll
@@ -364,14 +401,23 @@ __device__ __forceinline__ void wide_mm_body(const uint8_t *__restrict__ W, uint
                             const u32x4 gv = tl[((a0 >> (8 * l)) & 0xFF) * GM_COPIES];
                             const u32x4 sg = tl[(256 + ((a1 >> (7 * l)) & 127)) * GM_COPIES];
                             wv = gv ^ sg;
-                        } else {
+                        } else if constexpr (MINS) {
                             // weights 8 l .. 8 l + 7 of sub-block sb: code
-                            // bytes 8 l .. 8 l + 7, low (sb 0) or high nibbles,
-                            // as 1024 + q in fp16, then sc (1024 + q) - 1024 sc
-                            // = sc q, exact (<= 945), in one fma
+                            // bytes 8 l .. 8 l + 7, low (sb 0) or high nibbles
+                            // (Q5_K: with bit 2 g + sb of qh bytes 8 l .. as
+                            // the fifth), as 1024 + q in fp16, then
+                            // sc (1024 + q) - 1024 sc = sc q, exact (<= 945,
+                            // Q5_K 1953), in one fma
                             const uint32_t c0 = l < 2 ? w.q0[0][2 * l] : w.q1[0][2 * l - 4];
                             const uint32_t c1 = l < 2 ? w.q0[0][2 * l + 1] : w.q1[0][2 * l - 3];
-                            const uint32_t n0 = (c0 >> (4 * sb)) & 0x0F0F0F0Fu, n1 = (c1 >> (4 * sb)) & 0x0F0F0F0Fu;
+                            uint32_t n0 = (c0 >> (4 * sb)) & 0x0F0F0F0Fu, n1 = (c1 >> (4 * sb)) & 0x0F0F0F0Fu;
+                            if constexpr (F == Q5_K) {
+                                const uint32_t hb = 2 * (u & 3) + sb;
+                                const uint32_t q0h = l < 2 ? w.h0[0][2 * l] : w.h1[0][2 * l - 4];
+                                const uint32_t q1h = l < 2 ? w.h0[0][2 * l + 1] : w.h1[0][2 * l - 3];
+                                n0 |= ((q0h >> hb) & 0x01010101u) << 4;
+                                n1 |= ((q1h >> hb) & 0x01010101u) << 4;
+                            }
                             const _Float16 s = (_Float16)(float)sc[sb], o = (_Float16)(-1024.0f * (float)sc[sb]);
                             const half2v s2 = {s, s}, o2 = {o, o};
                             const uint32_t e4[4] = {perm(0x64646464u, n0, 0x04010400u), perm(0x64646464u, n0, 0x04030402u),
@@ -380,6 +426,27 @@ __device__ __forceinline__ void wide_mm_body(const uint8_t *__restrict__ W, uint
                             for (int i = 0; i < 4; i++)
                                 wv[i] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(
                                                                          __builtin_bit_cast(half2v, e4[i]), s2, o2));
+                        } else {
+                            // int8 weights (IQ4_XS: the levels of the nibbles,
+                            // weight j of a sub-block in byte j % 16's low (j <
+                            // 16) or high nibble; Q8_0: the codes) as fp16
+                            uint32_t b0, b1;
+                            if constexpr (F == IQ4_XS) {
+                                const u32x4 &cq = sb ? w.q1[0] : w.q0[0];
+                                const uint32_t sh = 4 * (l >> 1), i0 = 2 * (l & 1);
+                                b0 = IQ4Levels::levels((cq[i0] >> sh) & 0x0F0F0F0Fu);
+                                b1 = IQ4Levels::levels((cq[i0 + 1] >> sh) & 0x0F0F0F0Fu);
+                            } else {
+                                b0 = w.q[sb][l >> 1][2 * (l & 1)];
+                                b1 = w.q[sb][l >> 1][2 * (l & 1) + 1];
+                            }
+                            const half2v m2 = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+                            uint32_t e4[4];
+                            i8_h2(b0, e4[0], e4[1]);
+                            i8_h2(b1, e4[2], e4[3]);
+#pragma unroll
+                            for (int i = 0; i < 4; i++)
+                                wv[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, e4[i]) + m2);
                         }
 #pragma unroll
                         for (int h = 0; h < 2; h++) {
@@ -394,10 +461,18 @@ __device__ __forceinline__ void wide_mm_body(const uint8_t *__restrict__ W, uint
                     if constexpr (F == IQ2_XXS) {
                         const float db = live ? h2f(w.d[0]) * (0.5f + (float)(w.a[0][2 * sb + 1] >> 28)) * 0.25f : 0.0f;
                         tot += db * (acc * xf[uc * 2 + sb]);
-                    } else {
+                    } else if constexpr (MINS) {
                         const float d = live ? h2f(w.hdr[0][0] & 0xFFFF) : 0.0f;
                         const float dm = live ? h2f(w.hdr[0][0] >> 16) * (float)mn[sb] : 0.0f;
                         tot += d * (acc * xf[uc * 2 + sb]) - dm * xsum[uc * 2 + sb];
+                    } else if constexpr (F == IQ4_XS) {
+                        const uint32_t g = u & 3, shi = w.hdr[0].x >> 16, slo = byte_of(w.hdr[0].y, g);
+                        const uint32_t ls = ((slo >> (4 * sb)) & 0xF) | (((shi >> (4 * g + 2 * sb)) & 3) << 4);
+                        const float dl = live ? h2f(w.hdr[0].x & 0xFFFF) * (float)((int)ls - 32) : 0.0f;
+                        tot += dl * (acc * xf[uc * 2 + sb]);
+                    } else {
+                        const float d = live ? h2f(w.d[sb]) : 0.0f;
+                        tot += d * (acc * xf[uc * 2 + sb]);
                     }
                 }
                 if (++su == P && st + j + 1 < s1) {  // next step starts a row quad
@@ -437,12 +512,12 @@ __global__ __launch_bounds__(GW_THREADS) void gemv_wide_iq2mm_kernel(const uint8
     wide_mm_body<IQ2_XXS, NC, D, SP>(W, row_bytes, K, M, X, Y, tab_g, kmax);
 }
 
-template <int NC, int D, uint32_t SP>
-__global__ __launch_bounds__(GW_THREADS) void gemv_wide_q4kmm_kernel(const uint8_t *__restrict__ W,
-                                                                     uint64_t row_bytes, uint32_t K,
-                                                                     uint32_t M, const float *__restrict__ X,
-                                                                     float *__restrict__ Y, uint32_t kmax) {
-    wide_mm_body<Q4_K, NC, D, SP>(W, row_bytes, K, M, X, Y, nullptr, kmax);
+template <int F, int NC, int D, uint32_t SP>
+__global__ __launch_bounds__(GW_THREADS) void gemv_wide_mm_kernel(const uint8_t *__restrict__ W,
+                                                                  uint64_t row_bytes, uint32_t K, uint32_t M,
+                                                                  const float *__restrict__ X,
+                                                                  float *__restrict__ Y, uint32_t kmax) {
+    wide_mm_body<F, NC, D, SP>(W, row_bytes, K, M, X, Y, nullptr, kmax);
 }
 
 }  // namespace okf

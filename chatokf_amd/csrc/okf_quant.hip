@@ -185,19 +185,24 @@ enum class Path { Auto, Tile };
 // columns 53, tile 171-179; Q8_0 64 / 152; Q5_K 68 / 171; Q6_K 65 / 161;
 // Q2_K 53 / 132; Q4_0 4 columns 28 / 125 (and at 2048 x 2048 Q8_0 7.1 / 56,
 // Q2_0 2048 x 6144 11.5 / 123).
-// Q4_K with K <= 6144 (its 2..4-column matrix-core kernel fits): 4-column
-// chunks, 19.8 us each at 17408 x 5120 against 56 us for 5 columns at once.
-bool q4k_mm_fits(int32_t t, uint32_t K) { return t == Q4_K && K <= 6144; }
-uint32_t narrow_cols(int32_t t, uint32_t K) {
-    return t == IQ2_XXS || t == Q4_0 || t == IQ4_NL || q4k_mm_fits(t, K) ? 4 : 5;
+// Q4_K, Q5_K and IQ4_XS where their 2..4-column matrix-core kernel runs
+// (K <= 6144, M >= 4096): 4-column chunks, each about as long as one
+// column (17408 x 5120: Q4_K 19.8, Q5_K 22.8, IQ4_XS 21.9 us against 56.9,
+// 67.0 and 61.7 us for 5 columns at once).
+bool mm_fits(int32_t t, uint32_t M, uint32_t K) {
+    return (t == Q4_K || t == Q5_K || t == IQ4_XS) && K <= 6144 && K % 64 == 0 && M >= 4096;
+}
+uint32_t narrow_cols(int32_t t, uint32_t M, uint32_t K) {
+    return t == IQ2_XXS || t == Q4_0 || t == IQ4_NL || mm_fits(t, M, K) ? 4 : 5;
 }
 // the first N taken in chunks: 5 where a 4-column kernel is much faster
 // than the 5-column one (IQ2_XXS 19.4 + 16.3 against 52.6 us, Q4_K 19.8 +
 // 14.2 against 56.9)
-uint32_t narrow_from(int32_t t, uint32_t K) { return t == IQ2_XXS || q4k_mm_fits(t, K) ? 5 : 6; }
-uint32_t narrow_max(int32_t t, uint32_t K) {
+uint32_t narrow_from(int32_t t, uint32_t M, uint32_t K) { return t == IQ2_XXS || mm_fits(t, M, K) ? 5 : 6; }
+uint32_t narrow_max(int32_t t, uint32_t M, uint32_t K) {
+    if (mm_fits(t, M, K)) return t == Q4_K ? 16 : 24;  // (tile: Q4_K 100 us at N = 16, Q5_K 172-180)
     switch (t) {
-    case Q4_K: return q4k_mm_fits(t, K) ? 16 : 7;
+    case Q4_K: return 7;
     case IQ2_XXS: return 28;
     case Q4_0: case IQ4_NL: return 16;
     case Q5_K: case Q2_K: return 12;
@@ -220,9 +225,9 @@ int run_gemm(okf_ctx *c, const okf_weight *w, const float *X, uint32_t N, float 
     // (at M <= 4096 the 128 x 128 tile kernel runs at most 32 workgroups per
     // 128 columns: chunks win to N = 32, e.g. Q8_0 2048 x 2048 N = 28 about
     // 39 against 59 us, Q2_0 2048 x 6144 69 against 130)
-    const uint32_t nmax = std::max(narrow_max(w->ggml_type, w->K), w->M <= 4096 ? 32u : 0u);
-    if (path == Path::Auto && N >= narrow_from(w->ggml_type, w->K) && N <= nmax && !X2) {
-        const uint32_t nc = narrow_cols(w->ggml_type, w->K);
+    const uint32_t nmax = std::max(narrow_max(w->ggml_type, w->M, w->K), w->M <= 4096 ? 32u : 0u);
+    if (path == Path::Auto && N >= narrow_from(w->ggml_type, w->M, w->K) && N <= nmax && !X2) {
+        const uint32_t nc = narrow_cols(w->ggml_type, w->M, w->K);
         for (uint32_t c0 = 0; c0 < N; c0 += nc) {
             const GemvCall call{W, X + (uint64_t)c0 * w->K, Y + (uint64_t)c0 * w->M, w->M, nullptr};
             OKF_DISPATCH(w->ggml_type, launch_gemv, c, &call, 1, rb, w->K, std::min(nc, N - c0));

@@ -244,16 +244,32 @@ def test_iq2_xxs_mtp_verify_full_config(enc):
     assert r <= TOL_MV
 
 
+@pytest.mark.parametrize("t", [Q4_K, Q5_K, IQ4_XS, Q8_0], ids=lambda t: NAMES[t])
 @pytest.mark.parametrize("N", [2, 3, 4])
-def test_q4_k_narrow_full_config(enc, N):
-    # Q4_K 17408 x 5120 with 2..4 columns (the matrix-core narrow kernel)
-    t, M, K = Q4_K, 17408, 5120
+def test_narrow_mm_full_config(enc, t, N):
+    # 17408 x 5120 with 2..4 columns (the matrix-core narrow kernels; Q8_0 from 3)
+    M, K = 17408, 5120
     w = weights(t, M, K, 1003)
     X = acts(N, K, 2006)
     ref = oracle.matmul(t, w, K, M, X).astype(np.float64)
     r = rel(run_gemm(enc, t, M, K, w, X), ref)
-    say("q4_k N", N, "rel", r)
+    say(NAMES[t], "N", N, "rel", r)
     assert r <= TOL_MV
+
+
+# the same kernels on ragged shapes: rows that leave a partial row quad per
+# workgroup, K whose 64-weight units leave a partial last step
+@pytest.mark.parametrize("t", [Q4_K, Q5_K, IQ4_XS, Q8_0], ids=lambda t: NAMES[t])
+@pytest.mark.parametrize("M,K,N", [(4101, 2304, 4), (4099, 1280, 3), (5000, 768, 2), (4097, 6144, 4)])
+def test_narrow_mm_edges(enc, t, M, K, N):
+    say("narrow mm", NAMES[t], M, K, N)
+    w = weights(t, M, K, 41)
+    X = acts(N, K, 42)
+    ref = oracle.matmul(t, w, K, M, X).astype(np.float64)
+    got = run_gemm(enc, t, M, K, w, X)
+    assert rel(got, ref) <= TOL_MV
+    for n in range(N):  # each column as its own matvec
+        assert rel(got[n], run_gemm(enc, t, M, K, w, X[n:n + 1])[0].astype(np.float64)) <= 1e-5
 
 
 # ------------------------------------------- one workgroup per CU (wide)
@@ -562,18 +578,23 @@ NARROW_MAX = {Q4_K: 7, IQ2_XXS: 28, Q4_0: 16, IQ4_NL: 16, Q5_K: 12, Q2_K: 12, Q8
 NARROW_COLS = {IQ2_XXS: 4, Q4_0: 4, IQ4_NL: 4}
 
 
-def narrow_cols(t, K):
-    return 4 if t in NARROW_COLS or (t == Q4_K and K <= 6144) else 5
+def mm_fits(t, M, K):
+    return t in (Q4_K, Q5_K, IQ4_XS) and K <= 6144 and K % 64 == 0 and M >= 4096
 
 
-def narrow_chunks(t, M, N, K=0):
-    nmax = 16 if t == Q4_K and K <= 6144 else NARROW_MAX.get(t, 15)
-    first = 5 if t == IQ2_XXS or (t == Q4_K and K <= 6144) else 6
+def narrow_cols(t, M, K):
+    return 4 if t in NARROW_COLS or mm_fits(t, M, K) else 5
+
+
+def narrow_chunks(t, M, N, K):
+    nmax = (16 if t == Q4_K else 24) if mm_fits(t, M, K) else NARROW_MAX.get(t, 15)
+    first = 5 if t == IQ2_XXS or mm_fits(t, M, K) else 6
     return first <= N <= max(nmax, 32 if M <= 4096 else 0)
 CHUNKS = [(Q4_K, 260, 2304, 7), (IQ2_XXS, 129, 1536, 6), (IQ2_XXS, 1000, 1280, 28), (Q8_0, 300, 2048, 11),
           (Q2_0, 130, 1024, 13), (Q4_0, 300, 2048, 9), (IQ3_XXS, 130, 768, 15), (Q2_K, 130, 768, 12),
           (Q6_K, 129, 768, 8), (Q8_0, 2048, 2048, 32), (F32, 300, 1024, 17), (Q4_K, 4000, 2304, 20),
-          (Q4_K, 1030, 2048, 5), (IQ2_XXS, 1030, 2048, 5), (Q4_K, 300, 8192, 7)]
+          (Q4_K, 4100, 2048, 5), (IQ2_XXS, 1030, 2048, 5), (Q4_K, 300, 8192, 7), (Q5_K, 4100, 1024, 9),
+          (IQ4_XS, 4100, 1024, 6)]
 
 
 @pytest.mark.parametrize("t,M,K,N", CHUNKS)
@@ -585,7 +606,7 @@ def test_small_n_narrow_chunks(enc, t, M, K, N):
     ref = oracle.matmul(t, w, K, M, X).astype(np.float64)
     got = run_gemm(enc, t, M, K, w, X)
     assert rel(got, ref) <= TOL_MV
-    nc = narrow_cols(t, K)
+    nc = narrow_cols(t, M, K)
     for c0 in range(0, N, nc):
         assert np.array_equal(got[c0:c0 + nc], run_gemm(enc, t, M, K, w, X[c0:c0 + nc]))
 
