@@ -234,15 +234,27 @@ struct MMUnit<Q8_0> {
 // 32-weight sub-blocks): F = IQ2_XXS (weights from the replicated fp16
 // tables), Q4_K / Q5_K (weights sc * q, exact in fp16, from the nibbles and
 // the fifth bit; the mins through the per-32 activation sums staged beside
-// the scales), IQ4_XS (the levels, scale per sub-block) or Q8_0 (the int8
-// codes, scale per block).
+// the scales), IQ4_XS (the levels, scale per sub-block), Q8_0 (the int8
+// codes, scale per block), the grid formats (their signed int8 grid values
+// from the matvec's tables, copied once to LDS; a scale per 32 or per 16
+// weights) or Q2_K / Q3_K (the small codes, a scale per 16 weights and the
+// per-16 activation sums for their offsets).
 template <int F, int NC, int D, uint32_t SP>
 __device__ __forceinline__ void wide_mm_body(const uint8_t *__restrict__ W, uint64_t row_bytes, uint32_t K,
                                              uint32_t M, const float *__restrict__ X, float *__restrict__ Y,
                                              const u32x4 *__restrict__ tab_g, uint32_t kmax) {
-    static_assert(F == IQ2_XXS || F == Q4_K || F == Q5_K || F == IQ4_XS || F == Q8_0, "matrix-core narrow formats");
+    static_assert(F == IQ2_XXS || F == Q4_K || F == Q5_K || F == IQ4_XS || F == Q8_0 || F == IQ3_XXS ||
+                      F == IQ3_S || F == IQ2_XS || F == IQ2_S || F == IQ1_S || F == IQ1_M || F == Q2_K || F == Q3_K,
+                  "matrix-core narrow formats");
     constexpr bool MINS = F == Q4_K || F == Q5_K;
-    constexpr uint32_t TABR = F == IQ2_XXS ? GM_TAB : 0;
+    // (IQ2_XS, IQ2_S, IQ1_M, Q2_K, Q3_K: a scale per 16 weights, one per
+    // pair of 8-weight steps l) the activations' per-16 sums where the
+    // format subtracts a multiple of them
+    constexpr bool HSUM = F == Q2_K || F == Q3_K;
+    // tables: IQ2_XXS's fp16 rows replicated GM_COPIES times; the other grid
+    // formats' integer tables (the matvec's) once
+    constexpr uint32_t TREP = F == IQ2_XXS ? GM_COPIES : 1;
+    constexpr uint32_t TABR = F == IQ2_XXS ? GM_TAB : (F == IQ1_S || F == IQ1_M) ? 512 : itab_rows(F);
     constexpr int L = GV_L;
     constexpr uint32_t UW = 64;
     extern __shared__ u32x4 lds[];
@@ -256,15 +268,14 @@ __device__ __forceinline__ void wide_mm_body(const uint8_t *__restrict__ W, uint
     u32x4 *tab = lds;
     u32x4 *xs = lds + TABR;
     floatx4 *xf = (floatx4 *)(xs + (size_t)P * L * GM_UNIT);
-    floatx4 *xsum = xf + (size_t)P * L * 2;  // (Q4_K, Q5_K) per-32 sums of x, as xf
-    float *part = (float *)(xsum + (MINS ? (size_t)P * L * 2 : 0));
+    floatx4 *xsum = xf + (size_t)P * L * 2;  // per-32 (Q4_K, Q5_K) or per-16 (Q2_K, Q3_K) sums of x
+    float *part = (float *)(xsum + (MINS ? (size_t)P * L * 2 : HSUM ? (size_t)P * L * 4 : 0));
 
     // loads: table entries, then activations, then the weight ring
-    constexpr uint32_t TPT = TABR / GW_THREADS;
-    static_assert(TABR % GW_THREADS == 0, "table entries per thread");
+    constexpr uint32_t TPT = (TABR + GW_THREADS - 1) / GW_THREADS;
     u32x4 trow[TPT > 0 ? TPT : 1];
 #pragma unroll
-    for (uint32_t k = 0; k < TPT; k++) trow[k] = tab_g[(tid + k * GW_THREADS) / GM_COPIES];
+    for (uint32_t k = 0; k < TPT; k++) trow[k] = tab_g[min(tid + k * GW_THREADS, TABR - 1) / TREP];
     const uint32_t nx = units * 8 * 4;  // (unit, k-slot, column) entries, <= SP * 1024
     floatx4 A[SP], B[SP];
 #pragma unroll
@@ -309,7 +320,8 @@ __device__ __forceinline__ void wide_mm_body(const uint8_t *__restrict__ W, uint
     __builtin_amdgcn_sched_barrier(0);
 
 #pragma unroll
-    for (uint32_t k = 0; k < TPT; k++) tab[tid + k * GW_THREADS] = trow[k];
+    for (uint32_t k = 0; k < TPT; k++)
+        if (tid + k * GW_THREADS < TABR) tab[tid + k * GW_THREADS] = trow[k];
 #pragma unroll
     for (uint32_t p = 0; p < SP; p++) {
         // (c, sl, u) = lane bits 0-1, 2-4, 5-: a 32-weight group of column c
@@ -323,14 +335,14 @@ __device__ __forceinline__ void wide_mm_body(const uint8_t *__restrict__ W, uint
         m = fmaxf(m, __shfl_xor(m, 4, 64));
         m = fmaxf(m, __shfl_xor(m, 8, 64));
         const int ex = min(__builtin_amdgcn_frexp_expf(m), 127);
-        float sx = 0;  // (Q4_K, Q5_K) the group's sum of x, in order within a slot
-        if constexpr (MINS) {
+        float sx = 0;  // (MINS, HSUM) the group's (half group's) sum of x
+        if constexpr (MINS || HSUM) {
 #pragma unroll
             for (int k = 0; k < 4; k++) sx += A[p][k];
 #pragma unroll
             for (int k = 0; k < 4; k++) sx += B[p][k];
             sx += __shfl_xor(sx, 4, 64);
-            sx += __shfl_xor(sx, 8, 64);
+            if constexpr (MINS) sx += __shfl_xor(sx, 8, 64);
         }
         floatx4 Ah, Al, Bh, Bl;
 #pragma unroll
@@ -355,6 +367,8 @@ __device__ __forceinline__ void wide_mm_body(const uint8_t *__restrict__ W, uint
                 ((float *)xf)[(u * 2 + (sl >> 2)) * 4 + c] = f;
                 if constexpr (MINS) ((float *)xsum)[(u * 2 + (sl >> 2)) * 4 + c] = sx;
             }
+            if constexpr (HSUM)
+                if ((sl & 1) == 0) ((float *)xsum)[(u * 4 + (sl >> 1)) * 4 + c] = sx;
         }
     }
     __syncthreads();
@@ -391,9 +405,10 @@ __device__ __forceinline__ void wide_mm_body(const uint8_t *__restrict__ W, uint
                                        (u & 3), sc[0], mn[0], sc[1], mn[1]);
 #pragma unroll
                 for (int sb = 0; sb < 2; sb++) {
-                    floatx4 acc = {0, 0, 0, 0};
+                    floatx4 acc2[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};  // steps l = 0, 1 and 2, 3
 #pragma unroll
                     for (int l = 0; l < 4; l++) {
+                        floatx4 &acc = acc2[l >> 1];
                         const u32x4 xv = xp[(4 * sb + l) * 4], xl = xp[32 + (4 * sb + l) * 4];
                         u32x4 wv;
                         if constexpr (F == IQ2_XXS) {
@@ -427,18 +442,78 @@ __device__ __forceinline__ void wide_mm_body(const uint8_t *__restrict__ W, uint
                                 wv[i] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(
                                                                          __builtin_bit_cast(half2v, e4[i]), s2, o2));
                         } else {
-                            // int8 weights (IQ4_XS: the levels of the nibbles,
-                            // weight j of a sub-block in byte j % 16's low (j <
-                            // 16) or high nibble; Q8_0: the codes) as fp16
+                            // int8 weights as fp16: IQ4_XS the levels of the
+                            // nibbles (weight j of a sub-block in byte j % 16's
+                            // low (j < 16) or high nibble), Q8_0 the codes, the
+                            // grid formats their signed grid values (the
+                            // matvec's tables and v_perm selection), Q2_K the
+                            // 2-bit fields, Q3_K q + 4 hbit
                             uint32_t b0, b1;
+                            const uint2 *t2 = (const uint2 *)tab;
+                            const int e = l & 1;
                             if constexpr (F == IQ4_XS) {
                                 const u32x4 &cq = sb ? w.q1[0] : w.q0[0];
                                 const uint32_t sh = 4 * (l >> 1), i0 = 2 * (l & 1);
                                 b0 = IQ4Levels::levels((cq[i0] >> sh) & 0x0F0F0F0Fu);
                                 b1 = IQ4Levels::levels((cq[i0 + 1] >> sh) & 0x0F0F0F0Fu);
-                            } else {
+                            } else if constexpr (F == Q8_0) {
                                 b0 = w.q[sb][l >> 1][2 * (l & 1)];
                                 b1 = w.q[sb][l >> 1][2 * (l & 1) + 1];
+                            } else if constexpr (F == IQ3_XXS || F == IQ3_S) {
+                                const uint32_t qd = w.q[0][2 * sb + (l >> 1)];
+                                uint32_t i1 = (qd >> (16 * e)) & 0xFF, i2 = (qd >> (16 * e + 8)) & 0xFF, sv;
+                                if constexpr (F == IQ3_S) {
+                                    const uint32_t qh = (w.qh[0] >> (8 * sb)) & 0xFF;
+                                    i1 |= (qh << (8 - 2 * l)) & 256;
+                                    i2 |= (qh << (7 - 2 * l)) & 256;
+                                    sv = 512 + (((sb ? w.sg[0].y : w.sg[0].x) >> (8 * l)) & 0xFF);
+                                } else {
+                                    sv = 256 + (((sb ? w.aux[0].y : w.aux[0].x) >> (7 * l)) & 127);
+                                }
+                                const uint2 g1 = t2[i1], g2 = t2[i2], sg = t2[sv];
+                                b0 = perm(g1.y, g1.x, sg.x);
+                                b1 = perm(g2.y, g2.x, sg.y);
+                            } else if constexpr (F == IQ2_XS || F == IQ2_S) {
+                                uint32_t idx, sv;
+                                if constexpr (F == IQ2_S) {
+                                    const uint32_t qd = sb ? w.q[0].y : w.q[0].x, qh = (w.qh[0] >> (8 * sb)) & 0xFF;
+                                    idx = ((qd >> (8 * l)) & 0xFF) | ((qh << (8 - 2 * l)) & 0x300);
+                                    sv = 1024 + (((sb ? w.sg[0].y : w.sg[0].x) >> (8 * l)) & 0xFF);
+                                } else {
+                                    const uint32_t q16 = (w.q[0][2 * sb + (l >> 1)] >> (16 * e)) & 0xFFFF;
+                                    idx = q16 & 511;
+                                    sv = 512 + (q16 >> 9);
+                                }
+                                const uint2 gv = t2[idx], sg = t2[sv];
+                                b0 = perm(IQ2_NEG, IQ2_POS, gv.x + sg.x - 0x03020100u);
+                                b1 = perm(IQ2_NEG, IQ2_POS, gv.y + sg.y - 0x03020100u);
+                            } else if constexpr (F == IQ1_S || F == IQ1_M) {
+                                const uint32_t qd = sb ? w.q[0].y : w.q[0].x;
+                                uint32_t hb, neg;
+                                if constexpr (F == IQ1_S) {
+                                    const uint32_t qh = (w.qh[0] >> (16 * sb)) & 0xFFFF;
+                                    hb = (qh >> (3 * l)) & 7;
+                                    neg = qh >> 15;
+                                } else {
+                                    const uint32_t hq = (w.qh[0] >> (16 * sb + 8 * (l >> 1))) & 0xFF;
+                                    hb = (hq >> (4 * e)) & 7;
+                                    neg = (hq >> (4 * e + 3)) & 1;
+                                }
+                                const uint32_t gv = ((const uint32_t *)tab)[((qd >> (8 * l)) & 0xFF) | (hb << 8)];
+                                const uint32_t nm = neg ? 0x04040404u : 0u;
+                                b0 = perm(0x0007FFF7u, 0x000901F9u, (gv & 0x0F0F0F0Fu) | nm);
+                                b1 = perm(0x0007FFF7u, 0x000901F9u, ((gv >> 4) & 0x0F0F0F0Fu) | nm);
+                            } else {  // Q2_K, Q3_K: group j = 2 (u % 4) + sb, half l / 2
+                                const uint32_t jg = 2 * (u & 3) + sb, sh = 2 * (jg & 3);
+                                const u32x4 &cq = (l >> 1) ? w.q1[0] : w.q0[0];
+                                b0 = (cq[2 * e] >> sh) & 0x03030303u;
+                                b1 = (cq[2 * e + 1] >> sh) & 0x03030303u;
+                                if constexpr (F == Q3_K) {
+                                    const uint32_t hbit = 4 * (jg >> 2) + (jg & 3);
+                                    const u32x4 &hq = (l >> 1) ? w.h1[0] : w.h0[0];
+                                    b0 |= ((hq[2 * e] >> hbit) & 0x01010101u) << 2;
+                                    b1 |= ((hq[2 * e + 1] >> hbit) & 0x01010101u) << 2;
+                                }
                             }
                             const half2v m2 = {(_Float16)-1152.0f, (_Float16)-1152.0f};
                             uint32_t e4[4];
@@ -458,6 +533,7 @@ __device__ __forceinline__ void wide_mm_body(const uint8_t *__restrict__ W, uint
                         }
                     }
                     const uint32_t uc = min(u, units - 1);
+                    const floatx4 acc = acc2[0] + acc2[1];
                     if constexpr (F == IQ2_XXS) {
                         const float db = live ? h2f(w.d[0]) * (0.5f + (float)(w.a[0][2 * sb + 1] >> 28)) * 0.25f : 0.0f;
                         tot += db * (acc * xf[uc * 2 + sb]);
@@ -470,9 +546,50 @@ __device__ __forceinline__ void wide_mm_body(const uint8_t *__restrict__ W, uint
                         const uint32_t ls = ((slo >> (4 * sb)) & 0xF) | (((shi >> (4 * g + 2 * sb)) & 3) << 4);
                         const float dl = live ? h2f(w.hdr[0].x & 0xFFFF) * (float)((int)ls - 32) : 0.0f;
                         tot += dl * (acc * xf[uc * 2 + sb]);
-                    } else {
+                    } else if constexpr (F == Q8_0) {
                         const float d = live ? h2f(w.d[sb]) : 0.0f;
                         tot += d * (acc * xf[uc * 2 + sb]);
+                    } else if constexpr (F == IQ3_XXS) {
+                        const uint32_t aux = sb ? w.aux[0].y : w.aux[0].x;
+                        const float db = live ? h2f(w.d[0]) * (0.5f + (float)(aux >> 28)) * 0.5f : 0.0f;
+                        tot += db * (acc * xf[uc * 2 + sb]);
+                    } else if constexpr (F == IQ3_S) {
+                        const float db = live ? h2f(w.d[0]) * (float)(1 + 2 * ((w.sc[0] >> (4 * sb)) & 0xF)) : 0.0f;
+                        tot += db * (acc * xf[uc * 2 + sb]);
+                    } else if constexpr (F == IQ1_S) {
+                        const uint32_t qh = (w.qh[0] >> (16 * sb)) & 0xFFFF;
+                        const float db = live ? h2f(w.d[0]) * (float)(2 * ((qh >> 12) & 7) + 1) * 0.125f : 0.0f;
+                        tot += db * (acc * xf[uc * 2 + sb]);
+                    } else {
+                        // HALF: a scale per 16 weights (acc2[0]: weights 0-15)
+                        const floatx4 f = xf[uc * 2 + sb];
+#pragma unroll
+                        for (int h = 0; h < 2; h++) {
+                            float dl = 0, ml = 0;
+                            if constexpr (F == IQ2_XS || F == IQ2_S) {
+                                dl = h2f(w.d[0]) * (0.5f + (float)((w.sc[0] >> (8 * sb + 4 * h)) & 0xF)) * 0.25f;
+                            } else if constexpr (F == IQ1_M) {
+                                const uint32_t a = w.sc[0].x, b = w.sc[0].y;
+                                const uint32_t bits = ((a & 0xFFFF) >> 12) | ((a >> 24) & 0x00f0) |
+                                                      (((b & 0xFFFF) >> 4) & 0x0f00) | ((b >> 16) & 0xf000);
+                                const uint32_t sv = w.sw[0] >> (6 * sb);
+                                dl = h2f((uint16_t)bits) * (float)(2 * ((sv >> (3 * h)) & 7) + 1) * 0.125f;
+                            } else if constexpr (F == Q2_K) {
+                                const uint32_t scb = (w.sc[0] >> (16 * sb + 8 * h)) & 0xFF;
+                                dl = h2f(w.dd[0] & 0xFFFF) * (float)(scb & 0xF);
+                                ml = h2f(w.dd[0] >> 16) * (float)(scb >> 4);
+                            } else {  // Q3_K: scale i of the superblock, dl (sum (q + 4 hbit) x - 4 sum x)
+                                const uint32_t jg = 2 * (u & 3) + sb, i = (jg >> 2) * 8 + (jg & 3) * 2 + h;
+                                const uint32_t lo8 = (i & 7) < 4 ? w.s8[0].x : w.s8[0].y;
+                                const uint32_t lo = (lo8 >> (8 * (i & 3) + 4 * (i >> 3))) & 0xF;
+                                const uint32_t hi = (w.s4[0] >> (8 * (i & 3) + 2 * (i >> 2))) & 3;
+                                dl = h2f(w.d[0]) * (float)((int)(lo | (hi << 4)) - 32);
+                                ml = 4.0f * dl;
+                            }
+                            if (!live) dl = ml = 0.0f;
+                            tot += dl * (acc2[h] * f);
+                            if constexpr (HSUM) tot -= ml * xsum[uc * 4 + sb * 2 + h];
+                        }
                     }
                 }
                 if (++su == P && st + j + 1 < s1) {  // next step starts a row quad
@@ -516,8 +633,9 @@ template <int F, int NC, int D, uint32_t SP>
 __global__ __launch_bounds__(GW_THREADS) void gemv_wide_mm_kernel(const uint8_t *__restrict__ W,
                                                                   uint64_t row_bytes, uint32_t K, uint32_t M,
                                                                   const float *__restrict__ X,
-                                                                  float *__restrict__ Y, uint32_t kmax) {
-    wide_mm_body<F, NC, D, SP>(W, row_bytes, K, M, X, Y, nullptr, kmax);
+                                                                  float *__restrict__ Y,
+                                                                  const u32x4 *__restrict__ tab_g, uint32_t kmax) {
+    wide_mm_body<F, NC, D, SP>(W, row_bytes, K, M, X, Y, tab_g, kmax);
 }
 
 }  // namespace okf

@@ -48,7 +48,7 @@ struct okf_ctx {
     int gemv_sb_rw = 0;  // its rows per workgroup (0 = auto)
     int gemv_sb_t = 0;   // its threads per workgroup (0 = auto)
     int gemm_ks = 0;     // wide-tile GEMM: K ranges per remainder tile (0 = auto)
-    int q4k_mm = 15;     // 2..4 columns on the matrix cores, bits: Q4_K, Q5_K, IQ4_XS, Q8_0 (0: the dot4 kernels)
+    int q4k_mm = 0xFFF;  // 2..4 columns on the matrix cores, bits mm_bit(F) (0: the dot4 kernels)
     int gemm_thin = 0;   // leftover-tile kernel variant (A/B switch)
     int gemm_ng = 4;     // wide-tile GEMM: N tiles that share an XCD's row blocks
     uint32_t cus = 256;  // compute units of the device
@@ -248,23 +248,33 @@ bool launch_iq2mm(okf_ctx *c, const GemvCall &call, uint64_t rb, uint32_t K) {
     return true;
 }
 
-// Q4_K, Q5_K, IQ4_XS and Q8_0 with 2..4 columns on the matrix cores
-// (gemv_wide_mm_kernel): true when launched.
+// The formats with a matrix-core 2..4-column kernel, and their bit in
+// okf_ctx::q4k_mm.
+constexpr int mm_bit(int f) {
+    return f == Q4_K ? 0 : f == Q5_K ? 1 : f == IQ4_XS ? 2 : f == Q8_0 ? 3 : f == IQ3_XXS ? 4 : f == IQ3_S ? 5
+         : f == IQ2_XS ? 6 : f == IQ2_S ? 7 : f == IQ1_S ? 8 : f == IQ1_M ? 9 : f == Q2_K ? 10 : f == Q3_K ? 11 : -1;
+}
+
+// Q4_K, Q5_K, IQ4_XS, Q8_0, the grid formats, Q2_K and Q3_K with 2..4
+// columns on the matrix cores (gemv_wide_mm_kernel): true when launched.
 template <int F, int NC>
 bool launch_widemm(okf_ctx *c, const GemvCall &call, uint64_t rb, uint32_t K) {
     // (measured on MI355X: at M = 2048 the many-workgroup dot4 kernels are
     // faster, e.g. Q8_0 2048 x 2048 N = 2 5.6 against 14.6 us; Q8_0 at N = 2
     // also at 17408 x 5120, 29.6 against 35.4)
-    if (!(c->q4k_mm & (1 << (F == Q4_K ? 0 : F == Q5_K ? 1 : F == IQ4_XS ? 2 : 3))) || K % 64 ||
-        call.M < 4096 || (F == Q8_0 && NC < 3))
-        return false;
-    constexpr bool MINS = F == Q4_K || F == Q5_K;
+    static_assert(mm_bit(F) >= 0, "matrix-core narrow format");
+    if (!(c->q4k_mm & (1 << mm_bit(F))) || K % 64 || call.M < 4096 || (F == Q8_0 && NC < 3)) return false;
+    constexpr bool MINS = F == Q4_K || F == Q5_K, HSUM = F == Q2_K || F == Q3_K;
+    constexpr uint32_t TABR = (F == IQ1_S || F == IQ1_M) ? 512 : itab_rows(F);
     const uint32_t G = std::min(c->cus, call.M), units = K / 64, P = (units + GV_L - 1) / GV_L;
     const uint64_t nq = ((call.M + G - 1) / G + 3) / 4, lmax = (nq * P + GM_WAVES - 1) / GM_WAVES;
     const uint32_t kmax = (uint32_t)((lmax + P - 1) / P + 1);
-    const size_t lds = (size_t)P * GV_L * (GM_UNIT + (MINS ? 4 : 2)) * 16 + (size_t)GM_WAVES * kmax * 4 * NC * 4;
+    const size_t lds = (size_t)TABR * 16 + (size_t)P * GV_L * (GM_UNIT + (MINS ? 4 : HSUM ? 6 : 2)) * 16 +
+                       (size_t)GM_WAVES * kmax * 4 * NC * 4;
     const uint32_t sp = (units * 32 + GW_THREADS - 1) / GW_THREADS;
     if (lds > c->max_lds || sp > 3 || nq * P * GM_WAVES >= (1ull << 32)) return false;
+    const u32x4 *tab = itab_rows(F) ? c->tab8 + itab_at(F)
+                     : TABR ? (const u32x4 *)(c->grids + gt_off(F)) : nullptr;
     constexpr int D = 2;
     auto go = [&](auto spc) {
         constexpr uint32_t SP = decltype(spc)::value;
@@ -272,7 +282,7 @@ bool launch_widemm(okf_ctx *c, const GemvCall &call, uint64_t rb, uint32_t K) {
         static std::atomic<uint64_t> attr{0};  // devices that have the attribute set
         set_lds_attr(c, fn, attr);
         hipLaunchKernelGGL((gemv_wide_mm_kernel<F, NC, D, SP>), dim3(G), dim3(GW_THREADS), lds, c->stream,
-                           call.W, rb, K, call.M, call.X, call.Y, kmax);
+                           call.W, rb, K, call.M, call.X, call.Y, tab, kmax);
     };
     if (sp <= 1) go(std::integral_constant<uint32_t, 1>{});
     else if (sp == 2) go(std::integral_constant<uint32_t, 2>{});
@@ -377,7 +387,7 @@ bool launch_gemv_sb(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint3
 template <int F, int NC, bool SILU = false>
 void launch_gemv_nc(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32_t K) {
     if (launch_gemv_sb<F, NC, SILU>(c, calls, n, rb, K)) return;
-    if constexpr ((F == Q4_K || F == Q5_K || F == IQ4_XS || F == Q8_0) && !SILU && NC >= 2 && NC <= 4)
+    if constexpr (mm_bit(F) >= 0 && !SILU && NC >= 2 && NC <= 4)
         if (n == 1 && launch_widemm<F, NC>(c, calls[0], rb, K)) return;
     // (Q4_K and Q8_0 units are too large for a deep ring at N > 1; the
     // formats added after the measurements take the many-workgroup kernel)

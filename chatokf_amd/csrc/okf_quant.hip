@@ -185,12 +185,14 @@ enum class Path { Auto, Tile };
 // columns 53, tile 171-179; Q8_0 64 / 152; Q5_K 68 / 171; Q6_K 65 / 161;
 // Q2_K 53 / 132; Q4_0 4 columns 28 / 125 (and at 2048 x 2048 Q8_0 7.1 / 56,
 // Q2_0 2048 x 6144 11.5 / 123).
-// Q4_K, Q5_K and IQ4_XS where their 2..4-column matrix-core kernel runs
-// (K <= 6144, M >= 4096): 4-column chunks, each about as long as one
-// column (17408 x 5120: Q4_K 19.8, Q5_K 22.8, IQ4_XS 21.9 us against 56.9,
-// 67.0 and 61.7 us for 5 columns at once).
+// The formats whose 2..4-column matrix-core kernel runs (K <= 6144, M >=
+// 4096), Q8_0 aside: 4-column chunks, each about as long as one column
+// (17408 x 5120: Q4_K 19.8, Q5_K 22.8, IQ4_XS 21.9 us against 56.9, 67.0
+// and 61.7 us for 5 columns at once; the grid formats 17.4-21.4 against
+// 48-53 for 4 columns on the dot4 kernel, Q2_K 17.9 / 43.2, Q3_K 32.0 /
+// 53.5).
 bool mm_fits(int32_t t, uint32_t M, uint32_t K) {
-    return (t == Q4_K || t == Q5_K || t == IQ4_XS) && K <= 6144 && K % 64 == 0 && M >= 4096;
+    return mm_bit(t) >= 0 && t != Q8_0 && K <= 6144 && K % 64 == 0 && M >= 4096;
 }
 uint32_t narrow_cols(int32_t t, uint32_t M, uint32_t K) {
     return t == IQ2_XXS || t == Q4_0 || t == IQ4_NL || mm_fits(t, M, K) ? 4 : 5;
@@ -200,7 +202,12 @@ uint32_t narrow_cols(int32_t t, uint32_t M, uint32_t K) {
 // 14.2 against 56.9)
 uint32_t narrow_from(int32_t t, uint32_t M, uint32_t K) { return t == IQ2_XXS || mm_fits(t, M, K) ? 5 : 6; }
 uint32_t narrow_max(int32_t t, uint32_t M, uint32_t K) {
-    if (mm_fits(t, M, K)) return t == Q4_K ? 16 : 24;  // (tile: Q4_K 100 us at N = 16, Q5_K 172-180)
+    // (17408 x 5120, chunks against the tile kernel, us: Q4_K N = 16 about
+    // 80 / 100; Q5_K N = 24 130 / 176; IQ3_XXS N = 32 160 / 177, IQ1_S 145 /
+    // 156; IQ1_M N = 24 122 / 139, 32 157 / 143; Q2_K N = 24 112 / 140, 32
+    // 145 / 143; Q3_K N = 16 135 / 162, 24 197 / 165)
+    if (mm_fits(t, M, K))
+        return t == Q4_K || t == Q3_K ? 16 : (t == Q5_K || t == IQ4_XS || t == IQ1_M) ? 24 : t == Q2_K ? 28 : 32;
     switch (t) {
     case Q4_K: return 7;
     case IQ2_XXS: return 28;

@@ -145,11 +145,11 @@ int okf_silu_mul(okf_ctx *ctx, float *a, const float *b, uint32_t n);
  * policy as the reference: N == 1 -> gemv; 2 <= N <= 5 -> narrow (one weight
  * pass serving all N columns, gemmNarrow / gemmNarrowIQ :176-239);
  * N > 5 -> MFMA tile GEMM (gemmTiled / iqGemmTiled, :354-400), except that
- * a small N past 5 (up to a per-format bound, 7..28 columns, and 32 when
+ * a small N past 5 (up to a per-format bound, 7..32 columns, and 32 when
  * M <= 4096) runs as consecutive narrow launches of 4 or 5 columns, which
- * fill the GPU where the tile grid would not (for IQ2_XXS, and for Q4_K,
- * Q5_K and IQ4_XS with K <= 6144 and M >= 4096, from N = 5 on, in 4-column
- * launches).  The results are the
+ * fill the GPU where the tile grid would not (for IQ2_XXS, and for every
+ * other K-quant and i-quant format but Q6_K and IQ4_NL with K <= 6144 and
+ * M >= 4096, from N = 5 on, in 4-column launches).  The results are the
  * narrow kernels' for those N. */
 int okf_gemm(okf_ctx *ctx, const okf_weight *w, const float *X, uint32_t N, float *Y);
 

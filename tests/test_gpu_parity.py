@@ -244,7 +244,10 @@ def test_iq2_xxs_mtp_verify_full_config(enc):
     assert r <= TOL_MV
 
 
-@pytest.mark.parametrize("t", [Q4_K, Q5_K, IQ4_XS, Q8_0], ids=lambda t: NAMES[t])
+MM_FMTS = [Q4_K, Q5_K, IQ4_XS, Q8_0, IQ3_XXS, IQ3_S, IQ2_XS, IQ2_S, IQ1_S, IQ1_M, Q2_K, Q3_K]
+
+
+@pytest.mark.parametrize("t", MM_FMTS, ids=lambda t: NAMES[t])
 @pytest.mark.parametrize("N", [2, 3, 4])
 def test_narrow_mm_full_config(enc, t, N):
     # 17408 x 5120 with 2..4 columns (the matrix-core narrow kernels; Q8_0 from 3)
@@ -259,7 +262,7 @@ def test_narrow_mm_full_config(enc, t, N):
 
 # the same kernels on ragged shapes: rows that leave a partial row quad per
 # workgroup, K whose 64-weight units leave a partial last step
-@pytest.mark.parametrize("t", [Q4_K, Q5_K, IQ4_XS, Q8_0], ids=lambda t: NAMES[t])
+@pytest.mark.parametrize("t", MM_FMTS, ids=lambda t: NAMES[t])
 @pytest.mark.parametrize("M,K,N", [(4101, 2304, 4), (4099, 1280, 3), (5000, 768, 2), (4097, 6144, 4)])
 def test_narrow_mm_edges(enc, t, M, K, N):
     say("narrow mm", NAMES[t], M, K, N)
@@ -579,7 +582,10 @@ NARROW_COLS = {IQ2_XXS: 4, Q4_0: 4, IQ4_NL: 4}
 
 
 def mm_fits(t, M, K):
-    return t in (Q4_K, Q5_K, IQ4_XS) and K <= 6144 and K % 64 == 0 and M >= 4096
+    return t in MM_FMTS and t != Q8_0 and K <= 6144 and K % 64 == 0 and M >= 4096
+
+
+MM_MAX = {Q4_K: 16, Q3_K: 16, Q5_K: 24, IQ4_XS: 24, IQ1_M: 24, Q2_K: 28}
 
 
 def narrow_cols(t, M, K):
@@ -587,14 +593,15 @@ def narrow_cols(t, M, K):
 
 
 def narrow_chunks(t, M, N, K):
-    nmax = (16 if t == Q4_K else 24) if mm_fits(t, M, K) else NARROW_MAX.get(t, 15)
+    nmax = MM_MAX.get(t, 32) if mm_fits(t, M, K) else NARROW_MAX.get(t, 15)
     first = 5 if t == IQ2_XXS or mm_fits(t, M, K) else 6
     return first <= N <= max(nmax, 32 if M <= 4096 else 0)
 CHUNKS = [(Q4_K, 260, 2304, 7), (IQ2_XXS, 129, 1536, 6), (IQ2_XXS, 1000, 1280, 28), (Q8_0, 300, 2048, 11),
           (Q2_0, 130, 1024, 13), (Q4_0, 300, 2048, 9), (IQ3_XXS, 130, 768, 15), (Q2_K, 130, 768, 12),
           (Q6_K, 129, 768, 8), (Q8_0, 2048, 2048, 32), (F32, 300, 1024, 17), (Q4_K, 4000, 2304, 20),
           (Q4_K, 4100, 2048, 5), (IQ2_XXS, 1030, 2048, 5), (Q4_K, 300, 8192, 7), (Q5_K, 4100, 1024, 9),
-          (IQ4_XS, 4100, 1024, 6)]
+          (IQ4_XS, 4100, 1024, 6), (IQ3_S, 4100, 1024, 30), (IQ1_M, 4099, 768, 9), (Q3_K, 4100, 1280, 13),
+          (Q2_K, 4200, 1024, 27), (IQ2_S, 4096, 512, 32), (IQ1_S, 4097, 1536, 5)]
 
 
 @pytest.mark.parametrize("t,M,K,N", CHUNKS)
