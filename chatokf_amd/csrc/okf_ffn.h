@@ -1,0 +1,264 @@
+// okf_ffn.h -- the FFN block of one token (gate, up, SiLU, down) in one
+// cooperative launch, for the ternary Q2_0 blocks of the Bonsai FFN
+// (LLM/Qwen/QwenMetalEngine.swift:918-929: MetalEnc.parallel { gemv(gate);
+// gemv(up) }, siluMul, gemv(down)).
+//
+// The three weight matrices of this FFN are small (3.3 MB each at 6144 x
+// 2048), so as separate launches every kernel pays its own start-up: the
+// first weight bytes arrive a full HBM latency after the launch, and the
+// down projection cannot even request its weights before gate and up are
+// done.  Here every lane requests all of its weights of both phases at the
+// kernel's start (a few units per lane: the whole FFN fits in the
+// registers of a co-resident grid), then
+//   phase A: x staged as digit planes; each wavefront takes row pairs (gate
+//            row r on lanes 0-31, up row r on lanes 32-63) and writes
+//            g[r] = silu(gate x) * (up x), u[r] = up x;
+//   a grid-wide barrier (all workgroups are resident: cooperative launch);
+//   phase B: g staged as digit planes; each wavefront takes down rows
+//            (units lane, lane + 64, ...) and writes y.
+// The arithmetic per unit is the exact digit-plane scheme of okf_gemv.h;
+// each row's lanes add their partial sums in a fixed shuffle order, so the
+// results are deterministic.
+#pragma once
+#include "okf_gemv.h"
+
+namespace okf {
+
+constexpr uint32_t FF_SPIN = 1u << 20;  // barrier polls before giving up (~0.3 s)
+// the barrier's words, each on its own 256-byte line: FF_SUB arrival
+// counters, the top counter, FF_SUB release flags, the time-out flag
+constexpr uint32_t FF_SUB = 8, FF_LINE = 64;
+constexpr uint32_t FF_TOP = FF_SUB * FF_LINE, FF_FLAG = FF_TOP + FF_LINE;
+constexpr uint32_t FF_TIMEOUT = FF_FLAG + FF_SUB * FF_LINE;
+constexpr size_t FF_BAR_BYTES = (FF_TIMEOUT + FF_LINE) * 4;
+
+struct FfnArgs {
+    const uint8_t *wg, *wu, *wd;
+    uint64_t rba, rbb;    // row bytes of gate / up, of down
+    uint32_t ka, ma, mb;  // gate / up K and M (= down K), down M
+    const float *x;
+    float *g, *u, *y;
+    uint32_t *bar;  // FF_BAR_BYTES, zero before the first launch
+};
+
+// Grid-wide barrier for a grid whose workgroups are all resident, in two
+// levels, so that no word takes more than a few dozen atomics (same-address
+// atomics are served one at a time): workgroup b arrives at counter
+// b % FF_SUB; the last of each subgroup arrives at the top counter; the last
+// of those resets the counters and advances all FF_SUB release flags
+// (whatever the grid, so they stay equal); workgroup b polls flag b % FF_SUB.
+// The polls are bounded: after FF_SPIN of them a workgroup goes on and
+// reports false, so no wave waits forever.
+//
+// Memory: the data exchanged across the barrier (g) is written with
+// device-scope stores (written through to memory) and read with
+// device-scope loads (which miss any stale line in this XCD's L2), and
+// __syncthreads waits for each wave's stores to complete before the
+// arrival.  So the barrier needs no cache-wide write-back or invalidate:
+// device-scope fences here, one per wave, each flushing or invalidating a
+// whole L2, made the kernel take 60 us.
+__device__ __forceinline__ bool ff_grid_sync(uint32_t *bar) {
+    __shared__ uint32_t ok;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        ok = 1;
+        const uint32_t nb = gridDim.x, s = blockIdx.x % FF_SUB, nsub = min(nb, FF_SUB);
+        const uint32_t members = (nb - s + FF_SUB - 1) / FF_SUB;  // workgroups b with b % FF_SUB == s
+        uint32_t *flag = bar + FF_FLAG + s * FF_LINE;
+        const uint32_t gen = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        bool wait = true;
+        if (__hip_atomic_fetch_add(bar + s * FF_LINE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 ==
+            members) {
+            __hip_atomic_store(bar + s * FF_LINE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (__hip_atomic_fetch_add(bar + FF_TOP, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 == nsub) {
+                __hip_atomic_store(bar + FF_TOP, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+                for (uint32_t k = 0; k < FF_SUB; k++)
+                    __hip_atomic_store(bar + FF_FLAG + k * FF_LINE, gen + 1, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                wait = false;
+            }
+        }
+        for (uint32_t it = 0; wait && __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gen;
+             it++) {
+            if (it == FF_SPIN) {
+                __hip_atomic_store(bar + FF_TIMEOUT, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                ok = 0;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+    __syncthreads();
+    return ok != 0;
+}
+
+// a device-scope store of one float (see ff_grid_sync)
+__device__ __forceinline__ void ff_put(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Staging of n values v (n / UW units) as digit planes and group data for
+// Compute<F, 1, 1>, in the layout of xs_index<F, GV_L>, in rounds of one
+// 8-value slot per thread.  Every thread of the workgroup takes part (a quad
+// of lanes shares each 32-value group; nslots and the round bases are
+// multiples of 4, so quads are whole).  ff_load_x / ff_stage_x split it so
+// that the loads can go first: loads complete in issue order, so the
+// staging must not sit behind the weight loads.
+template <int F, int T, int XR>
+__device__ __forceinline__ void ff_load_x(const float *v, uint32_t n, float (&s)[XR][1][8]) {
+    constexpr uint32_t SL = unit_weights<F>() / 8;
+    const uint32_t nslots = n / unit_weights<F>() * SL;
+#pragma unroll
+    for (int k = 0; k < XR; k++) {
+        const uint32_t q = min(k * T + threadIdx.x, nslots - 1), uu = q / SL;
+        load_slot<F>(v + unit_x_base<F>(uu), q % SL, s[k][0]);
+    }
+}
+template <int F, int T, int XR>
+__device__ __forceinline__ void ff_stage_x(const float (&s)[XR][1][8], uint32_t n, uint32_t *xs, floatx4 *&gdp) {
+    constexpr int L = GV_L;
+    constexpr uint32_t UW = unit_weights<F>(), SL = UW / 8, UG = unit_groups<F>();
+    const uint32_t units = n / UW, cu = (units + L - 1) / L * L, cs = cu * unit_chunks<F>() * 4;
+    gdp = (floatx4 *)(xs + cs);
+    const uint32_t nslots = units * SL;
+#pragma unroll
+    for (int k = 0; k < XR; k++) {
+        const uint32_t q0 = k * T + threadIdx.x, q = min(q0, nslots - 1);
+        if (k * T < nslots)  // (the whole workgroup)
+            stage_slot<F, 1, L, false>(s[k], q / SL, q % SL, q0 < nslots, xs, cs, gdp, cu * UG);
+    }
+}
+// g (written by other workgroups behind the grid barrier) staged the same
+// way, read with device-scope loads, 8 bytes each, all issued before the
+// staging: the 8 values of a slot are those load_slot<Q2_0> reads,
+// x[16 j + 4 b + k0] and x[16 j + 4 b + k0 + 1] (b < 4).
+template <int F, int T, int XR>
+__device__ __forceinline__ void ff_stage_g(const float *v, uint32_t n, uint32_t *xs, floatx4 *&gdp) {
+    static_assert(F == Q2_0, "the slot order of load_slot<Q2_0>");
+    constexpr uint32_t SL = unit_weights<F>() / 8;
+    const uint32_t nslots = n / unit_weights<F>() * SL;
+    float s[XR][1][8];
+#pragma unroll
+    for (int k = 0; k < XR; k++) {
+        const uint32_t q = min(k * T + threadIdx.x, nslots - 1), uu = q / SL;
+        const uint64_t *xu = (const uint64_t *)(v + unit_x_base<F>(uu) + 16 * ((q % SL) >> 1) + 2 * (q & 1));
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const float2 t = __builtin_bit_cast(
+                float2, __hip_atomic_load(xu + 2 * b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+            s[k][0][b] = t.x;
+            s[k][0][4 + b] = t.y;
+        }
+    }
+    ff_stage_x<F, T, XR>(s, n, xs, gdp);
+}
+
+template <int F>
+__device__ __forceinline__ uint32_t ff_cs(uint32_t n) {
+    const uint32_t units = n / unit_weights<F>(), cu = (units + GV_L - 1) / GV_L * GV_L;
+    return cu * unit_chunks<F>() * 4;
+}
+
+// T threads a workgroup; UA: units per lane of a gate / up row (32 lanes a
+// row), UB: of a down row (64 lanes a row).  Wavefront w takes row pairs
+// w + p W (p < RA) and down rows w + p W (p < RB), W = the grid's
+// wavefronts (host-checked).
+template <int F, int T, int UA, int UB, int RA, int RB>
+__global__ __launch_bounds__(T) void ffn_fused_kernel(FfnArgs a) {
+    constexpr uint32_t FF_WAVES = T / 64;
+    constexpr int L = GV_L;
+    constexpr uint32_t UW = unit_weights<F>(), UG = unit_groups<F>();
+    extern __shared__ u32x4 lds[];
+    uint32_t *xs = (uint32_t *)lds;
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t W = gridDim.x * FF_WAVES, w0 = blockIdx.x * FF_WAVES + (tid >> 6);
+    const uint32_t una = a.ka / UW, unb = a.ma / UW;
+    const uint32_t half = lane >> 5, lh = lane & 31;
+
+    // x's loads, then every weight load of both phases; x of gate / up is at
+    // most UA * 32 units, UA rounds of slots.  The loads are unconditional
+    // (rows past the end re-read the last row): loads under a branch make
+    // the compiler wait for all of them before the staging.
+    constexpr int XR = (UA * 32 * unit_weights<F>() / 8 + T - 1) / T;
+    float xv[XR][1][8];
+    ff_load_x<F, T, XR>(a.x, a.ka, xv);
+    __builtin_amdgcn_sched_barrier(0);
+    Unit<F, 1> wa[RA][UA];
+    Unit<F, 1> wb[RB][UB];
+#pragma unroll
+    for (int p = 0; p < RA; p++) {
+        const uint32_t r = min(w0 + p * W, a.ma - 1);
+        const uint8_t *rows[1] = {(half ? a.wu : a.wg) + (uint64_t)r * a.rba};
+#pragma unroll
+        for (int j = 0; j < UA; j++) load_unit<F, 1>(rows, min(lh + 32 * j, una - 1), wa[p][j]);
+    }
+#pragma unroll
+    for (int p = 0; p < RB; p++) {
+        const uint32_t r = min(w0 + p * W, a.mb - 1);
+        const uint8_t *rows[1] = {a.wd + (uint64_t)r * a.rbb};
+#pragma unroll
+        for (int j = 0; j < UB; j++) load_unit<F, 1>(rows, min(lane + 64 * j, unb - 1), wb[p][j]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // phase A: gate and up
+    floatx4 *gdp;
+    ff_stage_x<F, T, XR>(xv, a.ka, xs, gdp);
+    __syncthreads();
+    {
+        const uint32_t cs = ff_cs<F>(a.ka), gcs = cs / (unit_chunks<F>() * 4) * UG;
+#pragma unroll
+        for (int p = 0; p < RA; p++) {
+            const uint32_t r = w0 + p * W;
+            if (r < a.ma) {  // (the whole wavefront)
+                float acc[1][1] = {{0.0f}};
+#pragma unroll
+                for (int j = 0; j < UA; j++) {
+                    const uint32_t uu = lh + 32 * j;
+                    if (uu < una)
+                        Compute<F, 1, 1>::run(wa[p][j], XLds{xs + xs_index<F, L>(uu, 0), 4 * L, cs, gdp + uu * UG, gcs},
+                                              uu, acc, nullptr);
+                }
+                float v = acc[0][0];
+#pragma unroll
+                for (int m = 16; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+                const float up = __shfl(v, 32, 64);
+                if (lane == 0) {
+                    ff_put(a.g + r, silu_mul1(v, up));
+                    a.u[r] = up;
+                }
+            }
+        }
+    }
+    const bool synced = ff_grid_sync(a.bar);
+
+    // phase B: down on g (staged after the barrier, so every row of it is in)
+    constexpr int XB = (UB * 64 * unit_weights<F>() / 8 + T - 1) / T;
+    ff_stage_g<F, T, XB>(a.g, a.ma, xs, gdp);
+    __syncthreads();
+    {
+        const uint32_t cs = ff_cs<F>(a.ma), gcs = cs / (unit_chunks<F>() * 4) * UG;
+#pragma unroll
+        for (int p = 0; p < RB; p++) {
+            const uint32_t r = w0 + p * W;
+            if (r < a.mb) {
+                float acc[1][1] = {{0.0f}};
+#pragma unroll
+                for (int j = 0; j < UB; j++) {
+                    const uint32_t uu = lane + 64 * j;
+                    if (uu < unb)
+                        Compute<F, 1, 1>::run(wb[p][j], XLds{xs + xs_index<F, L>(uu, 0), 4 * L, cs, gdp + uu * UG, gcs},
+                                              uu, acc, nullptr);
+                }
+                float v = acc[0][0];
+#pragma unroll
+                for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+                // a barrier that timed out leaves NaN, never a plausible y
+                if (lane == 0) a.y[r] = synced ? v : __builtin_nanf("");
+            }
+        }
+    }
+}
+
+}  // namespace okf

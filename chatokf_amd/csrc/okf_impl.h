@@ -22,6 +22,7 @@
 #include "okf_gemv.h"
 #include "okf_gemv_wide.h"
 #include "okf_gemv_sb.h"
+#include "okf_ffn.h"
 
 // one matvec y = W x of a launch group (with X2: x = silu(X) * X2)
 struct GemvCall {
@@ -72,6 +73,12 @@ struct okf_ctx {
     size_t cnt_n = 0;
     bool reserved = false;    // okf_ctx_reserve fixed the scratch sizes: no growth
     uint8_t *scratch = nullptr;  // this device's copy of the static scratch array
+    uint32_t *ffn_bar = nullptr;  // the one-launch FFN's grid barrier (zeroed at creation)
+    int ffn_fused = 1;            // okf_ffn as one cooperative launch where it fits (0: two launches)
+    int ffn_wg = 1;               // its workgroups per CU, at most
+    int ffn_coop = 0;             // launched with hipLaunchCooperativeKernel (1) or as a plain grid
+    int ffn_nb[3] = {0, 0, 0};    // its kernels' resident workgroups per CU (0: not yet queried)
+    int ffn_t = 0;                // its exact-fit variant: threads a workgroup (0: the default, 512)
 };
 
 namespace okf_impl {
@@ -445,6 +452,11 @@ void launch_gemv_pair(okf_ctx *c, const GemvCall *calls, uint64_t rb, uint32_t K
     if (cunits * per_unit > budget) cunits = (uint32_t)(budget / per_unit) / 64 * 64;
     launch_gemv_s<F, 1, 1, false>(c, calls, 2, rb, K, cunits, tab + cunits * per_unit + red, true);
 }
+
+// The FFN block of Q2_0 gate / up / down in one cooperative launch
+// (okf_fmt_q2_0.hip): false, with nothing launched, where its shape or the
+// device does not fit it.
+bool launch_ffn_fused(okf_ctx *c, const FfnArgs &a);
 
 // The context's scratch (split-tile partial sums, argmax pairs), grown to at
 // least `need` bytes; the stream is drained before an old buffer is freed.

@@ -361,7 +361,10 @@ int okf_ctx_create(int device, okf_ctx **out) {
             return OKF_E_HIP;
         }
         if (e == hipSuccess) e = hipGetSymbolAddress((void **)&c->scratch, HIP_SYMBOL(scratch));
+        if (e == hipSuccess) e = hipMalloc((void **)&c->ffn_bar, FF_BAR_BYTES);
+        if (e == hipSuccess) e = hipMemset(c->ffn_bar, 0, FF_BAR_BYTES);
         if (e != hipSuccess) {
+            if (c->ffn_bar) (void)hipFree(c->ffn_bar);
             if (c->grid) (void)hipFree(c->grid);
             if (c->grids) (void)hipFree(c->grids);
             if (c->tab) (void)hipFree(c->tab);
@@ -386,6 +389,10 @@ int okf_ctx_create(int device, okf_ctx **out) {
         if (const char *e = getenv("OKF_GEMM_NG")) c->gemm_ng = atoi(e);
         if (const char *e = getenv("OKF_GEMM_THIN")) c->gemm_thin = atoi(e);
         if (const char *e = getenv("OKF_Q4K_MM")) c->q4k_mm = atoi(e);
+        if (const char *e = getenv("OKF_FFN_FUSED")) c->ffn_fused = atoi(e);
+        if (const char *e = getenv("OKF_FFN_WG")) c->ffn_wg = atoi(e);
+        if (const char *e = getenv("OKF_FFN_COOP")) c->ffn_coop = atoi(e);
+        if (const char *e = getenv("OKF_FFN_T")) c->ffn_t = atoi(e);
     } else if (device != -1) {
         delete c;
         return OKF_E_ARG;
@@ -407,6 +414,7 @@ int okf_ctx_destroy(okf_ctx *c) {
         if (c->xh) (void)hipFree(c->xh);
         if (c->part) (void)hipFree(c->part);
         if (c->cnt) (void)hipFree(c->cnt);
+        if (c->ffn_bar) (void)hipFree(c->ffn_bar);
         (void)hipStreamDestroy(c->stream);
     }
     delete c;
@@ -490,6 +498,19 @@ int okf_ffn(okf_ctx *c, const okf_weight *gate, const okf_weight *up, const okf_
     if (st) return st;
     if (!gate || !y) return OKF_E_ARG;
     if (down->K != gate->M) return OKF_E_SHAPE;
+    if (gate->ggml_type == Q2_0 && up && up->ggml_type == Q2_0 && down->ggml_type == Q2_0 && c && !c->grouping) {
+        // the ternary FFN in one launch where it fits
+        uint64_t rb0 = 0, rb0u = 0;
+        if ((st = check_weight(gate, &rb0)) || (st = check_weight(up, &rb0u))) return st;
+        if (!x || !g || !u) return OKF_E_ARG;
+        if (gate->K != up->K || gate->M != up->M) return OKF_E_SHAPE;
+        if (!aligned16(x) || !aligned16(g) || !aligned16(u)) return OKF_E_SHAPE;
+        if ((st = begin(c))) return st;
+        const FfnArgs a{(const uint8_t *)gate->base + gate->off, (const uint8_t *)up->base + up->off,
+                        (const uint8_t *)down->base + down->off, rb0, rb1, gate->K, gate->M, down->M,
+                        x, g, u, y, nullptr};
+        if (launch_ffn_fused(c, a)) return finish(c);
+    }
     if ((st = okf_gemv_gate_up(c, gate, up, x, g, u))) return st;
     const GemvCall dn{(const uint8_t *)down->base + down->off, g, y, down->M};
     OKF_DISPATCH(down->ggml_type, launch_gemv, c, &dn, 1, rb1, down->K, 1u);

@@ -131,10 +131,12 @@ int okf_gemv_gate_up(okf_ctx *ctx, const okf_weight *gate, const okf_weight *up,
  * 918-929: MetalEnc.parallel { gemv(gate); gemv(up) }, siluMul, gemv(down)):
  * u = W_up x, g = silu(W_gate x) * u, y = W_down g.  As in the reference,
  * whose siluMul works in place on the gate buffer, g holds silu(gate) * up
- * after the call.  Two launches when gate and up share a format: one grid
- * whose workgroups each compute the same rows of gate and up and form
- * silu(g) * u there, then the down projection.  down->K must equal gate->M;
- * x, g, u 16-byte aligned. */
+ * after the call.  With Q2_0 gate, up and down (gate / up K <= 4096, M <=
+ * 8192) one launch: gate and up, a grid-wide barrier, then down, every
+ * weight requested at the start.  Otherwise two launches when gate and up
+ * share a format: one grid whose workgroups each compute the same rows of
+ * gate and up and form silu(g) * u there, then the down projection.
+ * down->K must equal gate->M; x, g, u 16-byte aligned. */
 int okf_ffn(okf_ctx *ctx, const okf_weight *gate, const okf_weight *up, const okf_weight *down, const float *x,
             float *g, float *u, float *y);
 

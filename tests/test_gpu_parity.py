@@ -472,7 +472,8 @@ FFN = [(Q2_0, Q2_0, Q2_0, 6144, 2048, 1002), (Q4_K, Q4_K, Q4_K, 768, 512, 31), (
        (Q8_0, Q8_0, Q8_0, 320, 2080, 33), (Q2_0, Q2_0, Q2_0, 256, 1024, 34),
        (Q4_K, Q4_K, Q8_0, 512, 768, 35),  # (down's format differs)
        (Q4_K, Q8_0, Q2_0, 256, 512, 36),  # (gate's and up's formats differ: no pairing)
-       (Q2_0, Q2_0, Q8_0, 224, 1024, 37)]
+       (Q2_0, Q2_0, Q8_0, 224, 1024, 37),
+       (Q2_0, Q2_0, Q2_0, 8192, 4096, 38), (Q2_0, Q2_0, Q2_0, 384, 640, 39)]
 
 
 @pytest.mark.parametrize("tg,tu,td,H,D,seed", FFN)
@@ -496,6 +497,41 @@ def test_ffn_matches_oracle(enc, tg, tu, td, H, D, seed):
         r = rel(host(y), ry)
         say("  rel", r)
         assert r <= TOL_MV
+
+
+# The all-Q2_0 FFN runs as one cooperative launch (gate and up, a grid-wide
+# barrier, down); OKF_FFN_FUSED=0 keeps the two launches.  Both compute every
+# unit exactly and differ only in the order of the fp32 partial sums, and
+# each is deterministic: a second call gives the same bits.
+@pytest.fixture(scope="module")
+def enc_ffn2():
+    import os
+    os.environ["OKF_FFN_FUSED"] = "0"
+    try:
+        e = ok.Enc(0)
+    finally:
+        del os.environ["OKF_FFN_FUSED"]
+    yield e
+    e.close()
+
+
+@pytest.mark.parametrize("H,D,seed", [(6144, 2048, 1002), (8192, 4096, 38), (384, 640, 39), (128, 128, 40)])
+def test_ffn_one_launch_matches_two(enc, enc_ffn2, H, D, seed):
+    say("ffn one launch", H, D)
+    wg, wu, wd = weights(Q2_0, H, D, seed), weights(Q2_0, H, D, seed + 1), weights(Q2_0, D, H, seed + 2)
+    qg, qu, qd = (ok.QuantTensor(dev(w), k, m, Q2_0) for w, k, m in ((wg, D, H), (wu, D, H), (wd, H, D)))
+    x = dev(acts(1, D, seed + 10)[0])
+    outs = []
+    for e in (enc, enc, enc_ffn2):
+        g, u = (torch.full((H,), float("nan"), device="cuda") for _ in range(2))
+        y = torch.full((D,), float("nan"), device="cuda")
+        e.ffn(qg, qu, qd, x, g, u, y)
+        e.sync()
+        outs.append([host(v).astype(np.float64) for v in (g, u, y)])
+    for a, b in zip(outs[0], outs[1]):
+        assert np.array_equal(a, b)
+    for a, b in zip(outs[0], outs[2]):
+        assert rel(a, b) <= 1e-5
 
 
 @pytest.mark.parametrize("tg,tu,H,D,seed", [(Q2_0, Q2_0, 6144, 2048, 51), (Q2_0, Q2_0, 40, 1024, 52),
