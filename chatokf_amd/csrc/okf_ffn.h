@@ -25,11 +25,11 @@
 namespace okf {
 
 constexpr uint32_t FF_SPIN = 1u << 20;  // barrier polls before giving up (~0.3 s)
-// the barrier's words, each on its own 256-byte line: FF_SUB arrival
-// counters, the top counter, FF_SUB release flags, the time-out flag
+// the barrier's words, each on its own 256-byte line (FF_LINE uint32):
+// FF_SUB 64-bit arrival counters, FF_SUB 64-bit release flags, the
+// time-out flag
 constexpr uint32_t FF_SUB = 8, FF_LINE = 64;
-constexpr uint32_t FF_TOP = FF_SUB * FF_LINE, FF_FLAG = FF_TOP + FF_LINE;
-constexpr uint32_t FF_TIMEOUT = FF_FLAG + FF_SUB * FF_LINE;
+constexpr uint32_t FF_FLAG = FF_SUB * FF_LINE, FF_TIMEOUT = 2 * FF_SUB * FF_LINE;
 constexpr size_t FF_BAR_BYTES = (FF_TIMEOUT + FF_LINE) * 4;
 
 struct FfnArgs {
@@ -41,54 +41,75 @@ struct FfnArgs {
     uint32_t *bar;  // FF_BAR_BYTES, zero before the first launch
 };
 
-// Grid-wide barrier for a grid whose workgroups are all resident, in two
-// levels, so that no word takes more than a few dozen atomics (same-address
-// atomics are served one at a time): workgroup b arrives at counter
-// b % FF_SUB; the last of each subgroup arrives at the top counter; the last
-// of those resets the counters and advances all FF_SUB release flags
-// (whatever the grid, so they stay equal); workgroup b polls flag b % FF_SUB.
-// The polls are bounded: after FF_SPIN of them a workgroup goes on and
-// reports false, so no wave waits forever.
+// Grid-wide barrier for a grid whose workgroups are all resident.  The
+// grid is split into FF_SUB subgroups (workgroup b in b % FF_SUB), each with
+// a 64-bit arrival counter and a 64-bit release flag, every word on its own
+// 256-byte line.  The counters only ever grow (every launch adds each
+// subgroup's size: every launch on them has the same grid), and the flags
+// hold the epoch, the number of barriers passed.  A workgroup reads its
+// subgroup's flag (the epoch e) and then, once that read is back, adds one
+// to its counter without waiting for the result.  Workgroup 0's first
+// wavefront polls the counters (lane k counter k) until each reaches
+// (e + 1) times its subgroup's size, then sets every flag to e + 1; the
+// other workgroups poll their flag.  So the atomics meet no polling on
+// their lines, and only one wavefront polls them.  The polls are bounded:
+// after FF_SPIN of them a workgroup goes on and reports false, so no wave
+// waits forever.
 //
 // Memory: the data exchanged across the barrier (g) is written with
-// device-scope stores (written through to memory) and read with
-// device-scope loads (which miss any stale line in this XCD's L2), and
-// __syncthreads waits for each wave's stores to complete before the
-// arrival.  So the barrier needs no cache-wide write-back or invalidate:
+// device-scope stores (coherent at device scope once acknowledged) and read
+// with device-scope loads (which miss any stale line in this XCD's L2), and
+// every wave waits for its stores to be acknowledged (s_waitcnt, which
+// __syncthreads does not do for global memory) before the workgroup
+// arrives.  So the barrier needs no cache-wide write-back or invalidate:
 // device-scope fences here, one per wave, each flushing or invalidating a
 // whole L2, made the kernel take 60 us.
 __device__ __forceinline__ bool ff_grid_sync(uint32_t *bar) {
+    __shared__ uint64_t epoch;
     __shared__ uint32_t ok;
+    uint64_t *cnt = (uint64_t *)bar;             // counter k at cnt[k * FF_LINE / 2]
+    uint64_t *flag = (uint64_t *)(bar + FF_FLAG);  // flag k at flag[k * FF_LINE / 2]
+    const uint32_t nb = gridDim.x, s = blockIdx.x % FF_SUB;
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's stores of g acknowledged
     __syncthreads();
     if (threadIdx.x == 0) {
+        const uint64_t e = __hip_atomic_load(flag + s * (FF_LINE / 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        epoch = e;
         ok = 1;
-        const uint32_t nb = gridDim.x, s = blockIdx.x % FF_SUB, nsub = min(nb, FF_SUB);
-        const uint32_t members = (nb - s + FF_SUB - 1) / FF_SUB;  // workgroups b with b % FF_SUB == s
-        uint32_t *flag = bar + FF_FLAG + s * FF_LINE;
-        const uint32_t gen = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        bool wait = true;
-        if (__hip_atomic_fetch_add(bar + s * FF_LINE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 ==
-            members) {
-            __hip_atomic_store(bar + s * FF_LINE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (__hip_atomic_fetch_add(bar + FF_TOP, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 == nsub) {
-                __hip_atomic_store(bar + FF_TOP, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-                for (uint32_t k = 0; k < FF_SUB; k++)
-                    __hip_atomic_store(bar + FF_FLAG + k * FF_LINE, gen + 1, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-                wait = false;
-            }
-        }
-        for (uint32_t it = 0; wait && __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gen;
-             it++) {
+        // the added value depends on e (e < 2^63: it is 1), so the add is
+        // issued only once the read is back
+        __hip_atomic_fetch_add(cnt + s * (FF_LINE / 2), 1 + (e >> 63), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    const uint64_t e = epoch;
+    if (blockIdx.x == 0 && threadIdx.x < 64) {
+        const uint32_t k = threadIdx.x, mk = k < FF_SUB ? (nb - k + FF_SUB - 1) / FF_SUB : 0;
+        const uint64_t target = (e + 1) * mk;
+        bool done = k >= FF_SUB || mk == 0;
+        for (uint32_t it = 0;; it++) {
+            if (!done)
+                done = __hip_atomic_load(cnt + k * (FF_LINE / 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >=
+                       target;
+            if (__all(done)) break;
             if (it == FF_SPIN) {
-                __hip_atomic_store(bar + FF_TIMEOUT, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (k == 0) ok = 0;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (k < FF_SUB)
+            __hip_atomic_store(flag + k * (FF_LINE / 2), e + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else if (threadIdx.x == 0) {
+        for (uint32_t it = 0;
+             __hip_atomic_load(flag + s * (FF_LINE / 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == e; it++) {
+            if (it == FF_SPIN) {
                 ok = 0;
                 break;
             }
             __builtin_amdgcn_s_sleep(1);
         }
     }
+    if (threadIdx.x == 0 && !ok) __hip_atomic_store(bar + FF_TIMEOUT, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     return ok != 0;
 }

@@ -4,9 +4,9 @@
 namespace okf_impl {
 OKF_INSTANTIATE(Q2_0)
 
-// ffn_fused_kernel on one workgroup per CU (okf_ctx::ffn_wg), all resident
-// (the grid is sized by the occupancy query, so every workgroup has a CU;
-// the barrier's polls are bounded all the same): the exact fits of the
+// ffn_fused_kernel on one workgroup per CU (okf_ctx::ffn_wg, the same for
+// every launch of a context), all resident (the occupancy query must allow
+// it; the barrier's polls are bounded all the same): the exact fits of the
 // Bonsai FFN (gate / up 6144 x 2048, down 2048 x 6144 on 256 CUs; with 512
 // threads a workgroup 3 row pairs and 1 down row per wavefront, with 256
 // threads 6 and 2; no load re-reads a row), or the general instance for
@@ -44,8 +44,11 @@ bool launch_ffn_fused(okf_ctx *c, const FfnArgs &a0) {
                 nb = -1;
             }
         }
-        if (nb < 1) return false;
-        const uint32_t G = (uint32_t)std::min(nb, std::max(c->ffn_wg, 1)) * c->cus, W = G * (k.threads / 64);
+        // every launch on the context's barrier counters has the same grid
+        // (ff_grid_sync derives its epoch from it): ffn_wg workgroups a CU
+        const int wg = std::max(c->ffn_wg, 1);
+        if (nb < wg) return false;
+        const uint32_t G = (uint32_t)wg * c->cus, W = G * (k.threads / 64);
         const uint32_t ra = (a0.ma + W - 1) / W, rb = (a0.mb + W - 1) / W;
         if (k.ra ? (una > 32 || unb <= 64 || ra != k.ra || rb != k.rb) : (ra > 4 || rb > 2)) continue;
         FfnArgs a = a0;
