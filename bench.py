@@ -196,7 +196,7 @@ def main():
         # gate and up in one parallel group, as the reference's FFN encodes
         # them (LLM/Qwen/QwenMetalEngine.swift:918-923, MetalEnc.parallel),
         # then down on silu(gate) * up (siluMul + gemv, :924-928): one
-        # okf_ffn call per step (one cooperative launch: gate and up, a grid
+        # okf_ffn call per step (one launch: gate and up, a grid
         # barrier, down; OKF_FFN_FUSED=0 gives the two-launch form)
         pbegin, pend, hctx = enc._lib.okf_parallel_begin, enc._lib.okf_parallel_end, enc.h
         ffn_c = enc._lib.okf_ffn

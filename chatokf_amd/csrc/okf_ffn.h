@@ -1,5 +1,5 @@
 // okf_ffn.h -- the FFN block of one token (gate, up, SiLU, down) in one
-// cooperative launch, for the ternary Q2_0 blocks of the Bonsai FFN
+// launch, for the ternary Q2_0 blocks of the Bonsai FFN
 // (LLM/Qwen/QwenMetalEngine.swift:918-929: MetalEnc.parallel { gemv(gate);
 // gemv(up) }, siluMul, gemv(down)).
 //
@@ -13,7 +13,8 @@
 //   phase A: x staged as digit planes; each wavefront takes row pairs (gate
 //            row r on lanes 0-31, up row r on lanes 32-63) and writes
 //            g[r] = silu(gate x) * (up x), u[r] = up x;
-//   a grid-wide barrier (all workgroups are resident: cooperative launch);
+//   a grid-wide barrier (all workgroups are resident: one per CU, a grid
+//            the occupancy query allows);
 //   phase B: g staged as digit planes; each wavefront takes down rows
 //            (units lane, lane + 64, ...) and writes y.
 // The arithmetic per unit is the exact digit-plane scheme of okf_gemv.h;

@@ -74,7 +74,7 @@ struct okf_ctx {
     bool reserved = false;    // okf_ctx_reserve fixed the scratch sizes: no growth
     uint8_t *scratch = nullptr;  // this device's copy of the static scratch array
     uint32_t *ffn_bar = nullptr;  // the one-launch FFN's grid barrier (zeroed at creation)
-    int ffn_fused = 1;            // okf_ffn as one cooperative launch where it fits (0: two launches)
+    int ffn_fused = 1;            // okf_ffn as one launch with a grid barrier where it fits (0: two launches)
     int ffn_wg = 1;               // its workgroups per CU, at most
     int ffn_coop = 0;             // launched with hipLaunchCooperativeKernel (1) or as a plain grid
     int ffn_nb[3] = {0, 0, 0};    // its kernels' resident workgroups per CU (0: not yet queried)
@@ -453,7 +453,7 @@ void launch_gemv_pair(okf_ctx *c, const GemvCall *calls, uint64_t rb, uint32_t K
     launch_gemv_s<F, 1, 1, false>(c, calls, 2, rb, K, cunits, tab + cunits * per_unit + red, true);
 }
 
-// The FFN block of Q2_0 gate / up / down in one cooperative launch
+// The FFN block of Q2_0 gate / up / down in one launch (grid barrier)
 // (okf_fmt_q2_0.hip): false, with nothing launched, where its shape or the
 // device does not fit it.
 bool launch_ffn_fused(okf_ctx *c, const FfnArgs &a);
