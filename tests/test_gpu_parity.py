@@ -515,6 +515,48 @@ def enc_ffn2():
     e.close()
 
 
+# The one-launch FFN captured into a HIP graph on the context's stream and
+# replayed: its grid barrier keeps its state in counters that only grow, so
+# every replay must synchronise as a fresh launch does.  Each replay runs on
+# a new x (written into the captured buffer), with eager calls between the
+# replays, and must give the eager call's bits for that x.
+def test_ffn_graph_replay(enc):
+    hip = ctypes.CDLL("libamdhip64.so")
+    vp = ctypes.c_void_p
+    H, D = 6144, 2048
+    wg, wu, wd = weights(Q2_0, H, D, 51), weights(Q2_0, H, D, 52), weights(Q2_0, D, H, 53)
+    qg, qu, qd = (ok.QuantTensor(dev(w), k, m, Q2_0) for w, k, m in ((wg, D, H), (wu, D, H), (wd, H, D)))
+    x = dev(acts(1, D, 60)[0])
+    g, u = torch.zeros(H, device="cuda"), torch.zeros(H, device="cuda")
+    y = torch.zeros(D, device="cuda")
+    ge, ue, ye = torch.zeros(H, device="cuda"), torch.zeros(H, device="cuda"), torch.zeros(D, device="cuda")
+    enc.ffn(qg, qu, qd, x, g, u, y)  # (first call outside the capture)
+    enc.sync()
+    st = vp(enc.stream)
+    graph, exe = vp(), vp()
+    assert hip.hipStreamBeginCapture(st, 0) == 0  # hipStreamCaptureModeGlobal
+    enc.ffn(qg, qu, qd, x, g, u, y)
+    assert hip.hipStreamEndCapture(st, ctypes.byref(graph)) == 0
+    assert hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0) == 0
+    try:
+        for rep in range(4):
+            say("ffn graph replay", rep)
+            x.copy_(dev(acts(1, D, 70 + rep)[0]))
+            torch.cuda.synchronize()
+            enc.ffn(qg, qu, qd, x, ge, ue, ye)  # eager, same x
+            enc.sync()
+            g.fill_(float("nan"))
+            y.fill_(float("nan"))
+            torch.cuda.synchronize()
+            assert hip.hipGraphLaunch(exe, st) == 0
+            assert hip.hipStreamSynchronize(st) == 0
+            for a, b in ((g, ge), (u, ue), (y, ye)):
+                assert np.array_equal(host(a), host(b))
+    finally:
+        hip.hipGraphExecDestroy(exe)
+        hip.hipGraphDestroy(graph)
+
+
 @pytest.mark.parametrize("H,D,seed", [(6144, 2048, 1002), (8192, 4096, 38), (384, 640, 39), (128, 128, 40)])
 def test_ffn_one_launch_matches_two(enc, enc_ffn2, H, D, seed):
     say("ffn one launch", H, D)
