@@ -25,7 +25,7 @@
 
 namespace okf {
 
-constexpr uint32_t FF_SPIN = 1u << 20;  // barrier polls before giving up (~0.3 s)
+constexpr uint32_t FF_SPIN = 1u << 20;  // default barrier polls before giving up (~0.3 s)
 // the barrier's words, each on its own 256-byte line (FF_LINE uint32):
 // FF_SUB 64-bit arrival counters, FF_SUB 64-bit release flags, the
 // time-out flag
@@ -40,6 +40,8 @@ struct FfnArgs {
     const float *x;
     float *g, *u, *y;
     uint32_t *bar;  // FF_BAR_BYTES, zero before the first launch
+    uint32_t spin;  // polls before a waiting workgroup gives up
+    uint32_t stall;  // 1: the barrier waits for one arrival more than the grid has (time-out tests)
 };
 
 // Grid-wide barrier for a grid whose workgroups are all resident.  The
@@ -54,8 +56,10 @@ struct FfnArgs {
 // (e + 1) times its subgroup's size, then sets every flag to e + 1; the
 // other workgroups poll their flag.  So the atomics meet no polling on
 // their lines, and only one wavefront polls them.  The polls are bounded:
-// after FF_SPIN of them a workgroup goes on and reports false, so no wave
-// waits forever.
+// after `spin` of them a workgroup goes on and reports false, so no wave
+// waits forever; the master then still advances the flags, so the
+// counters and flags agree for the next launch.  `stall` (a test of that
+// path) makes the master wait for one arrival too many.
 //
 // Memory: the data exchanged across the barrier (g) is written with
 // device-scope stores (coherent at device scope once acknowledged) and read
@@ -65,7 +69,7 @@ struct FfnArgs {
 // arrives.  So the barrier needs no cache-wide write-back or invalidate:
 // device-scope fences here, one per wave, each flushing or invalidating a
 // whole L2, made the kernel take 60 us.
-__device__ __forceinline__ bool ff_grid_sync(uint32_t *bar) {
+__device__ __forceinline__ bool ff_grid_sync(uint32_t *bar, uint32_t spin, uint32_t stall) {
     __shared__ uint64_t epoch;
     __shared__ uint32_t ok;
     uint64_t *cnt = (uint64_t *)bar;             // counter k at cnt[k * FF_LINE / 2]
@@ -85,14 +89,14 @@ __device__ __forceinline__ bool ff_grid_sync(uint32_t *bar) {
     const uint64_t e = epoch;
     if (blockIdx.x == 0 && threadIdx.x < 64) {
         const uint32_t k = threadIdx.x, mk = k < FF_SUB ? (nb - k + FF_SUB - 1) / FF_SUB : 0;
-        const uint64_t target = (e + 1) * mk;
+        const uint64_t target = (e + 1) * mk + (k == 0 ? stall : 0);
         bool done = k >= FF_SUB || mk == 0;
         for (uint32_t it = 0;; it++) {
             if (!done)
                 done = __hip_atomic_load(cnt + k * (FF_LINE / 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >=
                        target;
             if (__all(done)) break;
-            if (it == FF_SPIN) {
+            if (it == spin) {
                 if (k == 0) ok = 0;
                 break;
             }
@@ -103,7 +107,7 @@ __device__ __forceinline__ bool ff_grid_sync(uint32_t *bar) {
     } else if (threadIdx.x == 0) {
         for (uint32_t it = 0;
              __hip_atomic_load(flag + s * (FF_LINE / 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == e; it++) {
-            if (it == FF_SPIN) {
+            if (it == spin) {
                 ok = 0;
                 break;
             }
@@ -253,7 +257,7 @@ __global__ __launch_bounds__(T) void ffn_fused_kernel(FfnArgs a) {
             }
         }
     }
-    const bool synced = ff_grid_sync(a.bar);
+    const bool synced = ff_grid_sync(a.bar, a.spin, a.stall);
 
     // phase B: down on g (staged after the barrier, so every row of it is in)
     constexpr int XB = (UB * 64 * unit_weights<F>() / 8 + T - 1) / T;

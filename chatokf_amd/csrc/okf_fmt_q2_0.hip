@@ -53,6 +53,8 @@ bool launch_ffn_fused(okf_ctx *c, const FfnArgs &a0) {
         if (k.ra ? (una > 32 || unb <= 64 || ra != k.ra || rb != k.rb) : (ra > 4 || rb > 2)) continue;
         FfnArgs a = a0;
         a.bar = c->ffn_bar;
+        a.spin = c->ffn_spin > 0 ? (uint32_t)c->ffn_spin : FF_SPIN;
+        a.stall = c->ffn_stall > 0 ? 1u : 0u;
         void *args[] = {&a};
         const hipError_t e =
             c->ffn_coop ? hipLaunchCooperativeKernel(k.fn, dim3(G), dim3(k.threads), args, (unsigned)lds, c->stream)
@@ -61,6 +63,7 @@ bool launch_ffn_fused(okf_ctx *c, const FfnArgs &a0) {
             (void)hipGetLastError();
             return false;
         }
+        if (c->ffn_stall > 0) c->ffn_stall--;
         return true;
     }
     return false;

@@ -393,6 +393,8 @@ int okf_ctx_create(int device, okf_ctx **out) {
         if (const char *e = getenv("OKF_FFN_WG")) c->ffn_wg = atoi(e);
         if (const char *e = getenv("OKF_FFN_COOP")) c->ffn_coop = atoi(e);
         if (const char *e = getenv("OKF_FFN_T")) c->ffn_t = atoi(e);
+        if (const char *e = getenv("OKF_FFN_SPIN")) c->ffn_spin = atoi(e);
+        if (const char *e = getenv("OKF_FFN_STALL")) c->ffn_stall = atoi(e);
     } else if (device != -1) {
         delete c;
         return OKF_E_ARG;

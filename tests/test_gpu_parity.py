@@ -557,6 +557,37 @@ def test_ffn_graph_replay(enc):
         hip.hipGraphDestroy(graph)
 
 
+# The grid barrier's bounded wait, forced from the host: OKF_FFN_STALL=1
+# makes the next launch's barrier wait for one arrival more than the grid
+# has, OKF_FFN_SPIN a short poll limit.  Every workgroup still finishes; the
+# call must fail loudly (NaN in y, never a plausible wrong value), and the
+# next call on the same context must give the normal result, bit for bit.
+def test_ffn_barrier_timeout_is_loud_and_recovers(enc):
+    import os
+    os.environ["OKF_FFN_STALL"], os.environ["OKF_FFN_SPIN"] = "1", "2000"
+    try:
+        e = ok.Enc(0)
+    finally:
+        del os.environ["OKF_FFN_STALL"], os.environ["OKF_FFN_SPIN"]
+    try:
+        H, D = 6144, 2048
+        wg, wu, wd = weights(Q2_0, H, D, 81), weights(Q2_0, H, D, 82), weights(Q2_0, D, H, 83)
+        qg, qu, qd = (ok.QuantTensor(dev(w), k, m, Q2_0) for w, k, m in ((wg, D, H), (wu, D, H), (wd, H, D)))
+        x = dev(acts(1, D, 84)[0])
+        outs = []
+        for en in (e, e, enc):
+            say("ffn barrier time-out", len(outs))
+            g, u = torch.zeros(H, device="cuda"), torch.zeros(H, device="cuda")
+            y = torch.zeros(D, device="cuda")
+            en.ffn(qg, qu, qd, x, g, u, y)
+            en.sync()
+            outs.append(host(y))
+        assert np.isnan(outs[0]).any()
+        assert np.array_equal(outs[1], outs[2])
+    finally:
+        e.close()
+
+
 @pytest.mark.parametrize("H,D,seed", [(6144, 2048, 1002), (8192, 4096, 38), (384, 640, 39), (128, 128, 40)])
 def test_ffn_one_launch_matches_two(enc, enc_ffn2, H, D, seed):
     say("ffn one launch", H, D)
