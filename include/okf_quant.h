@@ -133,7 +133,11 @@ int okf_gemv_gate_up(okf_ctx *ctx, const okf_weight *gate, const okf_weight *up,
  * whose siluMul works in place on the gate buffer, g holds silu(gate) * up
  * after the call.  With Q2_0 gate, up and down (gate / up K <= 4096, M <=
  * 8192) one launch: gate and up, a grid-wide barrier, then down, every
- * weight requested at the start.  Otherwise two launches when gate and up
+ * weight requested at the start.  That launch needs one workgroup resident
+ * on every CU at once: work that a caller keeps running on other streams of
+ * the same GPU can delay it, and a barrier that waits past its bound
+ * (about 0.3 s) leaves NaN in y rather than wait forever
+ * (OKF_FFN_FUSED=0 at okf_ctx_create selects the two launches).  Otherwise two launches when gate and up
  * share a format: one grid whose workgroups each compute the same rows of
  * gate and up and form silu(g) * u there, then the down projection.
  * down->K must equal gate->M; x, g, u 16-byte aligned. */
