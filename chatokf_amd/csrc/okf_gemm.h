@@ -33,13 +33,17 @@ __device__ __forceinline__ void zero_half32(_Float16 *dst) {
     for (int i = 0; i < 4; i++) *(half8 *)(dst + i * 8) = half8{};
 }
 
+// K split: workgroup z of the grid's third dimension takes K range
+// [z kper, (z + 1) kper) (kper a multiple of GB_K) and, with part, writes
+// its tile to part + z N M (Y's layout) for gemm_ksum_kernel to add.
 template <int F>
 __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t *__restrict__ W,
                                                         uint64_t row_bytes, uint32_t K, uint32_t M,
                                                         const float *__restrict__ X, uint32_t N,
                                                         float *__restrict__ Y,
                                                         const uint2 *__restrict__ grid_g,
-                                                        const uint8_t *__restrict__ gt) {
+                                                        const uint8_t *__restrict__ gt, uint32_t kper,
+                                                        float *__restrict__ part) {
     __shared__ __attribute__((aligned(16))) _Float16 As[GB_M * G_LDS_STRIDE];
     __shared__ __attribute__((aligned(16))) _Float16 Bs[GB_N * G_LDS_STRIDE];
     __shared__ uint2 grid[F == IQ2_XXS ? 256 : 1];
@@ -59,7 +63,8 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t *__restric
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = floatx4{0, 0, 0, 0};
 
-    for (uint32_t k0 = 0; k0 < K; k0 += GB_K) {
+    const uint32_t kb = blockIdx.z * kper, ke = min(K, kb + kper);
+    for (uint32_t k0 = kb; k0 < ke; k0 += GB_K) {
         __syncthreads();  // previous step's fragments are consumed (and grid loaded)
         const uint32_t u = k0 / 32 + lh;
         _Float16 *ad = As + lr * G_LDS_STRIDE + lh * 32;
@@ -111,7 +116,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t *__restric
             const uint32_t m = m0 + wm * 64 + i * 16 + 4 * (lane >> 4);
             const uint32_t n = n0 + wn * 64 + j * 16 + (lane & 15);
             if (n >= N) continue;
-            float *dst = Y + (uint64_t)n * M + m;
+            float *dst = (part ? part + (uint64_t)blockIdx.z * N * M : Y) + (uint64_t)n * M + m;
             if (m + 3 < M && (M & 3) == 0) {
                 *(float4 *)dst = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
             } else {
@@ -120,6 +125,39 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t *__restric
                     if (m + e < M) dst[e] = acc[i][j][e];
             }
         }
+}
+
+// Y = the sum of the ks K-range partials of gemm_mfma_kernel, in K order
+// (deterministic): 4 consecutive values of Y's N M per thread, all ks loads
+// issued first in groups of 8.
+static __global__ __launch_bounds__(256) void gemm_ksum_kernel(const float *__restrict__ part, float *__restrict__ Y,
+                                                        uint64_t nm, uint32_t ks) {
+    const uint64_t e = ((uint64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (e >= nm) return;
+    if (e + 4 <= nm) {
+        float4 v = *(const float4 *)(part + e);
+        for (uint32_t c0 = 1; c0 < ks; c0 += 8) {
+            float4 w[8];
+#pragma unroll
+            for (uint32_t c = 0; c < 8; c++)
+                if (c0 + c < ks) w[c] = *(const float4 *)(part + (uint64_t)(c0 + c) * nm + e);
+#pragma unroll
+            for (uint32_t c = 0; c < 8; c++)
+                if (c0 + c < ks) {
+                    v.x += w[c].x;
+                    v.y += w[c].y;
+                    v.z += w[c].z;
+                    v.w += w[c].w;
+                }
+        }
+        *(float4 *)(Y + e) = v;
+    } else {
+        for (uint64_t i = e; i < nm; i++) {
+            float v = part[i];
+            for (uint32_t c = 1; c < ks; c++) v += part[(uint64_t)c * nm + i];
+            Y[i] = v;
+        }
+    }
 }
 
 // One thread per 32-weight unit of a row; bit-exact with the CPU decoders.

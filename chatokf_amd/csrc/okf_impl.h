@@ -50,6 +50,7 @@ struct okf_ctx {
     int gemv_sb_t = 0;   // its threads per workgroup (0 = auto)
     int gemm_ks = 0;     // wide-tile GEMM: K ranges per remainder tile (0 = auto)
     int q4k_mm = 0xFFF;  // 2..4 columns on the matrix cores, bits mm_bit(F) (0: the dot4 kernels)
+    int gemm_split = 1;  // tile GEMM of the other formats: K split when the grid is small (0 never, > 1 ways)
     int gemm_thin = 0;   // leftover-tile kernel variant (A/B switch)
     int gemm_ng = 4;     // wide-tile GEMM: N tiles that share an XCD's row blocks
     uint32_t cus = 256;  // compute units of the device
@@ -580,9 +581,32 @@ int launch_gemm(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t 
                            c->stream, X, c->xh, n4);
         return launch_gemm_q4k_w(c, W, rb, K, M, N, Y);
     }
-    dim3 grid((N + GB_N - 1) / GB_N, (M + GB_M - 1) / GB_M);
+    // a grid of fewer than two tiles a CU (small M or N) takes K in ks
+    // ranges of whole 64-steps, partial tiles added by gemm_ksum_kernel
+    // (measured on MI355X, N = 512: Q2_0 2048 x 6144 178 us, Q8_0 2048 x 2048
+    // 72.6 us as one K range); without room for the partials (a reserved
+    // context), one range
+    const uint32_t tiles = ((N + GB_N - 1) / GB_N) * ((M + GB_M - 1) / GB_M), steps = (K + GB_K - 1) / GB_K;
+    uint32_t ks = 1;
+    if (c->gemm_split != 0 && tiles < 2 * c->cus) {
+        ks = c->gemm_split > 1 ? (uint32_t)c->gemm_split : (2 * c->cus + tiles - 1) / tiles;
+        ks = std::max(1u, std::min(ks, steps / 4));
+    }
+    const uint32_t kper = (steps + ks - 1) / ks * GB_K;
+    ks = (K + kper - 1) / kper;
+    float *part = nullptr;
+    if (ks > 1) {
+        if (grow_part(c, (size_t)ks * N * M * sizeof(float)) == OKF_OK) part = c->part;
+        else ks = 1;
+    }
+    dim3 grid((N + GB_N - 1) / GB_N, (M + GB_M - 1) / GB_M, ks);
     hipLaunchKernelGGL((gemm_mfma_kernel<F>), grid, dim3(256), 0, c->stream, W, rb, K, M, X, N, Y,
-                       c->grid, c->grids);
+                       c->grid, c->grids, ks > 1 ? kper : (steps * GB_K), part);
+    if (part) {
+        const uint64_t nm = (uint64_t)N * M;
+        hipLaunchKernelGGL(gemm_ksum_kernel, dim3((uint32_t)((nm + 1023) / 1024)), dim3(256), 0, c->stream,
+                           (const float *)part, Y, nm, ks);
+    }
     return OKF_OK;
 }
 

@@ -179,12 +179,16 @@ void build_iq2_xs_s_tables8(uint32_t *t, const uint64_t *grid, int n, const uint
 enum class Path { Auto, Tile };
 
 // N > 5 as consecutive narrow launches of up to narrow_cols columns, while N
-// <= narrow_max: the tile kernels fill few CUs at small N.  Measured on
-// MI355X at 17408 x 5120 (us): Q4_K narrow 5 columns 56, tile 84-88 at N =
-// 6..8; IQ2_XXS narrow 4 columns 19.4, tile 142-153 at N = 6..32; IQ3_XXS 5
-// columns 53, tile 171-179; Q8_0 64 / 152; Q5_K 68 / 171; Q6_K 65 / 161;
-// Q2_K 53 / 132; Q4_0 4 columns 28 / 125 (and at 2048 x 2048 Q8_0 7.1 / 56,
-// Q2_0 2048 x 6144 11.5 / 123).
+// <= narrow_max, where that is faster than the tile kernels.  Measured on
+// MI355X against the tile kernels with their K split (us, N = 6 / 8 / 12 /
+// 16): 2048 x 2048 Q8_0 chunks 11.3 / 12.4 / 18.2 / 24.6, tile 11.5 / 11.4 /
+// 11.6 / 11.6; Q6_K 11.1 / 12.5 against 12.3 / 12.6; IQ4_XS 11.2 / 12.0 /
+// 18.2 against 14.0 / 14.1 / 14.4; Q4_0, Q4_K, IQ2_XXS, IQ3_XXS, Q2_K and
+// Q2_0 (2048 x 6144) tile from N = 6.  17408 x 5120: IQ2_XXS 35.4 / 36.8 /
+// 54.8 / 72.5 against 56.7 / 56.5 / 56.8 / 57.3, IQ3_XXS 40.5 / 43.2 / 64.9
+// / 84.1 against 75.2-76.9, Q3_K 69.2 / 68.6 / 101.6 against 80.2-80.7,
+// Q4_0 48.3 / 57.1 against 57.2 / 57.4, Q8_0 84.7 against 66.2, Q4_K 36.1
+// / 36.9 / 57.1 / 80.7 against 78.8 / 81.1 / 86.6 / 91.7.
 // The formats whose 2..4-column matrix-core kernel runs (K <= 6144, M >=
 // 4096), Q8_0 aside: 4-column chunks, each about as long as one column
 // (17408 x 5120: Q4_K 19.8, Q5_K 22.8, IQ4_XS 21.9 us against 56.9, 67.0
@@ -202,20 +206,20 @@ uint32_t narrow_cols(int32_t t, uint32_t M, uint32_t K) {
 // 14.2 against 56.9)
 uint32_t narrow_from(int32_t t, uint32_t M, uint32_t K) { return t == IQ2_XXS || mm_fits(t, M, K) ? 5 : 6; }
 uint32_t narrow_max(int32_t t, uint32_t M, uint32_t K) {
-    // (17408 x 5120, chunks against the tile kernel, us: Q4_K N = 16 about
-    // 80 / 100; Q5_K N = 24 130 / 176; IQ3_XXS N = 32 160 / 177, IQ1_S 145 /
-    // 156; IQ1_M N = 24 122 / 139, 32 157 / 143; Q2_K N = 24 112 / 140, 32
-    // 145 / 143; Q3_K N = 16 135 / 162, 24 197 / 165)
-    if (mm_fits(t, M, K))
-        return t == Q4_K || t == Q3_K ? 16 : (t == Q5_K || t == IQ4_XS || t == IQ1_M) ? 24 : t == Q2_K ? 28 : 32;
+    if (M < 4096) {  // (a small grid: the K-split tile fills the GPU)
+        switch (t) {
+        case Q8_0: case Q5_K: return 6;
+        case Q6_K: case IQ4_XS: return 8;
+        default: return 5;
+        }
+    }
+    if (mm_fits(t, M, K)) return t == Q4_K ? 16 : t == Q3_K ? 8 : 12;
     switch (t) {
     case Q4_K: return 7;
-    case IQ2_XXS: return 28;
-    case Q4_0: case IQ4_NL: return 16;
-    case Q5_K: case Q2_K: return 12;
-    case Q8_0: case Q6_K: return 11;
-    case F32: case F16: case BF16: return 5;
-    default: return 15;  // the other grid formats, IQ4_XS, Q3_K, Q2_0
+    case IQ2_XXS: return 12;
+    case Q4_0: case IQ4_NL: return 8;
+    case Q8_0: case Q6_K: case Q2_0: case F32: case F16: case BF16: return 5;
+    default: return 12;  // the other grid formats and K-quants with K > 6144
     }
 }
 
@@ -232,7 +236,7 @@ int run_gemm(okf_ctx *c, const okf_weight *w, const float *X, uint32_t N, float 
     // (at M <= 4096 the 128 x 128 tile kernel runs at most 32 workgroups per
     // 128 columns: chunks win to N = 32, e.g. Q8_0 2048 x 2048 N = 28 about
     // 39 against 59 us, Q2_0 2048 x 6144 69 against 130)
-    const uint32_t nmax = std::max(narrow_max(w->ggml_type, w->M, w->K), w->M <= 4096 ? 32u : 0u);
+    const uint32_t nmax = narrow_max(w->ggml_type, w->M, w->K);
     if (path == Path::Auto && N >= narrow_from(w->ggml_type, w->M, w->K) && N <= nmax && !X2) {
         const uint32_t nc = narrow_cols(w->ggml_type, w->M, w->K);
         for (uint32_t c0 = 0; c0 < N; c0 += nc) {
@@ -388,6 +392,7 @@ int okf_ctx_create(int device, okf_ctx **out) {
         if (const char *e = getenv("OKF_GEMM_KS")) c->gemm_ks = atoi(e);
         if (const char *e = getenv("OKF_GEMM_NG")) c->gemm_ng = atoi(e);
         if (const char *e = getenv("OKF_GEMM_THIN")) c->gemm_thin = atoi(e);
+        if (const char *e = getenv("OKF_GEMM_SPLIT")) c->gemm_split = atoi(e);
         if (const char *e = getenv("OKF_Q4K_MM")) c->q4k_mm = atoi(e);
         if (const char *e = getenv("OKF_FFN_FUSED")) c->ffn_fused = atoi(e);
         if (const char *e = getenv("OKF_FFN_WG")) c->ffn_wg = atoi(e);

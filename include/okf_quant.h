@@ -150,13 +150,14 @@ int okf_silu_mul(okf_ctx *ctx, float *a, const float *b, uint32_t n);
 /* MetalEnc.gemm (MetalEnc.swift:241-289): Y[N][M] = X[N][K] W^T.  Dispatch
  * policy as the reference: N == 1 -> gemv; 2 <= N <= 5 -> narrow (one weight
  * pass serving all N columns, gemmNarrow / gemmNarrowIQ :176-239);
- * N > 5 -> MFMA tile GEMM (gemmTiled / iqGemmTiled, :354-400), except that
- * a small N past 5 (up to a per-format bound, 7..32 columns, and 32 when
- * M <= 4096) runs as consecutive narrow launches of 4 or 5 columns, which
- * fill the GPU where the tile grid would not (for IQ2_XXS, and for every
- * other K-quant and i-quant format but Q6_K and IQ4_NL with K <= 6144 and
- * M >= 4096, from N = 5 on, in 4-column launches).  The results are the
- * narrow kernels' for those N. */
+ * N > 5 -> MFMA tile GEMM (gemmTiled / iqGemmTiled, :354-400; a grid of
+ * fewer than two tiles a CU splits K over workgroups, partials added in K
+ * order), except that a small N past 5 (up to a per-format bound, 5..16
+ * columns, where measured faster than the tile) runs as consecutive narrow
+ * launches of 4 or 5 columns (for IQ2_XXS, and for every other K-quant and
+ * i-quant format but Q6_K and IQ4_NL with K <= 6144 and M >= 4096, from N =
+ * 5 on, in 4-column launches).  The results are the narrow kernels' for
+ * those N. */
 int okf_gemm(okf_ctx *ctx, const okf_weight *w, const float *X, uint32_t N, float *Y);
 
 /* MetalEnc.gemmTile (MetalEnc.swift:326-352): the tile GEMM for any N >= 1. */

@@ -683,10 +683,10 @@ def test_tile_gemm_matches_oracle(enc, t, M, K, N):
         assert np.array_equal(run_gemm(enc, t, M, K, w, X), got)
 
 
-# The auto path for 5 < N <= NARROW_MAX[t]: consecutive narrow launches of
-# up to NARROW_COLS[t] columns (okf_quant.hip's narrow_max / narrow_cols).
-NARROW_MAX = {Q4_K: 7, IQ2_XXS: 28, Q4_0: 16, IQ4_NL: 16, Q5_K: 12, Q2_K: 12, Q8_0: 11, Q6_K: 11, F32: 5,
-              F16: 5, BF16: 5}
+# The auto path for 5 < N <= narrow_max: consecutive narrow launches of up
+# to narrow_cols columns (okf_quant.hip's narrow_max / narrow_cols).
+SMALL_MAX = {Q8_0: 6, Q5_K: 6, Q6_K: 8, IQ4_XS: 8}  # M < 4096
+NARROW_MAX = {Q4_K: 7, IQ2_XXS: 12, Q4_0: 8, IQ4_NL: 8, Q8_0: 5, Q6_K: 5, Q2_0: 5, F32: 5, F16: 5, BF16: 5}
 NARROW_COLS = {IQ2_XXS: 4, Q4_0: 4, IQ4_NL: 4}
 
 
@@ -694,23 +694,29 @@ def mm_fits(t, M, K):
     return t in MM_FMTS and t != Q8_0 and K <= 6144 and K % 64 == 0 and M >= 4096
 
 
-MM_MAX = {Q4_K: 16, Q3_K: 16, Q5_K: 24, IQ4_XS: 24, IQ1_M: 24, Q2_K: 28}
+MM_MAX = {Q4_K: 16, Q3_K: 8}
 
 
 def narrow_cols(t, M, K):
     return 4 if t in NARROW_COLS or mm_fits(t, M, K) else 5
 
 
+def narrow_max(t, M, K):
+    if M < 4096:
+        return SMALL_MAX.get(t, 5)
+    return MM_MAX.get(t, 12) if mm_fits(t, M, K) else NARROW_MAX.get(t, 12)
+
+
 def narrow_chunks(t, M, N, K):
-    nmax = MM_MAX.get(t, 32) if mm_fits(t, M, K) else NARROW_MAX.get(t, 15)
     first = 5 if t == IQ2_XXS or mm_fits(t, M, K) else 6
-    return first <= N <= max(nmax, 32 if M <= 4096 else 0)
-CHUNKS = [(Q4_K, 260, 2304, 7), (IQ2_XXS, 129, 1536, 6), (IQ2_XXS, 1000, 1280, 28), (Q8_0, 300, 2048, 11),
-          (Q2_0, 130, 1024, 13), (Q4_0, 300, 2048, 9), (IQ3_XXS, 130, 768, 15), (Q2_K, 130, 768, 12),
-          (Q6_K, 129, 768, 8), (Q8_0, 2048, 2048, 32), (F32, 300, 1024, 17), (Q4_K, 4000, 2304, 20),
-          (Q4_K, 4100, 2048, 5), (IQ2_XXS, 1030, 2048, 5), (Q4_K, 300, 8192, 7), (Q5_K, 4100, 1024, 9),
-          (IQ4_XS, 4100, 1024, 6), (IQ3_S, 4100, 1024, 30), (IQ1_M, 4099, 768, 9), (Q3_K, 4100, 1280, 13),
-          (Q2_K, 4200, 1024, 27), (IQ2_S, 4096, 512, 32), (IQ1_S, 4097, 1536, 5)]
+    return first <= N <= narrow_max(t, M, K)
+
+
+CHUNKS = [(Q8_0, 300, 2048, 6), (Q6_K, 129, 768, 8), (IQ4_XS, 300, 1024, 7), (Q5_K, 130, 1024, 6),
+          (IQ2_XXS, 4100, 1280, 12), (IQ2_XXS, 4097, 2048, 5), (Q4_K, 4100, 2048, 5), (Q4_K, 4100, 8192, 7),
+          (Q4_K, 4200, 2304, 16), (Q5_K, 4100, 1024, 9), (IQ4_XS, 4100, 1024, 6), (IQ3_S, 4100, 1024, 12),
+          (IQ1_M, 4099, 768, 9), (Q3_K, 4100, 1280, 8), (Q2_K, 4200, 1024, 11), (IQ2_S, 4096, 512, 12),
+          (IQ1_S, 4097, 1536, 5), (Q4_0, 4100, 2048, 8), (IQ3_XXS, 4100, 768, 10)]
 
 
 @pytest.mark.parametrize("t,M,K,N", CHUNKS)
