@@ -233,9 +233,6 @@ int run_gemm(okf_ctx *c, const okf_weight *w, const float *X, uint32_t N, float 
     if (!aligned16(X) || (X2 && !aligned16(X2))) return OKF_E_SHAPE;
     if ((st = begin(c))) return st;
     const uint8_t *W = (const uint8_t *)w->base + w->off;
-    // (at M <= 4096 the 128 x 128 tile kernel runs at most 32 workgroups per
-    // 128 columns: chunks win to N = 32, e.g. Q8_0 2048 x 2048 N = 28 about
-    // 39 against 59 us, Q2_0 2048 x 6144 69 against 130)
     const uint32_t nmax = narrow_max(w->ggml_type, w->M, w->K);
     if (path == Path::Auto && N >= narrow_from(w->ggml_type, w->M, w->K) && N <= nmax && !X2) {
         const uint32_t nc = narrow_cols(w->ggml_type, w->M, w->K);
