@@ -33,6 +33,7 @@ __device__ __forceinline__ void zero_half32(_Float16 *dst) {
     for (int i = 0; i < 4; i++) *(half8 *)(dst + i * 8) = half8{};
 }
 
+// Xh: X in fp16 (converted once per call), else X is rounded here.
 // K split: workgroup z of the grid's third dimension takes K range
 // [z kper, (z + 1) kper) (kper a multiple of GB_K) and, with part, writes
 // its tile to part + z N M (Y's layout) for gemm_ksum_kernel to add.
@@ -43,7 +44,8 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t *__restric
                                                         float *__restrict__ Y,
                                                         const uint2 *__restrict__ grid_g,
                                                         const uint8_t *__restrict__ gt, uint32_t kper,
-                                                        float *__restrict__ part) {
+                                                        float *__restrict__ part,
+                                                        const _Float16 *__restrict__ Xh) {
     __shared__ __attribute__((aligned(16))) _Float16 As[GB_M * G_LDS_STRIDE];
     __shared__ __attribute__((aligned(16))) _Float16 Bs[GB_N * G_LDS_STRIDE];
     __shared__ uint2 grid[F == IQ2_XXS ? 256 : 1];
@@ -73,17 +75,23 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t *__restric
             float w[32];
             decode_unit<F>(wrow, u, w, grid, gt);
             store_half32(ad, w);
-            float x[32];
-            const float4 *xp = (const float4 *)(xrow + u * 32);
+            if (Xh) {  // X already in fp16 (x_to_f16_kernel, the same rounding)
+                const half8 *hp = (const half8 *)(Xh + (uint64_t)min(n0 + lr, N - 1) * K + u * 32);
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                float4 v = xp[i];
-                x[4 * i] = v.x;
-                x[4 * i + 1] = v.y;
-                x[4 * i + 2] = v.z;
-                x[4 * i + 3] = v.w;
+                for (int i = 0; i < 4; i++) *(half8 *)(bd + i * 8) = hp[i];
+            } else {
+                float x[32];
+                const float4 *xp = (const float4 *)(xrow + u * 32);
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    float4 v = xp[i];
+                    x[4 * i] = v.x;
+                    x[4 * i + 1] = v.y;
+                    x[4 * i + 2] = v.z;
+                    x[4 * i + 3] = v.w;
+                }
+                store_half32(bd, x);
             }
-            store_half32(bd, x);
         } else {
             zero_half32(ad);
             zero_half32(bd);

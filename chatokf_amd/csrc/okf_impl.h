@@ -51,6 +51,7 @@ struct okf_ctx {
     int gemm_ks = 0;     // wide-tile GEMM: K ranges per remainder tile (0 = auto)
     int q4k_mm = 0xFFF;  // 2..4 columns on the matrix cores, bits mm_bit(F) (0: the dot4 kernels)
     int gemm_split = 1;  // tile GEMM of the other formats: K split when the grid is small (0 never, > 1 ways)
+    int gemm_xh = 1;     // tile GEMM of the other formats: fp16 X converted once from N = 256 (0: never)
     int gemm_thin = 0;   // leftover-tile kernel variant (A/B switch)
     int gemm_ng = 4;     // wide-tile GEMM: N tiles that share an XCD's row blocks
     uint32_t cus = 256;  // compute units of the device
@@ -599,9 +600,20 @@ int launch_gemm(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t 
         if (grow_part(c, (size_t)ks * N * M * sizeof(float)) == OKF_OK) part = c->part;
         else ks = 1;
     }
+    // from N = 256 X is converted to fp16 once (every row tile would round
+    // the same columns again), when the buffer can hold it (measured, us,
+    // N = 512: Q2_0 6144 x 2048 58.9 -> 46.0, 2048 x 6144 52.0 -> 41.8; at
+    // N = 64..128 the extra launch costs about what it saves)
+    const _Float16 *xh = nullptr;
+    if (c->gemm_xh && N >= 256 && K % 32 == 0 && grow_xh(c, (size_t)N * K * sizeof(_Float16)) == OKF_OK) {
+        const uint64_t n4 = (uint64_t)N * K / 4;
+        hipLaunchKernelGGL(x_to_f16_kernel, dim3((uint32_t)((n4 + 256 * XV - 1) / (256 * XV))), dim3(256), 0,
+                           c->stream, X, c->xh, n4);
+        xh = c->xh;
+    }
     dim3 grid((N + GB_N - 1) / GB_N, (M + GB_M - 1) / GB_M, ks);
     hipLaunchKernelGGL((gemm_mfma_kernel<F>), grid, dim3(256), 0, c->stream, W, rb, K, M, X, N, Y,
-                       c->grid, c->grids, ks > 1 ? kper : (steps * GB_K), part);
+                       c->grid, c->grids, ks > 1 ? kper : (steps * GB_K), part, xh);
     if (part) {
         const uint64_t nm = (uint64_t)N * M;
         hipLaunchKernelGGL(gemm_ksum_kernel, dim3((uint32_t)((nm + 1023) / 1024)), dim3(256), 0, c->stream,

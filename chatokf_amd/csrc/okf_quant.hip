@@ -390,6 +390,7 @@ int okf_ctx_create(int device, okf_ctx **out) {
         if (const char *e = getenv("OKF_GEMM_NG")) c->gemm_ng = atoi(e);
         if (const char *e = getenv("OKF_GEMM_THIN")) c->gemm_thin = atoi(e);
         if (const char *e = getenv("OKF_GEMM_SPLIT")) c->gemm_split = atoi(e);
+        if (const char *e = getenv("OKF_GEMM_XH")) c->gemm_xh = atoi(e);
         if (const char *e = getenv("OKF_Q4K_MM")) c->q4k_mm = atoi(e);
         if (const char *e = getenv("OKF_FFN_FUSED")) c->ffn_fused = atoi(e);
         if (const char *e = getenv("OKF_FFN_WG")) c->ffn_wg = atoi(e);

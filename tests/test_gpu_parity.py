@@ -667,7 +667,7 @@ TILE = [(Q8_0, 300, 2048, 37), (Q2_0, 130, 1024, 129), (Q4_K, 260, 2304, 77), (I
         (Q4_K, 1, 256, 64), (Q8_0, 5, 96, 200), (Q4_K, 4224, 256, 512), (Q4_K, 1000, 512, 300),
         (Q4_K, 8192, 512, 1024),
         (Q4_0, 300, 2048, 37), (IQ4_NL, 130, 1024, 70), (Q5_K, 200, 1024, 40), (Q6_K, 129, 768, 33),
-        (IQ4_XS, 260, 1280, 90)] + [(t, 130, 768, 41) for t in (IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M, Q2_K, Q3_K, F32,
+        (IQ4_XS, 260, 1280, 90), (Q2_0, 300, 2048, 300), (Q8_0, 130, 1024, 257), (IQ3_XXS, 260, 768, 256)] + [(t, 130, 768, 41) for t in (IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M, Q2_K, Q3_K, F32,
                                                                 F16, BF16)]
 
 
@@ -681,6 +681,29 @@ def test_tile_gemm_matches_oracle(enc, t, M, K, N):
     assert rel(got, ref) <= TOL
     if N > 5 and not narrow_chunks(t, M, N, K):  # the auto path takes the tile past the narrow chunks
         assert np.array_equal(run_gemm(enc, t, M, K, w, X), got)
+
+
+# From N = 256 the tile GEMM of the other formats converts X to fp16 once
+# per call; the rounding is the one its loader applies per tile, so with
+# OKF_GEMM_XH=0 (rounded per tile) the results are the same bits.
+@pytest.fixture(scope="module")
+def enc_noxh():
+    import os
+    os.environ["OKF_GEMM_XH"] = "0"
+    try:
+        e = ok.Enc(0)
+    finally:
+        del os.environ["OKF_GEMM_XH"]
+    yield e
+    e.close()
+
+
+@pytest.mark.parametrize("t,M,K,N", [(Q2_0, 300, 2048, 300), (Q8_0, 130, 1024, 257), (Q6_K, 260, 768, 512)])
+def test_tile_fp16_x_same_bits(enc, enc_noxh, t, M, K, N):
+    say("tile fp16 x", NAMES[t], M, K, N)
+    w = weights(t, M, K, 23)
+    X = acts(N, K, 24)
+    assert np.array_equal(run_gemm(enc, t, M, K, w, X, tile=True), run_gemm(enc_noxh, t, M, K, w, X, tile=True))
 
 
 # The auto path for 5 < N <= narrow_max: consecutive narrow launches of up
