@@ -33,6 +33,59 @@ __device__ __forceinline__ void zero_half32(_Float16 *dst) {
     for (int i = 0; i < 4; i++) *(half8 *)(dst + i * 8) = half8{};
 }
 
+// Q8_0 / Q2_0 units straight to fp16 (halves in weight order, 4 x 8): their
+// weights are q d with q a small integer and d an fp16 value, so one fp16
+// multiply rounds the exact product once, as decode_unit's fp32 product
+// (exact) followed by the fp16 rounding does: the same bits.  q reaches
+// fp16 through a byte spread into 0x64xx (1024 + byte) and one packed
+// subtraction, exact.
+template <int F>
+__device__ __forceinline__ void decode_unit_h(const uint8_t *row, uint32_t u, half8 (&h)[4]) {
+    uint32_t o[16];
+    _Float16 d, off;
+    if constexpr (F == Q8_0) {  // Q8_0.dequant (LLM/Gemma/Gemma4Quant.swift:55-68)
+        const uint8_t *b = row + (uint64_t)u * 34;
+        d = __builtin_bit_cast(_Float16, ldu<uint16_t>(b));
+        uint32_t q[8];
+        *(uint4 *)&q[0] = ldu<uint4>(b + 2);
+        *(uint4 *)&q[4] = ldu<uint4>(b + 18);
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t v = q[k] ^ 0x80808080u;  // b + 128
+            o[2 * k] = __builtin_amdgcn_perm(0x64646464u, v, 0x04010400u);
+            o[2 * k + 1] = __builtin_amdgcn_perm(0x64646464u, v, 0x04030402u);
+        }
+        off = (_Float16)-1152.0f;
+    } else {  // Q2_0.dequant (LLM/Base/Quant.swift:10-25): code j at bits 2 (j % 16) of dword j / 16
+        static_assert(F == Q2_0, "fp16 unit decode: Q8_0, Q2_0");
+        const uint8_t *b = row + (uint64_t)(u >> 2) * 34;
+        d = __builtin_bit_cast(_Float16, ldu<uint16_t>(b));
+        const uint2 q = ldu<uint2>(b + 2 + (u & 3) * 8);
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            const uint32_t dw = s ? q.y : q.x;
+            const uint32_t f0 = dw & 0x03030303u, f1 = (dw >> 2) & 0x03030303u;
+            const uint32_t f2 = (dw >> 4) & 0x03030303u, f3 = (dw >> 6) & 0x03030303u;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {  // weights 16 s + 4 k + {0, 1 | 2, 3}: byte k of f0 f1 | f2 f3
+                const uint32_t sel = (uint32_t)k | 0x0C00u | (uint32_t)(4 + k) << 16 | 0x0C000000u;
+                o[8 * s + 2 * k] = __builtin_amdgcn_perm(f1, f0, sel) | 0x64006400u;
+                o[8 * s + 2 * k + 1] = __builtin_amdgcn_perm(f3, f2, sel) | 0x64006400u;
+            }
+        }
+        off = (_Float16)-1025.0f;
+    }
+    const half2v d2 = {d, d}, o2 = {off, off};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        uint32_t r[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            r[e] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(half2v, o[4 * i + e]) + o2) * d2);
+        h[i] = __builtin_bit_cast(half8, uint4{r[0], r[1], r[2], r[3]});
+    }
+}
+
 // Xh: X in fp16 (converted once per call), else X is rounded here.
 // K split: workgroup z of the grid's third dimension takes K range
 // [z kper, (z + 1) kper) (kper a multiple of GB_K) and, with part, writes
@@ -72,9 +125,16 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t *__restric
         _Float16 *ad = As + lr * G_LDS_STRIDE + lh * 32;
         _Float16 *bd = Bs + lr * G_LDS_STRIDE + lh * 32;
         if (u < units) {
-            float w[32];
-            decode_unit<F>(wrow, u, w, grid, gt);
-            store_half32(ad, w);
+            if constexpr (F == Q8_0 || F == Q2_0) {
+                half8 h[4];
+                decode_unit_h<F>(wrow, u, h);
+#pragma unroll
+                for (int i = 0; i < 4; i++) *(half8 *)(ad + i * 8) = h[i];
+            } else {
+                float w[32];
+                decode_unit<F>(wrow, u, w, grid, gt);
+                store_half32(ad, w);
+            }
             if (Xh) {  // X already in fp16 (x_to_f16_kernel, the same rounding)
                 const half8 *hp = (const half8 *)(Xh + (uint64_t)min(n0 + lr, N - 1) * K + u * 32);
 #pragma unroll
