@@ -99,8 +99,12 @@ int okf_ctx_stream(okf_ctx *ctx, void **stream);
  * tile GEMM with N * K <= gemm_nk, and the pairs and row counters of
  * okf_argmax_rows over up to argmax_rows rows of argmax_n values.  Afterwards
  * no call allocates or synchronises; one that needs more scratch than
- * reserved returns OKF_E_SHAPE.  Without it the scratch grows on demand
- * (hipMalloc after draining the stream). */
+ * reserved returns OKF_E_SHAPE.  (The tile GEMM of the other formats uses
+ * the same scratch for its K-split partials and fp16 activations where it
+ * fits, and otherwise runs without them: one K range, or the activations
+ * rounded per tile; the K split changes only the order of the fp32 sums.)
+ * Without it the scratch grows on demand (hipMalloc after draining the
+ * stream). */
 int okf_ctx_reserve(okf_ctx *ctx, uint64_t gemm_nk, uint32_t argmax_n, uint32_t argmax_rows);
 
 /* GGUF.rowByteCount (LLM/Base/GGUF.swift:160-188) for the types above: n a
