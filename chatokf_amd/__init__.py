@@ -22,7 +22,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("OKF_LIB") or os.path.join(HERE, "libokf_quant.so")
 
 (OKF_OK, OKF_E_TYPE, OKF_E_SHAPE, OKF_E_HIP, OKF_E_INJECTED, OKF_E_ARG, OKF_E_NODEV, OKF_E_IO,
- OKF_E_FORMAT, OKF_E_NOTFOUND) = range(10)
+ OKF_E_FORMAT, OKF_E_NOTFOUND, OKF_E_TIMEOUT) = range(11)
 
 # Every symbol include/okf_quant.h declares.
 EXPORTS = (

@@ -40,6 +40,7 @@ struct FfnArgs {
     const float *x;
     float *g, *u, *y;
     uint32_t *bar;  // FF_BAR_BYTES, zero before the first launch
+    uint32_t *status;  // host-visible failure word (pinned host memory): set to 1 by a failed barrier
     uint32_t spin;  // polls before a waiting workgroup gives up
     uint32_t stall;  // 1: the barrier waits for one arrival more than the grid has (time-out tests)
 };
@@ -55,27 +56,41 @@ struct FfnArgs {
 // wavefront polls the counters (lane k counter k) until each reaches
 // (e + 1) times its subgroup's size, then sets every flag to e + 1; the
 // other workgroups poll their flag.  So the atomics meet no polling on
-// their lines, and only one wavefront polls them.  The polls are bounded:
-// after `spin` of them a workgroup goes on and reports false, so no wave
-// waits forever; the master then still advances the flags, so the
-// counters and flags agree for the next launch.  `stall` (a test of that
-// path) makes the master wait for one arrival too many.
+// their lines, and only one wavefront polls them.
+//
+// Time-out: the polls are bounded.  A master that gives up writes the
+// barrier's time-out word = e + 1 (low 32 bits) and waits for that store's
+// acknowledgement before it releases the flags, so the counters and flags
+// still agree for the next launch.  Every workgroup reads the time-out word
+// after its release, so a barrier the master gave up on fails in every
+// workgroup of the launch (the word names the epoch, so later launches are
+// not affected); a workgroup whose own poll gave up fails too.  A failed
+// workgroup writes NaN to all of its outputs and sets the host-visible
+// status word (`status`, pinned host memory) that okf_sync / okf_ffn turn
+// into OKF_E_TIMEOUT.  `stall` (a test of that path) makes the master wait
+// for one arrival too many.
 //
 // Memory: the data exchanged across the barrier (g) is written with
-// device-scope stores (coherent at device scope once acknowledged) and read
-// with device-scope loads (which miss any stale line in this XCD's L2), and
-// every wave waits for its stores to be acknowledged (s_waitcnt, which
+// agent-scope stores and read with agent-scope loads (issued with the sc1
+// bit, so they miss any stale line in this XCD's L2), and every wave waits
+// for its stores to be acknowledged (s_waitcnt vmcnt(0), which
 // __syncthreads does not do for global memory) before the workgroup
-// arrives.  So the barrier needs no cache-wide write-back or invalidate:
-// device-scope fences here, one per wave, each flushing or invalidating a
-// whole L2, made the kernel take 60 us.
-__device__ __forceinline__ bool ff_grid_sync(uint32_t *bar, uint32_t spin, uint32_t stall) {
+// arrives.  The counter add and the flag accesses are relaxed atomics: no
+// release or acquire fence orders them, because on gfx950 an agent-scope
+// release writes back and an acquire invalidates the whole L2 of the XCD
+// (device-scope fences here, one per wave, made the kernel take 60 us).
+// The ordering rests on the ISA instead: stores are acknowledged in the
+// s_waitcnt before the arrival is issued, the flag load that ends a poll
+// has returned before any later load is issued (the loop exit depends on
+// its value), and the asm waits carry a memory clobber so that the compiler
+// moves no memory access across them.
+__device__ __forceinline__ bool ff_grid_sync(uint32_t *bar, uint32_t spin, uint32_t stall, uint32_t *status) {
     __shared__ uint64_t epoch;
     __shared__ uint32_t ok;
     uint64_t *cnt = (uint64_t *)bar;             // counter k at cnt[k * FF_LINE / 2]
     uint64_t *flag = (uint64_t *)(bar + FF_FLAG);  // flag k at flag[k * FF_LINE / 2]
     const uint32_t nb = gridDim.x, s = blockIdx.x % FF_SUB;
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's stores of g acknowledged
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");  // this wave's stores of g acknowledged
     __syncthreads();
     if (threadIdx.x == 0) {
         const uint64_t e = __hip_atomic_load(flag + s * (FF_LINE / 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -102,6 +117,12 @@ __device__ __forceinline__ bool ff_grid_sync(uint32_t *bar, uint32_t spin, uint3
             }
             __builtin_amdgcn_s_sleep(1);
         }
+        if (__any(k == 0 && !ok)) {
+            // the time-out word names this epoch; acknowledged before the release
+            if (k == 0)
+                __hip_atomic_store(bar + FF_TIMEOUT, (uint32_t)(e + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
         if (k < FF_SUB)
             __hip_atomic_store(flag + k * (FF_LINE / 2), e + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     } else if (threadIdx.x == 0) {
@@ -113,8 +134,12 @@ __device__ __forceinline__ bool ff_grid_sync(uint32_t *bar, uint32_t spin, uint3
             }
             __builtin_amdgcn_s_sleep(1);
         }
+        // released: did the master give up on this epoch?
+        asm volatile("" ::: "memory");
+        if (ok && __hip_atomic_load(bar + FF_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(e + 1))
+            ok = 0;
     }
-    if (threadIdx.x == 0 && !ok) __hip_atomic_store(bar + FF_TIMEOUT, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0 && !ok) __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     __syncthreads();
     return ok != 0;
 }
@@ -257,7 +282,7 @@ __global__ __launch_bounds__(T) void ffn_fused_kernel(FfnArgs a) {
             }
         }
     }
-    const bool synced = ff_grid_sync(a.bar, a.spin, a.stall);
+    const bool synced = ff_grid_sync(a.bar, a.spin, a.stall, a.status);
 
     // phase B: down on g (staged after the barrier, so every row of it is in)
     constexpr int XB = (UB * 64 * unit_weights<F>() / 8 + T - 1) / T;
@@ -280,7 +305,8 @@ __global__ __launch_bounds__(T) void ffn_fused_kernel(FfnArgs a) {
                 float v = acc[0][0];
 #pragma unroll
                 for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-                // a barrier that timed out leaves NaN, never a plausible y
+                // a failed barrier (this workgroup's poll or the master's
+                // gave up) leaves NaN in every row of the workgroup
                 if (lane == 0) a.y[r] = synced ? v : __builtin_nanf("");
             }
         }

@@ -14,7 +14,7 @@ OKF_INSTANTIATE(Q2_0)
 // (gate M <= 8192), and up to 4 row pairs and 2 down rows per wavefront.
 bool launch_ffn_fused(okf_ctx *c, const FfnArgs &a0) {
     constexpr uint32_t UW = unit_weights<Q2_0>();
-    if (!c->ffn_fused || !c->ffn_bar || a0.ka % UW || a0.ma % UW) return false;
+    if (!c->ffn_fused || !c->ffn_bar || !c->ffn_status || a0.ka % UW || a0.ma % UW) return false;
     const uint32_t una = a0.ka / UW, unb = a0.ma / UW;
     if (una > 64 || unb > 128) return false;
     auto stage_bytes = [](uint32_t units) {
@@ -53,6 +53,7 @@ bool launch_ffn_fused(okf_ctx *c, const FfnArgs &a0) {
         if (k.ra ? (una > 32 || unb <= 64 || ra != k.ra || rb != k.rb) : (ra > 4 || rb > 2)) continue;
         FfnArgs a = a0;
         a.bar = c->ffn_bar;
+        a.status = c->ffn_status;
         a.spin = c->ffn_spin > 0 ? (uint32_t)c->ffn_spin : FF_SPIN;
         a.stall = c->ffn_stall > 0 ? 1u : 0u;
         void *args[] = {&a};

@@ -197,12 +197,14 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t *__restric
 
 // Y = the sum of the ks K-range partials of gemm_mfma_kernel, in K order
 // (deterministic): 4 consecutive values of Y's N M per thread, all ks loads
-// issued first in groups of 8.
+// issued first in groups of 8.  vec: float4 accesses (the host sets it
+// only when N M is a multiple of 4 and Y is 16-byte aligned, so that every
+// partial and Y are too); else one value at a time.
 static __global__ __launch_bounds__(256) void gemm_ksum_kernel(const float *__restrict__ part, float *__restrict__ Y,
-                                                        uint64_t nm, uint32_t ks) {
+                                                        uint64_t nm, uint32_t ks, uint32_t vec) {
     const uint64_t e = ((uint64_t)blockIdx.x * 256 + threadIdx.x) * 4;
     if (e >= nm) return;
-    if (e + 4 <= nm) {
+    if (vec && e + 4 <= nm) {
         float4 v = *(const float4 *)(part + e);
         for (uint32_t c0 = 1; c0 < ks; c0 += 8) {
             float4 w[8];
@@ -220,7 +222,7 @@ static __global__ __launch_bounds__(256) void gemm_ksum_kernel(const float *__re
         }
         *(float4 *)(Y + e) = v;
     } else {
-        for (uint64_t i = e; i < nm; i++) {
+        for (uint64_t i = e; i < nm && i < e + 4; i++) {
             float v = part[i];
             for (uint32_t c = 1; c < ks; c++) v += part[(uint64_t)c * nm + i];
             Y[i] = v;

@@ -76,6 +76,7 @@ struct okf_ctx {
     bool reserved = false;    // okf_ctx_reserve fixed the scratch sizes: no growth
     uint8_t *scratch = nullptr;  // this device's copy of the static scratch array
     uint32_t *ffn_bar = nullptr;  // the one-launch FFN's grid barrier (zeroed at creation)
+    uint32_t *ffn_status = nullptr;  // pinned host word: 1 once a launch's barrier gave up (GPUGate verdict)
     int ffn_fused = 1;            // okf_ffn as one launch with a grid barrier where it fits (0: two launches)
     int ffn_wg = 1;               // its workgroups per CU, at most
     int ffn_coop = 0;             // launched with hipLaunchCooperativeKernel (1) or as a plain grid
@@ -127,6 +128,16 @@ inline int check_weight(const okf_weight *w, uint64_t *row_bytes) {
     // Q4_K kernels read 16-byte header/code chunks; others need 2-byte alignment.
     if (w->ggml_type == Q4_K ? (a & 15) : (a & 1)) return OKF_E_SHAPE;
     return OKF_OK;
+}
+
+// The one-launch FFN's failure word (written by the kernel, read by the
+// host without a copy): OKF_E_TIMEOUT once, and cleared, after a launch whose
+// grid barrier gave up (GPUGate.verdict, LLM/Base/MetalGates.swift:130-142).
+inline int take_timeout(okf_ctx *c) {
+    volatile uint32_t *w = c->ffn_status;
+    if (!w || *w == 0) return OKF_OK;
+    *w = 0;
+    return OKF_E_TIMEOUT;
 }
 
 inline bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
@@ -462,55 +473,62 @@ void launch_gemv_pair(okf_ctx *c, const GemvCall *calls, uint64_t rb, uint32_t K
 // device does not fit it.
 bool launch_ffn_fused(okf_ctx *c, const FfnArgs &a);
 
-// The context's scratch (split-tile partial sums, argmax pairs), grown to at
-// least `need` bytes; the stream is drained before an old buffer is freed.
-// After okf_ctx_reserve the sizes are fixed: a call that needs more is an
-// OKF_E_SHAPE, so nothing on the hot path allocates or synchronises.
-inline int grow_part(okf_ctx *c, size_t need) {
-    if (need <= c->part_bytes) return OKF_OK;
-    if (c->reserved) return OKF_E_SHAPE;
-    hipError_t e = hipStreamSynchronize(c->stream);
-    if (e != hipSuccess) return hip_fail(c, e);
-    if (c->part) (void)hipFree(c->part);
-    c->part = nullptr;
-    c->part_bytes = 0;
-    e = hipMalloc((void **)&c->part, need);
-    if (e != hipSuccess) return hip_fail(c, e);
-    c->part_bytes = need;
+// Whether the context's scratch may grow now: not after okf_ctx_reserve, and
+// not while the stream is being captured into a graph (a synchronisation or
+// hipMalloc would invalidate the capture).
+inline bool can_grow(okf_ctx *c) {
+    if (c->reserved) return false;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(c->stream, &cs) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return cs == hipStreamCaptureStatusNone;
+}
+
+// Grows one scratch buffer to at least `need` bytes (the stream is drained
+// before an old buffer is freed).  Where it may not grow (can_grow) a call
+// that needs more is an OKF_E_SHAPE, so nothing on a reserved or captured
+// hot path allocates or synchronises.  `optional`: a failure leaves the
+// buffer as it was and records no HIP error (the caller runs without it).
+inline int grow_buf(okf_ctx *c, void **buf, size_t &bytes, size_t need, bool zero, bool optional) {
+    if (need <= bytes) return OKF_OK;
+    if (!can_grow(c)) return OKF_E_SHAPE;
+    hipError_t e = hipSuccess;
+    if (*buf) {
+        e = hipStreamSynchronize(c->stream);
+        if (e != hipSuccess) return optional ? ((void)hipGetLastError(), OKF_E_HIP) : hip_fail(c, e);
+        (void)hipFree(*buf);
+        *buf = nullptr;
+        bytes = 0;
+    }
+    e = hipMalloc(buf, need);
+    if (e == hipSuccess && zero) e = hipMemset(*buf, 0, need);
+    if (e != hipSuccess) {
+        if (*buf) (void)hipFree(*buf);
+        *buf = nullptr;
+        return optional ? ((void)hipGetLastError(), OKF_E_HIP) : hip_fail(c, e);
+    }
+    bytes = need;
     return OKF_OK;
+}
+
+// split-tile partial sums and argmax pairs
+inline int grow_part(okf_ctx *c, size_t need, bool optional = false) {
+    return grow_buf(c, (void **)&c->part, c->part_bytes, need, false, optional);
 }
 
 // argmax row counters, zeroed when allocated (the kernel leaves them zero)
 inline int grow_cnt(okf_ctx *c, size_t rows) {
-    if (rows <= c->cnt_n) return OKF_OK;
-    if (c->reserved) return OKF_E_SHAPE;
-    hipError_t e = hipStreamSynchronize(c->stream);
-    if (e != hipSuccess) return hip_fail(c, e);
-    if (c->cnt) (void)hipFree(c->cnt);
-    c->cnt = nullptr;
-    c->cnt_n = 0;
-    e = hipMalloc((void **)&c->cnt, rows * sizeof(uint32_t));
-    if (e == hipSuccess) e = hipMemset(c->cnt, 0, rows * sizeof(uint32_t));
-    if (e != hipSuccess) return hip_fail(c, e);
-    c->cnt_n = rows;
-    return OKF_OK;
+    size_t bytes = c->cnt_n * sizeof(uint32_t);
+    const int st = grow_buf(c, (void **)&c->cnt, bytes, rows * sizeof(uint32_t), true, false);
+    c->cnt_n = bytes / sizeof(uint32_t);
+    return st;
 }
 
-// the fp16 copy of a Q4_K GEMM's activations: N K values
-inline int grow_xh(okf_ctx *c, size_t need) {
-    if (need <= c->xh_bytes) return OKF_OK;
-    if (c->reserved) return OKF_E_SHAPE;
-    if (c->xh) {
-        hipError_t e = hipStreamSynchronize(c->stream);
-        if (e != hipSuccess) return hip_fail(c, e);
-        (void)hipFree(c->xh);
-        c->xh = nullptr;
-        c->xh_bytes = 0;
-    }
-    hipError_t e = hipMalloc((void **)&c->xh, need);
-    if (e != hipSuccess) return hip_fail(c, e);
-    c->xh_bytes = need;
-    return OKF_OK;
+// the fp16 copy of a GEMM's activations: N K values
+inline int grow_xh(okf_ctx *c, size_t need, bool optional = false) {
+    return grow_buf(c, (void **)&c->xh, c->xh_bytes, need, false, optional);
 }
 
 // The wide-tile Q4_K GEMM (gemm_q4k_w8_kernel): one 256 x 128 tile per CU.
@@ -597,7 +615,7 @@ int launch_gemm(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t 
     ks = (K + kper - 1) / kper;
     float *part = nullptr;
     if (ks > 1) {
-        if (grow_part(c, (size_t)ks * N * M * sizeof(float)) == OKF_OK) part = c->part;
+        if (grow_part(c, (size_t)ks * N * M * sizeof(float), true) == OKF_OK) part = c->part;
         else ks = 1;
     }
     // from N = 256 X is converted to fp16 once (every row tile would round
@@ -605,7 +623,7 @@ int launch_gemm(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t 
     // N = 512: Q2_0 6144 x 2048 58.9 -> 46.0, 2048 x 6144 52.0 -> 41.8; at
     // N = 64..128 the extra launch costs about what it saves)
     const _Float16 *xh = nullptr;
-    if (c->gemm_xh && N >= 256 && K % 32 == 0 && grow_xh(c, (size_t)N * K * sizeof(_Float16)) == OKF_OK) {
+    if (c->gemm_xh && N >= 256 && K % 32 == 0 && grow_xh(c, (size_t)N * K * sizeof(_Float16), true) == OKF_OK) {
         const uint64_t n4 = (uint64_t)N * K / 4;
         hipLaunchKernelGGL(x_to_f16_kernel, dim3((uint32_t)((n4 + 256 * XV - 1) / (256 * XV))), dim3(256), 0,
                            c->stream, X, c->xh, n4);
@@ -617,7 +635,7 @@ int launch_gemm(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t K, uint32_t 
     if (part) {
         const uint64_t nm = (uint64_t)N * M;
         hipLaunchKernelGGL(gemm_ksum_kernel, dim3((uint32_t)((nm + 1023) / 1024)), dim3(256), 0, c->stream,
-                           (const float *)part, Y, nm, ks);
+                           (const float *)part, Y, nm, ks, (uint32_t)(nm % 4 == 0 && aligned16(Y)));
     }
     return OKF_OK;
 }

@@ -364,7 +364,10 @@ int okf_ctx_create(int device, okf_ctx **out) {
         if (e == hipSuccess) e = hipGetSymbolAddress((void **)&c->scratch, HIP_SYMBOL(scratch));
         if (e == hipSuccess) e = hipMalloc((void **)&c->ffn_bar, FF_BAR_BYTES);
         if (e == hipSuccess) e = hipMemset(c->ffn_bar, 0, FF_BAR_BYTES);
+        if (e == hipSuccess) e = hipHostMalloc((void **)&c->ffn_status, sizeof(uint32_t), hipHostMallocMapped);
+        if (e == hipSuccess) *(volatile uint32_t *)c->ffn_status = 0;
         if (e != hipSuccess) {
+            if (c->ffn_status) (void)hipHostFree(c->ffn_status);
             if (c->ffn_bar) (void)hipFree(c->ffn_bar);
             if (c->grid) (void)hipFree(c->grid);
             if (c->grids) (void)hipFree(c->grids);
@@ -420,6 +423,7 @@ int okf_ctx_destroy(okf_ctx *c) {
         if (c->part) (void)hipFree(c->part);
         if (c->cnt) (void)hipFree(c->cnt);
         if (c->ffn_bar) (void)hipFree(c->ffn_bar);
+        if (c->ffn_status) (void)hipHostFree(c->ffn_status);
         (void)hipStreamDestroy(c->stream);
     }
     delete c;
@@ -511,6 +515,8 @@ int okf_ffn(okf_ctx *c, const okf_weight *gate, const okf_weight *up, const okf_
         if (gate->K != up->K || gate->M != up->M) return OKF_E_SHAPE;
         if (!aligned16(x) || !aligned16(g) || !aligned16(u)) return OKF_E_SHAPE;
         if ((st = begin(c))) return st;
+        // an earlier launch's barrier that gave up is this call's failure (nothing is launched)
+        if ((st = take_timeout(c))) return st;
         const FfnArgs a{(const uint8_t *)gate->base + gate->off, (const uint8_t *)up->base + up->off,
                         (const uint8_t *)down->base + down->off, rb0, rb1, gate->K, gate->M, down->M,
                         x, g, u, y, nullptr};
@@ -671,7 +677,8 @@ int okf_sync(okf_ctx *c) {
         if (st) return st;
     }
     hipError_t e = hipStreamSynchronize(c->stream);
-    return e == hipSuccess ? OKF_OK : hip_fail(c, e);
+    if (e != hipSuccess) return hip_fail(c, e);
+    return take_timeout(c);
 }
 
 int okf_set_fault_rate(okf_ctx *c, double rate, uint64_t seed) {
@@ -822,6 +829,7 @@ const char *okf_strerror(int s) {
     case OKF_E_IO: return "cannot open or map the file";
     case OKF_E_FORMAT: return "malformed GGUF file";
     case OKF_E_NOTFOUND: return "no such tensor or key";
+    case OKF_E_TIMEOUT: return "grid barrier timed out (outputs are NaN)";
     default: return "unknown status";
     }
 }

@@ -42,7 +42,9 @@ typedef enum {
     OKF_E_NODEV = 6,    /* detached context (device -1): nothing can run */
     OKF_E_IO = 7,       /* a file could not be opened or mapped */
     OKF_E_FORMAT = 8,   /* a malformed GGUF file (GGUFErr.parse) */
-    OKF_E_NOTFOUND = 9  /* no such tensor or key */
+    OKF_E_NOTFOUND = 9, /* no such tensor or key */
+    OKF_E_TIMEOUT = 10  /* a one-launch FFN's grid barrier gave up (its outputs hold NaN);
+                           reported by the next okf_sync or okf_ffn on the context */
 } okf_status;
 
 /* ggml type ids, LLM/Base/GGUF.swift:3-14 */
@@ -99,7 +101,8 @@ int okf_ctx_stream(okf_ctx *ctx, void **stream);
  * tile GEMM with N * K <= gemm_nk, and the pairs and row counters of
  * okf_argmax_rows over up to argmax_rows rows of argmax_n values.  Afterwards
  * no call allocates or synchronises; one that needs more scratch than
- * reserved returns OKF_E_SHAPE.  (The tile GEMM of the other formats uses
+ * reserved returns OKF_E_SHAPE.  Nor does any call allocate while the
+ * context's stream is being captured into a graph.  (The tile GEMM of the other formats uses
  * the same scratch for its K-split partials and fp16 activations where it
  * fits, and otherwise runs without them: one K range, or the activations
  * rounded per tile; the K split changes only the order of the fp32 sums.)
@@ -140,7 +143,9 @@ int okf_gemv_gate_up(okf_ctx *ctx, const okf_weight *gate, const okf_weight *up,
  * weight requested at the start.  That launch needs one workgroup resident
  * on every CU at once: work that a caller keeps running on other streams of
  * the same GPU can delay it, and a barrier that waits past its bound
- * (about 0.3 s) leaves NaN in y rather than wait forever
+ * (about 0.3 s) leaves NaN in every y row of that launch rather than wait
+ * forever; the next okf_sync then returns OKF_E_TIMEOUT once (or, with no
+ * okf_sync between, the next okf_ffn returns it and launches nothing)
  * (OKF_FFN_FUSED=0 at okf_ctx_create selects the two launches).  Otherwise two launches when gate and up
  * share a format: one grid whose workgroups each compute the same rows of
  * gate and up and form silu(g) * u there, then the down projection.
@@ -161,7 +166,12 @@ int okf_silu_mul(okf_ctx *ctx, float *a, const float *b, uint32_t n);
  * launches of 4 or 5 columns (for IQ2_XXS, and for every other K-quant and
  * i-quant format but Q6_K and IQ4_NL with K <= 6144 and M >= 4096, from N =
  * 5 on, in 4-column launches).  The results are the narrow kernels' for
- * those N. */
+ * those N.  Scratch: the tile GEMM uses the context's buffers (see
+ * okf_ctx_reserve).  The Q4_K tile GEMM needs them and returns OKF_E_SHAPE
+ * where they may not grow (a reserved context that is too small, or a stream
+ * being captured into a graph before they were grown); the other formats'
+ * tile GEMM then runs without them.  The matvec and narrow paths allocate
+ * nothing. */
 int okf_gemm(okf_ctx *ctx, const okf_weight *w, const float *X, uint32_t N, float *Y);
 
 /* MetalEnc.gemmTile (MetalEnc.swift:326-352): the tile GEMM for any N >= 1. */

@@ -557,12 +557,63 @@ def test_ffn_graph_replay(enc):
         hip.hipGraphDestroy(graph)
 
 
+# The tile GEMM of a non-Q4_K format captured into a HIP graph on a fresh,
+# unreserved context: the capture must not allocate or synchronise (its
+# scratch cannot grow while the stream is captured, so it runs without the
+# K split and the fp16 copy of X), and every replay must match the oracle and
+# the replays must agree bit for bit.  Eager calls run between the replays
+# (they may grow the scratch; the graph keeps its own launches).
+@pytest.mark.parametrize("t,M,K,N", [(Q8_0, 512, 1024, 64), (Q2_0, 2048, 1024, 300)])
+def test_tile_gemm_graph_capture_unreserved(t, M, K, N):
+    hip = ctypes.CDLL("libamdhip64.so")
+    vp = ctypes.c_void_p
+    e = ok.Enc(0)
+    try:
+        say("tile gemm graph capture", NAMES[t], M, K, N)
+        w = weights(t, M, K, 91)
+        qw = ok.QuantTensor(dev(w), K, M, t)
+        X = acts(N, K, 92)
+        Xd = dev(X)
+        Y = torch.full((N, M), float("nan"), device="cuda")
+        Ye = torch.zeros((N, M), device="cuda")
+        st = vp(e.stream)
+        graph, exe = vp(), vp()
+        assert hip.hipStreamBeginCapture(st, 0) == 0
+        e.gemm(qw, Xd, Y, N)
+        assert hip.hipStreamEndCapture(st, ctypes.byref(graph)) == 0
+        assert hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0) == 0
+        ref = oracle.matmul(t, w, K, M, X).astype(np.float64)
+        try:
+            outs = []
+            for rep in range(3):
+                Y.fill_(float("nan"))
+                torch.cuda.synchronize()
+                assert hip.hipGraphLaunch(exe, st) == 0
+                assert hip.hipStreamSynchronize(st) == 0
+                outs.append(host(Y))
+                e.gemm(qw, Xd, Ye, N)  # eager between the replays
+                e.sync()
+                assert rel(host(Ye), ref) <= TOL
+            for o in outs:
+                assert rel(o, ref) <= TOL
+                assert np.array_equal(o, outs[0])
+        finally:
+            hip.hipGraphExecDestroy(exe)
+            hip.hipGraphDestroy(graph)
+    finally:
+        e.close()
+
+
 # The grid barrier's bounded wait, forced from the host: OKF_FFN_STALL=1
 # makes the next launch's barrier wait for one arrival more than the grid
 # has, OKF_FFN_SPIN a short poll limit.  Every workgroup still finishes; the
 # call must fail loudly (NaN in y, never a plausible wrong value), and the
 # next call on the same context must give the normal result, bit for bit.
 def test_ffn_barrier_timeout_is_loud_and_recovers(enc):
+    # The master's barrier wait is forced to give up (it waits for one arrival
+    # more than the grid has, polls bounded from the host): every workgroup of
+    # that launch must fail (NaN in every output row), the next okf_sync must
+    # report OKF_E_TIMEOUT once, and the next launch must match a clean context.
     import os
     os.environ["OKF_FFN_STALL"], os.environ["OKF_FFN_SPIN"] = "1", "2000"
     try:
@@ -574,16 +625,40 @@ def test_ffn_barrier_timeout_is_loud_and_recovers(enc):
         wg, wu, wd = weights(Q2_0, H, D, 81), weights(Q2_0, H, D, 82), weights(Q2_0, D, H, 83)
         qg, qu, qd = (ok.QuantTensor(dev(w), k, m, Q2_0) for w, k, m in ((wg, D, H), (wu, D, H), (wd, H, D)))
         x = dev(acts(1, D, 84)[0])
-        outs = []
+        outs, codes = [], []
         for en in (e, e, enc):
             say("ffn barrier time-out", len(outs))
             g, u = torch.zeros(H, device="cuda"), torch.zeros(H, device="cuda")
             y = torch.zeros(D, device="cuda")
             en.ffn(qg, qu, qd, x, g, u, y)
-            en.sync()
+            try:
+                en.sync()
+                codes.append(ok.OKF_OK)
+            except ok.OkfError as err:
+                codes.append(err.status)
             outs.append(host(y))
-        assert np.isnan(outs[0]).any()
+        assert codes == [ok.OKF_E_TIMEOUT, ok.OKF_OK, ok.OKF_OK]
+        assert np.isnan(outs[0]).all()
         assert np.array_equal(outs[1], outs[2])
+        # a failure not yet collected by okf_sync is reported by the next okf_ffn
+        os.environ["OKF_FFN_STALL"], os.environ["OKF_FFN_SPIN"] = "1", "2000"
+        try:
+            e2 = ok.Enc(0)
+        finally:
+            del os.environ["OKF_FFN_STALL"], os.environ["OKF_FFN_SPIN"]
+        try:
+            y = torch.zeros(D, device="cuda")
+            g, u = torch.zeros(H, device="cuda"), torch.zeros(H, device="cuda")
+            e2.ffn(qg, qu, qd, x, g, u, y)
+            torch.cuda.synchronize()
+            with pytest.raises(ok.OkfError) as err:
+                e2.ffn(qg, qu, qd, x, g, u, y)
+            assert err.value.status == ok.OKF_E_TIMEOUT
+            e2.ffn(qg, qu, qd, x, g, u, y)
+            e2.sync()
+            assert np.array_equal(host(y), outs[2])
+        finally:
+            e2.close()
     finally:
         e.close()
 
