@@ -291,22 +291,32 @@ namespace okf {
 // group of a superblock); the kernel is gemm_q4k_w8_kernel below.
 constexpr int QG_BN = 128, QG_BK = 64;
 
-// v_bfi_b32 with 0x64006400: drops the masked bits of a into the mantissas of
-// two fp16 1024.0 (written out: the compiler splits the constant form).
-__device__ __forceinline__ uint32_t gbfi(uint32_t mask, uint32_t a) {
-    uint32_t r;
-    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(a), "v"(0x64006400u));
-    return r;
-}
-
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
+// 8 nibbles of two code dwords (v0, v1: the low nibbles, or the high ones
+// shifted down) as one MFMA A operand, fma(q, a, o) per weight in packed
+// fp16.  q reaches fp16 exactly through v_cvt_scalef32_pk_f16_fp8: a nibble
+// in the low bits of an e4m3 byte is q * 2^-9 (exponent field 0 or 1,
+// mantissa the low 3 bits), and the conversion's power-of-two scale 2^9
+// restores q.
+__device__ __forceinline__ u32x4v q4k_group_a(uint32_t v0, uint32_t v1, half2v a, half2v o) {
+    const uint32_t l0 = v0 & 0x0F0F0F0Fu, l1 = v1 & 0x0F0F0F0Fu;
+    const half2v q0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(l0, 512.0f, false);
+    const half2v q1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(l0, 512.0f, true);
+    const half2v q2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(l1, 512.0f, false);
+    const half2v q3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(l1, 512.0f, true);
+    return u32x4v{__builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q0, a, o)),
+                  __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q1, a, o)),
+                  __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q2, a, o)),
+                  __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q3, a, o))};
+}
 
 // Q4_K code group g (64 weights) of one row as the four MFMA A operands of a
 // 32x32x16 f16 step: lane half h holds the group's code bytes 16 h .. 16 h + 15
 // in qv, and operand kk, element e is weight k = 16 h + 8 (kk & 1) +
 // 32 (kk >> 1) + e of the group (low nibbles are k < 32, high nibbles k >= 32).
-// The weight is fma(q, fp16(d sc), fp16(-dmin m)) in packed fp16 (q exact as
-// 1024 + q - 1024); vf (0 or 1) scales d and dmin, so vf = 0 gives zeros.
+// The weight is fma(q, fp16(d sc), fp16(-dmin m)) in packed fp16 (q exact,
+// q4k_group_a); vf (0 or 1) scales d and dmin, so vf = 0 gives zeros.
 __device__ __forceinline__ void q4k_dq_mfma_a(const u32x4v hdr, const u32x4v qv, uint32_t g, float vf,
                                               u32x4v *a) {
     // every loaded dword counts as used here: a dword that a group does
@@ -318,28 +328,11 @@ __device__ __forceinline__ void q4k_dq_mfma_a(const u32x4v hdr, const u32x4v qv,
     const float d = h2f(hdr[0] & 0xFFFF) * vf, dmin = h2f(hdr[0] >> 16) * vf;
     const half2v a0 = (half2v)(_Float16)(d * (float)sc0), o0 = (half2v)(_Float16)(-dmin * (float)mn0);
     const half2v a1 = (half2v)(_Float16)(d * (float)sc1), o1 = (half2v)(_Float16)(-dmin * (float)mn1);
-    const half2v m1024 = (half2v)(_Float16)-1024.0f;
-    uint32_t lo[8], hi[8];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const uint32_t v = qv[i];
-        const uint32_t p01 = __builtin_amdgcn_perm(v, v, 0x0C010C00u);
-        const uint32_t p23 = __builtin_amdgcn_perm(v, v, 0x0C030C02u);
-        const uint32_t l01 = gbfi(0x000F000Fu, p01), l23 = gbfi(0x000F000Fu, p23);
-        const uint32_t h01 = gbfi(0x000F000Fu, p01 >> 4), h23 = gbfi(0x000F000Fu, p23 >> 4);
-        auto dq = [&](uint32_t x, half2v sa_, half2v so) {
-            const half2v q = __builtin_bit_cast(half2v, x) + m1024;
-            return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, sa_, so));
-        };
-        lo[2 * i] = dq(l01, a0, o0);
-        lo[2 * i + 1] = dq(l23, a0, o0);
-        hi[2 * i] = dq(h01, a1, o1);
-        hi[2 * i + 1] = dq(h23, a1, o1);
-    }
-    a[0] = u32x4v{lo[0], lo[1], lo[2], lo[3]};
-    a[1] = u32x4v{lo[4], lo[5], lo[6], lo[7]};
-    a[2] = u32x4v{hi[0], hi[1], hi[2], hi[3]};
-    a[3] = u32x4v{hi[4], hi[5], hi[6], hi[7]};
+    // q exact through the fp8 conversion (q4k_group_a), then fma(q, a, o)
+    a[0] = q4k_group_a(qv[0], qv[1], a0, o0);
+    a[1] = q4k_group_a(qv[2], qv[3], a0, o0);
+    a[2] = q4k_group_a(qv[0] >> 4, qv[1] >> 4, a1, o1);
+    a[3] = q4k_group_a(qv[2] >> 4, qv[3] >> 4, a1, o1);
 }
 
 // X fp32 -> fp16 (round to nearest even), XV float4 per thread with all
