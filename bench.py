@@ -139,6 +139,25 @@ def main():
             fn(h, base + (i % nrot) * step, nb, op)
         return time_calls(call, args.steps, 5)[0]
 
+    hip = ctypes.CDLL("libamdhip64.so")
+    cp_dst = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
+
+    def hbm_copy_time(nbytes):
+        """Seconds per device-to-device copy of nbytes (read nbytes, write
+        nbytes), the source rotated over rd_buf as the read ceiling's is:
+        hipMemcpyAsync on the library's stream, a second, independent method
+        beside okf_stream_read for the attainable bandwidth."""
+        nb = nbytes // 16 * 16
+        nrot = max(2, ROTATE_BYTES // nb)
+        step = (ROTATE_BYTES // nrot) // 256 * 256
+        base, dst = rd_buf.data_ptr(), cp_dst.data_ptr()
+        st = ctypes.c_void_p(enc.stream)
+
+        def call(i):
+            hip.hipMemcpyAsync(ctypes.c_void_p(dst), ctypes.c_void_p(base + (i % nrot) * step),
+                               ctypes.c_size_t(nb), 3, st)  # hipMemcpyDeviceToDevice
+        return time_calls(call, max(20, args.steps // 4), 5)[0]
+
     cpu_cores = None
 
     def cpu_config(name, t, M, K, N, ws_np, Xn, xs):
@@ -317,6 +336,11 @@ def main():
             rd_s = hbm_read_time(wbytes)
             rec["hbm_read_us"] = round(rd_s * 1e6, 3)
             rec["hbm_read_frac"] = round(wbytes / rd_s / HBM_PEAK, 4)
+            if wbytes <= cp_dst.numel():
+                # the same bytes copied by hipMemcpyAsync: (read + write) / time
+                cp_s = hbm_copy_time(wbytes)
+                rec["hbm_copy_us"] = round(cp_s * 1e6, 3)
+                rec["hbm_copy_frac"] = round(2 * wbytes / cp_s / HBM_PEAK, 4)
             # warm: the same call on one weight copy (L2 / MALL resident after the
             # first call; reported beside, not the measurement)
             warm_s, _ = time_calls(lambda i: call(0), n_calls, 3)
@@ -327,6 +351,23 @@ def main():
         suite.append(rec)
         del X, Ys
     wcache.clear()
+
+    # the attainable bandwidth, two independent methods at two sizes: the
+    # library's plain streaming read and hipMemcpyAsync (a copy moves 2x its
+    # size), rotated over the same >= 1 GiB
+    if want is None or "hbm_ceiling" in want:
+        rec = {"name": "hbm_ceiling", "bound": "hbm"}
+        for mb in (50, 512):
+            nb = mb * 1000 * 1000
+            if nb > cp_dst.numel():
+                cp_dst = torch.empty(nb, dtype=torch.uint8, device="cuda")
+            rd_s, cp_s = hbm_read_time(nb), hbm_copy_time(nb)
+            rec[f"read_{mb}MB_us"] = round(rd_s * 1e6, 3)
+            rec[f"read_{mb}MB_frac"] = round(nb / rd_s / HBM_PEAK, 4)
+            rec[f"copy_{mb}MB_us"] = round(cp_s * 1e6, 3)
+            rec[f"copy_{mb}MB_frac"] = round(2 * nb / cp_s / HBM_PEAK, 4)
+        log("bench:", json.dumps(rec))
+        suite.append(rec)
 
     # the FFN's neighbours: add + RMSNorm over a pp512 batch (x, r, w read,
     # x and y written) and argmax over one 248320-wide vocabulary row
