@@ -497,7 +497,7 @@ __global__ __launch_bounds__(512, 1) void gemm_q4k_w8_kernel(const uint8_t *__re
     lds_void *const xdst = (lds_void *)(&Bs[kh][0][0] + (wr * 4) * 1024);
 
     struct WRegs {
-        u32x4v h0, h1, q0, q1;
+        u32x4v q0, q1;
     };
     // local step l of this half: superblock sb0 + 2 (l / 4) + kh (clamped
     // to the row, so every load is unconditional), code group l % 4
@@ -505,14 +505,22 @@ __global__ __launch_bounds__(512, 1) void gemm_q4k_w8_kernel(const uint8_t *__re
     // (written out, like every load of the loop: the compiler's own count
     // of outstanding loads is lost once a direct-to-LDS load is in flight,
     // and it would wait for all of them; the waits below are explicit)
+    // the code bytes of step l, rows r and r + 32
     auto fetch_w = [&](uint32_t l, WRegs &r) {
-        const uint64_t sbo = (uint64_t)lsb(l) * 144, qo = sbo + 16 + (l & 3) * 32 + 16 * h;
-        asm volatile("global_load_dwordx4 %0, %4, off\n\t"
-                     "global_load_dwordx4 %1, %5, off\n\t"
-                     "global_load_dwordx4 %2, %6, off\n\t"
-                     "global_load_dwordx4 %3, %7, off"
-                     : "=&v"(r.h0), "=&v"(r.h1), "=&v"(r.q0), "=&v"(r.q1)
-                     : "v"(w0 + sbo), "v"(w1 + sbo), "v"(w0 + qo), "v"(w1 + qo));
+        const uint64_t qo = (uint64_t)lsb(l) * 144 + 16 + (l & 3) * 32 + 16 * h;
+        asm volatile("global_load_dwordx4 %0, %2, off\n\t"
+                     "global_load_dwordx4 %1, %3, off"
+                     : "=&v"(r.q0), "=&v"(r.q1)
+                     : "v"(w0 + qo), "v"(w1 + qo));
+    };
+    // the 16-byte header (d, dmin, packed scales) of step l's superblock:
+    // loaded once per superblock, it serves the superblock's four steps
+    auto fetch_h = [&](uint32_t l, u32x4v &h0, u32x4v &h1) {
+        const uint64_t sbo = (uint64_t)lsb(l) * 144;
+        asm volatile("global_load_dwordx4 %0, %2, off\n\t"
+                     "global_load_dwordx4 %1, %3, off"
+                     : "=&v"(h0), "=&v"(h1)
+                     : "v"(w0 + sbo), "v"(w1 + sbo));
     };
     // stage l % NST <- activations of local step l (4 direct loads per lane)
     auto fetch_x = [&](uint32_t l, uint32_t st) {
@@ -544,6 +552,8 @@ __global__ __launch_bounds__(512, 1) void gemm_q4k_w8_kernel(const uint8_t *__re
                      : "v"(addr));
     };
 
+    auto read_b1 = [&](uint32_t addr, u32x4v &b) { asm volatile("ds_read_b128 %0, %1" : "+v"(b) : "v"(addr)); };
+
     typedef float floatx16 __attribute__((ext_vector_type(16)));
     floatx16 acc[2][4];
 #pragma unroll
@@ -563,22 +573,34 @@ __global__ __launch_bounds__(512, 1) void gemm_q4k_w8_kernel(const uint8_t *__re
     //
     // The odd half issues step t + XD's activations before the barrier, while
     // its partners may still read stage t - 1: hence XD + 2 stages.
-    // Counting loads issued later (8 per step: 4 direct, 4 weight): at the
-    // even half's barrier the activations of step t are followed by
-    // 8 XD - 4 loads, at the odd half's by 8 XD + 4; the weights of step t
-    // at its dequant by 8 D - 4.
-    static_assert(NST == XD + 2, "stages");
-    constexpr int WAIT_X0 = 8 * XD - 4, WAIT_X1 = 8 * XD + 4, WAIT_W = 8 * D - 4;
+    static_assert(NST == XD + 2 && D == 2 && XD == 2, "stages and the wait counts below");
+    // Loads issued at step s: step s + 2's activations (4 direct loads) and
+    // code bytes (2), and at s % 4 == 2, after those, the next superblock's
+    // headers (2).  The prologue issues steps 0 and 1 and the first headers
+    // in the same order.  Counting the loads issued later, with s % 4 = jj
+    // static in the loop:
+    //   even half's barrier, step s's activations: 8, + 2 where headers
+    //     were issued at step s - 1 or s - 2 (jj 3, 0);
+    //   odd half's barrier: that + 6, + 2 more at jj 2;
+    //   the dequant's wait, step s's code bytes: 10, + 2 at jj 3, 0;
+    //   a superblock's end (jj 3), the headers and code bytes issued at jj 2:
+    //     6.
+    constexpr int WAIT_E[4] = {10, 8, 8, 10}, WAIT_O[4] = {16, 14, 16, 16}, WAIT_W[4] = {12, 10, 10, 12};
+    constexpr int WAIT_N = 6;
     WRegs r[D];
-    constexpr int PRE = D > XD ? D : XD;
-#pragma unroll
-    for (int k = -PRE; k < 0; k++) {
-        if (k + XD >= 0) fetch_x(k + XD, (k + XD) % NST);
-        __builtin_amdgcn_sched_barrier(0);
-        if (k + D >= 0) fetch_w(k + D, r[(k + D) % D]);
-        __builtin_amdgcn_sched_barrier(0);
-    }
-    static_assert(PRE == D && PRE == XD, "the prologue issues whole steps");
+    u32x4v hcur0, hcur1, hnext0, hnext1;  // superblock headers, rows r and r + 32
+    fetch_x(0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    fetch_w(0, r[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    fetch_h(0, hcur0, hcur1);
+    __builtin_amdgcn_sched_barrier(0);
+    fetch_x(1, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    fetch_w(1, r[1]);
+    __builtin_amdgcn_sched_barrier(0);
+    // (step 0's dequant waits for its code bytes only)
+    asm volatile("s_waitcnt vmcnt(6)" : "+v"(hcur0), "+v"(hcur1));
     const uint32_t nit = (sb1 - sb0 + 1) / 2;
     // one loop trip is a superblock: the code group and every ring slot are static
     static_assert(4 % D == 0 && 4 % NST == 0, "ring sizes divide the 4 steps of a superblock");
@@ -590,38 +612,60 @@ __global__ __launch_bounds__(512, 1) void gemm_q4k_w8_kernel(const uint8_t *__re
             // (a bare barrier: __syncthreads' release fence would wait for
             // every outstanding direct load, the prefetched ones included)
             if (kh == 0) {
-                asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(WAIT_X0));
+                asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(WAIT_E[jj]));
             }
             __builtin_amdgcn_sched_barrier(0);
             fetch_x(l + XD, (jj + XD) % NST);
             __builtin_amdgcn_sched_barrier(0);
             const float vf = sb0 + 2 * (l >> 2) + kh < sb1 ? 1.0f : 0.0f;
-            asm volatile("s_waitcnt vmcnt(%4)" : "+v"(rj.h0), "+v"(rj.h1), "+v"(rj.q0), "+v"(rj.q1) : "n"(WAIT_W));
+            asm volatile("s_waitcnt vmcnt(%4)"
+                         : "+v"(rj.q0), "+v"(rj.q1), "+v"(hcur0), "+v"(hcur1)
+                         : "n"(WAIT_W[jj]));
             u32x4v a[2][4];
-            dq_row(rj.h0, rj.q0, jj, vf, a[0]);
-            dq_row(rj.h1, rj.q1, jj, vf, a[1]);
+            dq_row(hcur0, rj.q0, jj, vf, a[0]);
+            dq_row(hcur1, rj.q1, jj, vf, a[1]);
             __builtin_amdgcn_sched_barrier(0);
             fetch_w(l + D, rj);
+            if (jj == 2) fetch_h(l + 2, hnext0, hnext1);
             __builtin_amdgcn_sched_barrier(0);
             if (kh != 0) {
-                asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(WAIT_X1));
+                asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(WAIT_O[jj]));
             }
             __builtin_amdgcn_sched_barrier(0);
             const uint32_t so = (jj % NST) * STAGE_B;
+            u32x4v b[4];
+            read_b(baddr[0] + so, b);
 #pragma unroll
             for (int kk = 0; kk < 4; kk++) {
-                u32x4v b[4];
-                read_b(baddr[kk] + so, b);
-                asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]));
 #pragma unroll
-                for (int i = 0; i < 2; i++)
+                for (int jn = 0; jn < 4; jn++) {
+                    // fragment jn of group kk: the reads issued after it are
+                    // group kk's jn + 1.. and group kk + 1's ..jn - 1
+                    asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(b[jn]) : "n"(kk < 3 ? 3 : 3 - jn));
 #pragma unroll
-                    for (int jn = 0; jn < 4; jn++)
+                    for (int i = 0; i < 2; i++)
                         acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
                             __builtin_bit_cast(half8, a[i][kk]), __builtin_bit_cast(half8, b[jn]), acc[i][jn], 0,
                             0, 0);
+                    __builtin_amdgcn_sched_barrier(0);
+                    // group kk + 1's fragment jn, into the same registers
+                    // (the MFMAs above have read them once issued), so the
+                    // LDS latency hides behind the MFMAs
+                    if (kk < 3) read_b1(baddr[kk + 1] + so + 4096 * jn, b[jn]);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
             }
             __builtin_amdgcn_sched_barrier(0);
+            if (jj == 3) {
+                // the next superblock's headers, issued a step ago, into
+                // the registers the next trip reads: a copy the compiler
+                // makes at the loop's back edge then moves landed data
+                asm volatile("s_waitcnt vmcnt(%4)"
+                             : "+v"(hnext0), "+v"(hnext1), "+v"(r[0].q0), "+v"(r[0].q1)
+                             : "n"(WAIT_N));
+                hcur0 = hnext0;
+                hcur1 = hnext1;
+            }
         }
     }
     // The loads issued past the end are still in flight: the direct ones
@@ -629,8 +673,8 @@ __global__ __launch_bounds__(512, 1) void gemm_q4k_w8_kernel(const uint8_t *__re
     // their data has landed (an asm output whose value is never read could
     // otherwise be handed to another value while the load still writes it).
 #pragma unroll
-    for (int j = 0; j < D; j++)
-        asm volatile("s_waitcnt vmcnt(0)" : "+v"(r[j].h0), "+v"(r[j].h1), "+v"(r[j].q0), "+v"(r[j].q1)::"memory");
+    for (int j = 0; j < D; j++) asm volatile("s_waitcnt vmcnt(0)" : "+v"(r[j].q0), "+v"(r[j].q1)::"memory");
+    asm volatile("" : "+v"(hnext0), "+v"(hnext1));
 
     // odd half -> even half, one row tile (i) at a time through LDS:
     // red[(wr * 64 + e) * 64 + lane], e = 16 jn + register

@@ -543,6 +543,7 @@ inline int launch_gemm_q4k_w(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t
     GemmSplit sp{};
     sp.tiles_n = tn;
     sp.tiles = tm * tn;
+    sp.ng = (uint32_t)c->gemm_ng;
     const uint32_t round = c->cus ? c->cus : 256, rem = sp.tiles % round;
     sp.full = sp.tiles - rem;
     sp.ks = rem ? std::min(c->gemm_ks > 0 ? (uint32_t)c->gemm_ks : round / rem, sbs) : 1;
@@ -573,7 +574,6 @@ inline int launch_gemm_q4k_w(okf_ctx *c, const uint8_t *W, uint64_t rb, uint32_t
     sp.full_xcd = sp.full / 8;
     sp.units = sp.ks > 1 ? rem * sp.ks : 0;
     sp.units_xcd = (sp.units + 7) / 8;
-    sp.ng = (uint32_t)c->gemm_ng;
     if (sp.units) {
         const int st = grow_part(c, (size_t)sp.units * QW_BM * QG_BN * sizeof(float));
         if (st) return st;
