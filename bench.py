@@ -251,7 +251,11 @@ def main():
             # okf_ffn is one launch (ffn_fused_kernel): the step's bytes are the
             # three weight matrices, x, g and u written, g read back, y
             ffn_alg = step_bytes + 4 * (K1 + 2 * M1 + M1 + K1)
-            dom = ("q2_0_ffn_step_okf_ffn", ffn_alg, step_gpu_t, "okf::ffn_fused_kernel<Q2_0>")
+            # (at this shape okf_ffn launches ffn_mfma_kernel, the integer
+            # matrix-core form; OKF_FFN_MFMA=0 gives ffn_fused_kernel)
+            kern = "okf::ffn_fused_kernel<Q2_0>" if os.environ.get("OKF_FFN_MFMA", "1") == "0" else \
+                "okf::ffn_mfma_kernel<2, 6>"
+            dom = ("q2_0_ffn_step_okf_ffn", ffn_alg, step_gpu_t, kern)
         elif gate_t >= down_t:
             dom = ("q2_0_matvec_gate_up_2x6144x2048", gate_np.nbytes + up_np.nbytes, gate_t, "okf::gemv_kernel<Q2_0>")
         else:

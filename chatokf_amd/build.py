@@ -3,6 +3,10 @@
 Usage: ``python -m chatokf_amd.build`` (or ``__graft_entry__.build()``).
 The library is compiled here, on the CPU, and travels to the GPU box as a
 file; nothing is compiled at import time.
+
+``python -m chatokf_amd.build --trace`` builds the diagnostic variant
+``libokf_quant_trace.so`` (compiled with OKF_TRACE: the one-launch FFN
+records per-workgroup phase timestamps, read by ``chatokf_amd/trace_ffn.py``).
 """
 import glob
 import os
@@ -18,6 +22,7 @@ CSRC = os.path.join(HERE, "csrc")
 SRCS = [os.path.join(CSRC, "okf_quant.hip")] + sorted(glob.glob(os.path.join(CSRC, "okf_fmt_*.hip")))
 LIB = os.path.join(HERE, "libokf_quant.so")
 OBJ = os.path.join(HERE, "_build")
+LIB_TRACE = os.path.join(HERE, "libokf_quant_trace.so")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
@@ -48,16 +53,18 @@ def _run(cmd, verbose):
         print(err, file=sys.stderr)
 
 
-def build(verbose: bool = False) -> str:
-    os.makedirs(OBJ, exist_ok=True)
-    objs = [os.path.join(OBJ, os.path.basename(src)[:-4] + ".o") for src in SRCS]
+def build(verbose: bool = False, trace: bool = False) -> str:
+    obj_dir, lib = (OBJ + "_trace", LIB_TRACE) if trace else (OBJ, LIB)
+    flags = FLAGS + (["-DOKF_TRACE"] if trace else []) + os.environ.get("OKF_XFLAGS", "").split()
+    os.makedirs(obj_dir, exist_ok=True)
+    objs = [os.path.join(obj_dir, os.path.basename(src)[:-4] + ".o") for src in SRCS]
     jobs = min(len(SRCS), int(os.environ.get("MAX_JOBS", os.cpu_count() or 4)), 16)
     with ThreadPoolExecutor(jobs) as ex:
-        list(ex.map(lambda so: _run([HIPCC, *FLAGS, "-c", so[0], "-o", so[1]], verbose), zip(SRCS, objs)))
-    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", LIB + ".tmp"], verbose)
-    os.replace(LIB + ".tmp", LIB)
-    return LIB
+        list(ex.map(lambda so: _run([HIPCC, *flags, "-c", so[0], "-o", so[1]], verbose), zip(SRCS, objs)))
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", lib + ".tmp"], verbose)
+    os.replace(lib + ".tmp", lib)
+    return lib
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    print(build(verbose=True, trace="--trace" in sys.argv[1:]))

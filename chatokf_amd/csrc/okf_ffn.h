@@ -25,6 +25,27 @@
 
 namespace okf {
 
+// Phase timestamps (a diagnostic build only, compiled with OKF_TRACE): each
+// workgroup takes s_memrealtime (a 100 MHz counter common to the device) at
+// FF_TRACE_N points and thread 0 writes them at the end into slot
+// epoch % FF_TRACE_L of a ring of launches (the barrier's epoch numbers the
+// launches), so that a run of back-to-back launches can be read afterwards
+// with okf_ffn_trace_read (okf_fmt_q2_0.hip, same build).  Points 3 and 6
+// add a workgroup barrier so that they mark the last wavefront.
+#ifdef OKF_TRACE
+constexpr uint32_t FF_TRACE_N = 8, FF_TRACE_WG = 256, FF_TRACE_L = 64;
+static __device__ uint64_t ff_trace[FF_TRACE_L * FF_TRACE_WG * FF_TRACE_N];
+#define FF_MARK(k) ftr[k] = __builtin_amdgcn_s_memrealtime()
+#define FF_SYNC_MARK(k) \
+    do {                \
+        __syncthreads(); \
+        FF_MARK(k);     \
+    } while (0)
+#else
+#define FF_MARK(k) ((void)0)
+#define FF_SYNC_MARK(k) ((void)0)
+#endif
+
 constexpr uint32_t FF_SPIN = 1u << 20;  // default barrier polls before giving up (~0.3 s)
 // the barrier's words, each on its own 256-byte line (FF_LINE uint32):
 // FF_SUB 64-bit arrival counters, FF_SUB 64-bit release flags, the
@@ -84,7 +105,8 @@ struct FfnArgs {
 // has returned before any later load is issued (the loop exit depends on
 // its value), and the asm waits carry a memory clobber so that the compiler
 // moves no memory access across them.
-__device__ __forceinline__ bool ff_grid_sync(uint32_t *bar, uint32_t spin, uint32_t stall, uint32_t *status) {
+__device__ __forceinline__ bool ff_grid_sync(uint32_t *bar, uint32_t spin, uint32_t stall, uint32_t *status,
+                                             uint64_t *epoch_out = nullptr) {
     __shared__ uint64_t epoch;
     __shared__ uint32_t ok;
     uint64_t *cnt = (uint64_t *)bar;             // counter k at cnt[k * FF_LINE / 2]
@@ -102,6 +124,7 @@ __device__ __forceinline__ bool ff_grid_sync(uint32_t *bar, uint32_t spin, uint3
     }
     __syncthreads();
     const uint64_t e = epoch;
+    if (epoch_out) *epoch_out = e;
     if (blockIdx.x == 0 && threadIdx.x < 64) {
         const uint32_t k = threadIdx.x, mk = k < FF_SUB ? (nb - k + FF_SUB - 1) / FF_SUB : 0;
         const uint64_t target = (e + 1) * mk + (k == 0 ? stall : 0);
@@ -226,6 +249,10 @@ __global__ __launch_bounds__(T) void ffn_fused_kernel(FfnArgs a) {
     const uint32_t W = gridDim.x * FF_WAVES, w0 = blockIdx.x * FF_WAVES + (tid >> 6);
     const uint32_t una = a.ka / UW, unb = a.ma / UW;
     const uint32_t half = lane >> 5, lh = lane & 31;
+#ifdef OKF_TRACE
+    uint64_t ftr[FF_TRACE_N] = {}, fep = 0;
+#endif
+    FF_MARK(0);  // start
 
     // x's loads, then every weight load of both phases; x of gate / up is at
     // most UA * 32 units, UA rounds of slots.  The loads are unconditional
@@ -235,14 +262,16 @@ __global__ __launch_bounds__(T) void ffn_fused_kernel(FfnArgs a) {
     float xv[XR][1][8];
     ff_load_x<F, T, XR>(a.x, a.ka, xv);
     __builtin_amdgcn_sched_barrier(0);
-    Unit<F, 1> wa[RA][UA];
+    // (a lane's RA gate / up rows in one Unit: their units meet the same
+    // activations, read from LDS once for all of them)
+    Unit<F, RA> wa[UA];
     Unit<F, 1> wb[RB][UB];
+    {
+        const uint8_t *rows[RA];
 #pragma unroll
-    for (int p = 0; p < RA; p++) {
-        const uint32_t r = min(w0 + p * W, a.ma - 1);
-        const uint8_t *rows[1] = {(half ? a.wu : a.wg) + (uint64_t)r * a.rba};
+        for (int p = 0; p < RA; p++) rows[p] = (half ? a.wu : a.wg) + (uint64_t)min(w0 + p * W, a.ma - 1) * a.rba;
 #pragma unroll
-        for (int j = 0; j < UA; j++) load_unit<F, 1>(rows, min(lh + 32 * j, una - 1), wa[p][j]);
+        for (int j = 0; j < UA; j++) load_unit<F, RA>(rows, min(lh + 32 * j, una - 1), wa[j]);
     }
 #pragma unroll
     for (int p = 0; p < RB; p++) {
@@ -252,26 +281,33 @@ __global__ __launch_bounds__(T) void ffn_fused_kernel(FfnArgs a) {
         for (int j = 0; j < UB; j++) load_unit<F, 1>(rows, min(lane + 64 * j, unb - 1), wb[p][j]);
     }
     __builtin_amdgcn_sched_barrier(0);
+    FF_MARK(1);  // every load issued (wavefront 0)
+#ifdef FF_WAITALL
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    FF_MARK(1);
+#endif
 
     // phase A: gate and up
     floatx4 *gdp;
     ff_stage_x<F, T, XR>(xv, a.ka, xs, gdp);
     __syncthreads();
+    FF_MARK(2);  // x in, staged
     {
         const uint32_t cs = ff_cs<F>(a.ka), gcs = cs / (unit_chunks<F>() * 4) * UG;
+        float acc[RA][1] = {};
+#pragma unroll
+        for (int j = 0; j < UA; j++) {
+            const uint32_t uu = lh + 32 * j;
+            if (uu < una)
+                Compute<F, 1, RA>::run(wa[j], XLds{xs + xs_index<F, L>(uu, 0), 4 * L, cs, gdp + uu * UG, gcs}, uu,
+                                       acc, nullptr);
+        }
 #pragma unroll
         for (int p = 0; p < RA; p++) {
             const uint32_t r = w0 + p * W;
             if (r < a.ma) {  // (the whole wavefront)
-                float acc[1][1] = {{0.0f}};
-#pragma unroll
-                for (int j = 0; j < UA; j++) {
-                    const uint32_t uu = lh + 32 * j;
-                    if (uu < una)
-                        Compute<F, 1, 1>::run(wa[p][j], XLds{xs + xs_index<F, L>(uu, 0), 4 * L, cs, gdp + uu * UG, gcs},
-                                              uu, acc, nullptr);
-                }
-                float v = acc[0][0];
+                float v = acc[p][0];
 #pragma unroll
                 for (int m = 16; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
                 const float up = __shfl(v, 32, 64);
@@ -282,12 +318,19 @@ __global__ __launch_bounds__(T) void ffn_fused_kernel(FfnArgs a) {
             }
         }
     }
+    FF_SYNC_MARK(3);  // phase A done
+#ifdef OKF_TRACE
+    const bool synced = ff_grid_sync(a.bar, a.spin, a.stall, a.status, &fep);
+#else
     const bool synced = ff_grid_sync(a.bar, a.spin, a.stall, a.status);
+#endif
+    FF_MARK(4);  // released
 
     // phase B: down on g (staged after the barrier, so every row of it is in)
     constexpr int XB = (UB * 64 * unit_weights<F>() / 8 + T - 1) / T;
     ff_stage_g<F, T, XB>(a.g, a.ma, xs, gdp);
     __syncthreads();
+    FF_MARK(5);  // g in, staged
     {
         const uint32_t cs = ff_cs<F>(a.ma), gcs = cs / (unit_chunks<F>() * 4) * UG;
 #pragma unroll
@@ -311,6 +354,15 @@ __global__ __launch_bounds__(T) void ffn_fused_kernel(FfnArgs a) {
             }
         }
     }
+    FF_SYNC_MARK(6);  // phase B done
+#ifdef OKF_TRACE
+    if (threadIdx.x == 0 && blockIdx.x < FF_TRACE_WG) {
+        uint64_t *o = ff_trace + ((fep % FF_TRACE_L) * FF_TRACE_WG + blockIdx.x) * FF_TRACE_N;
+        ftr[7] = fep;
+#pragma unroll
+        for (uint32_t k = 0; k < FF_TRACE_N; k++) o[k] = ftr[k];
+    }
+#endif
 }
 
 }  // namespace okf

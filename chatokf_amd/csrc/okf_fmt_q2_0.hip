@@ -1,5 +1,6 @@
 // okf_fmt_q2_0.hip -- the launchers (and with them the kernels) of Q2_0.
 #include "okf_impl.h"
+#include "okf_ffn_mfma.h"
 
 namespace okf_impl {
 OKF_INSTANTIATE(Q2_0)
@@ -23,6 +24,39 @@ bool launch_ffn_fused(okf_ctx *c, const FfnArgs &a0) {
     };
     const size_t lds = std::max(stage_bytes(una), stage_bytes(unb));
     if (lds > c->max_lds) return false;
+    // the Bonsai shape on the integer matrix cores (okf_ffn_mfma.h): gate /
+    // up 6144 x 2048, down 2048 x 6144, at most 24 gate / up rows and 16
+    // down rows a workgroup
+    if (c->ffn_mfma && a0.ka == 2048 && a0.ma == 6144 && c->cus) {
+        const void *fn = (const void *)ffn_mfma_kernel<2, 6>;
+        const size_t lb = fm_lds_bytes(6144);
+        int &nb = c->ffn_nb[3];
+        if (nb == 0) {
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, (int)FM_T, lb) != hipSuccess || nb < 1) {
+                (void)hipGetLastError();
+                nb = -1;
+            }
+        }
+        const int wg = std::max(c->ffn_wg, 1);
+        const uint32_t G = (uint32_t)wg * c->cus;
+        if (nb >= wg && lb <= c->max_lds && (a0.ma + G - 1) / G <= FM_RA && (a0.mb + G - 1) / G <= FM_RB) {
+            FfnArgs a = a0;
+            a.bar = c->ffn_bar;
+            a.status = c->ffn_status;
+            a.spin = c->ffn_spin > 0 ? (uint32_t)c->ffn_spin : FF_SPIN;
+            a.stall = c->ffn_stall > 0 ? 1u : 0u;
+            void *args[] = {&a};
+            const hipError_t e =
+                c->ffn_coop ? hipLaunchCooperativeKernel(fn, dim3(G), dim3(FM_T), args, (unsigned)lb, c->stream)
+                            : hipLaunchKernel(fn, dim3(G), dim3(FM_T), args, lb, c->stream);
+            if (e != hipSuccess) {
+                (void)hipGetLastError();
+                return false;
+            }
+            if (c->ffn_stall > 0) c->ffn_stall--;
+            return true;
+        }
+    }
     struct Var {
         const void *fn;
         uint32_t threads, ra, rb;  // ra = rb = 0: the general instance
@@ -70,3 +104,13 @@ bool launch_ffn_fused(okf_ctx *c, const FfnArgs &a0) {
     return false;
 }
 }  // namespace okf_impl
+
+#ifdef OKF_TRACE
+// the phase timestamps of the last FF_TRACE_L ffn_fused_kernel launches
+// (okf_ffn.h): n values, [slot][workgroup][point], point 7 the epoch
+extern "C" int okf_ffn_trace_read(uint64_t *host, uint32_t n) {
+    if (n > okf::FF_TRACE_L * okf::FF_TRACE_WG * okf::FF_TRACE_N) return OKF_E_SHAPE;
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(okf::ff_trace), (size_t)n * sizeof(uint64_t), 0,
+                               hipMemcpyDeviceToHost) == hipSuccess ? OKF_OK : OKF_E_HIP;
+}
+#endif

@@ -80,7 +80,8 @@ struct okf_ctx {
     int ffn_fused = 1;            // okf_ffn as one launch with a grid barrier where it fits (0: two launches)
     int ffn_wg = 1;               // its workgroups per CU, at most
     int ffn_coop = 0;             // launched with hipLaunchCooperativeKernel (1) or as a plain grid
-    int ffn_nb[3] = {0, 0, 0};    // its kernels' resident workgroups per CU (0: not yet queried)
+    int ffn_mfma = 1;             // the Bonsai shape on the integer matrix cores (ffn_mfma_kernel; 0: off)
+    int ffn_nb[4] = {0, 0, 0, 0}; // its kernels' resident workgroups per CU (0: not yet queried)
     int ffn_spin = 0;             // its barrier's poll limit (0: FF_SPIN)
     int ffn_stall = 0;            // its next launches whose barrier must time out (failure tests)
     int ffn_t = 0;                // its exact-fit variant: threads a workgroup (0: the default, 512)
