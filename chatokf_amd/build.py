@@ -55,7 +55,7 @@ def _run(cmd, verbose):
 
 def build(verbose: bool = False, trace: bool = False) -> str:
     obj_dir, lib = (OBJ + "_trace", LIB_TRACE) if trace else (OBJ, LIB)
-    flags = FLAGS + (["-DOKF_TRACE"] if trace else []) + os.environ.get("OKF_XFLAGS", "").split()
+    flags = FLAGS + (["-DOKF_TRACE"] if trace else [])
     os.makedirs(obj_dir, exist_ok=True)
     objs = [os.path.join(obj_dir, os.path.basename(src)[:-4] + ".o") for src in SRCS]
     jobs = min(len(SRCS), int(os.environ.get("MAX_JOBS", os.cpu_count() or 4)), 16)

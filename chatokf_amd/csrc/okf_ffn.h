@@ -282,11 +282,6 @@ __global__ __launch_bounds__(T) void ffn_fused_kernel(FfnArgs a) {
     }
     __builtin_amdgcn_sched_barrier(0);
     FF_MARK(1);  // every load issued (wavefront 0)
-#ifdef FF_WAITALL
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    FF_MARK(1);
-#endif
 
     // phase A: gate and up
     floatx4 *gdp;
