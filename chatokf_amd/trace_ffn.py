@@ -1,4 +1,5 @@
-"""Per-phase timestamps of the one-launch FFN (ffn_fused_kernel) on a GPU.
+"""Per-phase timestamps of the one-launch FFN (ffn_mfma_kernel at the Bonsai
+shape, ffn_fused_kernel otherwise) on a GPU.
 
 Usage (after ``python -m chatokf_amd.build --trace``)::
 
@@ -11,9 +12,10 @@ Loads the diagnostic library ``libokf_quant_trace.so`` (built with
 OKF_TRACE: every workgroup records s_memrealtime, a 100 MHz device counter,
 at seven points of each launch), runs the benchmark's FFN step (Q2_0 gate /
 up 6144 x 2048 with the SiLU, down 2048 x 6144, weights rotated over >= 1 GiB
-of copies like bench.py) back to back, and prints a markdown summary:
-per phase the median over launches of the workgroups' minimum, median and
-maximum time, and per launch its span and the gap to the next launch.
+of copies like bench.py) back to back, once with each one-launch kernel,
+and prints a markdown summary per kernel: per phase the median over
+launches of the workgroups' minimum, median and maximum time, and per
+launch its span and the gap to the next launch.
 """
 import argparse
 import ctypes
@@ -45,35 +47,15 @@ PHASES = [
 ]
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--launches", type=int, default=L)
-    args = ap.parse_args()
-    n = min(args.launches, L)
-    H, D = 6144, 2048
-    enc = ok.Enc(0)
+def trace(enc, refs, ptrs, n):
+    """Runs n okf_ffn calls back to back on enc after a warm-up; returns the
+    markdown rows of the phase table and the wall time a call."""
     lib = enc._lib
     lib.okf_ffn_trace_read.argtypes = [ctypes.c_void_p, ctypes.c_uint32]
-
-    def rotated(w_np):
-        base = torch.from_numpy(w_np).cuda()
-        return [base] + [base.clone() for _ in range(max(1, (1 << 30) // w_np.nbytes))]
-
-    gates = rotated(synth.q2_0(H, D, 1002))
-    ups = rotated(synth.q2_0(H, D, 1202))
-    downs = rotated(synth.q2_0(D, H, 1102))
-    nrot = len(gates)
-    gw = [ok.QuantTensor(g, D, H, ok.Q2_0).c() for g in gates]
-    uw = [ok.QuantTensor(u, D, H, ok.Q2_0).c() for u in ups]
-    dw = [ok.QuantTensor(d, H, D, ok.Q2_0).c() for d in downs]
-    refs = [(ctypes.byref(g), ctypes.byref(u), ctypes.byref(d)) for g, u, d in zip(gw, uw, dw)]
-    x = torch.from_numpy(synth.activations(1, D, 2002)).cuda()
-    h, h2, y = torch.empty(H, device="cuda"), torch.empty(H, device="cuda"), torch.empty(D, device="cuda")
-    ptrs = [t.data_ptr() for t in (x, h, h2, y)]
     ffn = lib.okf_ffn
 
     def step(i):
-        gr, ur, dr = refs[i % nrot]
+        gr, ur, dr = refs[i % len(refs)]
         if ffn(enc.h, gr, ur, dr, *ptrs):
             raise RuntimeError("okf_ffn failed")
 
@@ -106,19 +88,52 @@ def main():
         spans.append((tt[:, 6].max() - start) * us)
         if j + 1 < len(runs) and runs[j + 1][0] == e + 1:
             gaps.append((t[runs[j + 1][1], :, 0].min() - tt[:, 6].max()) * us)
-    print(f"# q2_0 FFN step (okf_ffn, ffn_fused_kernel): phase timestamps\n")
-    print(f"{len(runs)} back-to-back launches, {WG} workgroups each; wall {wall * 1e6:.2f} us per okf_ffn call "
-          f"in this run (trace build).  Times in us, medians over the launches.\n")
-    print("| phase | what ends it | min WG | median WG | max WG |")
-    print("|---|---|---:|---:|---:|")
-    print(f"| start spread | last workgroup's start after the first's | | | {np.median(starts):.2f} |")
+    out = [f"{len(runs)} back-to-back launches, {WG} workgroups each; wall {wall * 1e6:.2f} us per okf_ffn call "
+           f"in this run (trace build).  Times in us, medians over the launches.\n",
+           "| phase | what ends it | min WG | median WG | max WG |", "|---|---|---:|---:|---:|",
+           f"| start spread | last workgroup's start after the first's | | | {np.median(starts):.2f} |"]
     for name, a, b, what in PHASES:
         m = np.median(np.array(rows[name]), axis=0)
-        print(f"| {name} | {what} | {m[0]:.2f} | {m[1]:.2f} | {m[2]:.2f} |")
-    print(f"| launch span | first start -> last end | | {np.median(spans):.2f} | |")
+        out.append(f"| {name} | {what} | {m[0]:.2f} | {m[1]:.2f} | {m[2]:.2f} |")
+    out.append(f"| launch span | first start -> last end | | {np.median(spans):.2f} | |")
     if gaps:
-        print(f"| gap | last end -> next launch's first start | {np.min(gaps):.2f} | {np.median(gaps):.2f} | "
-              f"{np.max(gaps):.2f} |")
+        out.append(f"| gap | last end -> next launch's first start | {np.min(gaps):.2f} | {np.median(gaps):.2f} | "
+                   f"{np.max(gaps):.2f} |")
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--launches", type=int, default=L)
+    args = ap.parse_args()
+    n = min(args.launches, L)
+    H, D = 6144, 2048
+
+    def rotated(w_np):
+        base = torch.from_numpy(w_np).cuda()
+        return [base] + [base.clone() for _ in range(max(1, (1 << 30) // w_np.nbytes))]
+
+    gates = rotated(synth.q2_0(H, D, 1002))
+    ups = rotated(synth.q2_0(H, D, 1202))
+    downs = rotated(synth.q2_0(D, H, 1102))
+    gw = [ok.QuantTensor(g, D, H, ok.Q2_0).c() for g in gates]
+    uw = [ok.QuantTensor(u, D, H, ok.Q2_0).c() for u in ups]
+    dw = [ok.QuantTensor(d, H, D, ok.Q2_0).c() for d in downs]
+    refs = [(ctypes.byref(g), ctypes.byref(u), ctypes.byref(d)) for g, u, d in zip(gw, uw, dw)]
+    x = torch.from_numpy(synth.activations(1, D, 2002)).cuda()
+    h, h2, y = torch.empty(H, device="cuda"), torch.empty(H, device="cuda"), torch.empty(D, device="cuda")
+    ptrs = [t.data_ptr() for t in (x, h, h2, y)]
+    print("# q2_0_ffn_step_okf_ffn: phase timestamps of the one-launch FFN\n")
+    print("Command (run from the repository root on one MI355X, after `python -m chatokf_amd.build --trace`):\n")
+    print(f"    python chatokf_amd/trace_ffn.py --launches {n}\n")
+    # the context reads OKF_FFN_MFMA when it is created
+    for title, mf in (("ffn_mfma_kernel (the default at this shape)", "1"),
+                      ("ffn_fused_kernel (OKF_FFN_MFMA=0, the VALU digit-plane form)", "0")):
+        os.environ["OKF_FFN_MFMA"] = mf
+        enc = ok.Enc(0)
+        print(f"## {title}\n")
+        print("\n".join(trace(enc, refs, ptrs, n)) + "\n")
+        enc.close()
 
 
 if __name__ == "__main__":
