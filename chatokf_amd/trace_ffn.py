@@ -28,7 +28,9 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 if "chatokf_amd" in sys.modules:
     raise SystemExit("run this file directly (python chatokf_amd/trace_ffn.py), not with -m")
-os.environ["OKF_LIB"] = os.path.join(HERE, "libokf_quant_trace.so")
+# (--lib PATH: another build with OKF_TRACE; read here, before the import)
+_lib = sys.argv[sys.argv.index("--lib") + 1] if "--lib" in sys.argv else os.path.join(HERE, "libokf_quant_trace.so")
+os.environ["OKF_LIB"] = os.path.abspath(_lib)
 sys.path.insert(0, os.path.dirname(HERE))
 
 import torch  # noqa: E402
@@ -105,6 +107,8 @@ def trace(enc, refs, ptrs, n):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--launches", type=int, default=L)
+    ap.add_argument("--lib", help="a library built with OKF_TRACE (default: libokf_quant_trace.so)")
+    ap.add_argument("--mfma-only", action="store_true", help="trace ffn_mfma_kernel only")
     args = ap.parse_args()
     n = min(args.launches, L)
     H, D = 6144, 2048
@@ -127,8 +131,9 @@ def main():
     print("Command (run from the repository root on one MI355X, after `python -m chatokf_amd.build --trace`):\n")
     print(f"    python chatokf_amd/trace_ffn.py --launches {n}\n")
     # the context reads OKF_FFN_MFMA when it is created
-    for title, mf in (("ffn_mfma_kernel (the default at this shape)", "1"),
-                      ("ffn_fused_kernel (OKF_FFN_MFMA=0, the VALU digit-plane form)", "0")):
+    variants = (("ffn_mfma_kernel (the default at this shape)", "1"),
+                ("ffn_fused_kernel (OKF_FFN_MFMA=0, the VALU digit-plane form)", "0"))
+    for title, mf in variants[:1] if args.mfma_only else variants:
         os.environ["OKF_FFN_MFMA"] = mf
         enc = ok.Enc(0)
         print(f"## {title}\n")
