@@ -161,8 +161,8 @@ __global__ __launch_bounds__(FM_T) void ffn_mfma_kernel(FfnArgs a) {
 #endif
     FF_MARK(0);
 
-    // x's loads first (slot tid of KA / 8), then every weight load of both
-    // phases, unconditional (columns past the rows re-read the last row)
+    // x's loads first (slot tid of KA / 8), then gate / up's weight loads,
+    // unconditional (columns past the rows re-read the last row)
     float xv[8];
     {
         const uint32_t s = min(tid, KA / 8 - 1), u = s >> 3;
@@ -188,14 +188,6 @@ __global__ __launch_bounds__(FM_T) void ffn_mfma_kernel(FfnArgs a) {
             ca[t][i] = ldu<uint3>(row + (uint64_t)(w * NBA + i) * 34 + lo);
         }
     }
-    {
-        const uint32_t r = min(blockIdx.x * RB + min(col, RB - 1), a.mb - 1);
-        const uint8_t *row = a.wd + (uint64_t)r * a.rbb;
-#pragma unroll
-        for (int i = 0; i < NBB; i++) {
-            cb[i] = ldu<uint3>(row + (uint64_t)(w * NBB + i) * 34 + lo);
-        }
-    }
     __builtin_amdgcn_sched_barrier(0);
     FF_MARK(1);
 
@@ -205,6 +197,17 @@ __global__ __launch_bounds__(FM_T) void ffn_mfma_kernel(FfnArgs a) {
     fm_stage_slot(xv, tid, tid < KA / 8, planes, KA, gd);
     __syncthreads();
     FF_MARK(2);
+    // the down projection's weights only now: issued at the start they
+    // shared the first microseconds' stream with gate / up's, which phase A
+    // waits for (launch span 8.6 -> 8.1 us); they arrive during phase A and
+    // the barrier
+    {
+        const uint32_t r = min(blockIdx.x * RB + min(col, RB - 1), a.mb - 1);
+        const uint8_t *row = a.wd + (uint64_t)r * a.rbb;
+#pragma unroll
+        for (int i = 0; i < NBB; i++) cb[i] = ldu<uint3>(row + (uint64_t)(w * NBB + i) * 34 + lo);
+    }
+    __builtin_amdgcn_sched_barrier(0);
 
     // phase A: three tiles of gate / up columns
     {
