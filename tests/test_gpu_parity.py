@@ -609,25 +609,35 @@ def test_tile_gemm_graph_capture_unreserved(t, M, K, N):
 # has, OKF_FFN_SPIN a short poll limit.  Every workgroup still finishes; the
 # call must fail loudly (NaN in y, never a plausible wrong value), and the
 # next call on the same context must give the normal result, bit for bit.
-def test_ffn_barrier_timeout_is_loud_and_recovers(enc):
+@pytest.mark.parametrize("mfma", ["1", "0"])
+def test_ffn_barrier_timeout_is_loud_and_recovers(mfma):
     # The master's barrier wait is forced to give up (it waits for one arrival
     # more than the grid has, polls bounded from the host): every workgroup of
     # that launch must fail (NaN in every output row), the next okf_sync must
-    # report OKF_E_TIMEOUT once, and the next launch must match a clean context.
+    # report OKF_E_TIMEOUT once, and the next launch must match a clean context
+    # of the same kernel (mfma "1": ffn_mfma_kernel, "0": ffn_fused_kernel).
     import os
-    os.environ["OKF_FFN_STALL"], os.environ["OKF_FFN_SPIN"] = "1", "2000"
-    try:
-        e = ok.Enc(0)
-    finally:
-        del os.environ["OKF_FFN_STALL"], os.environ["OKF_FFN_SPIN"]
+
+    def ctx(stall):
+        env = {"OKF_FFN_MFMA": mfma}
+        if stall:
+            env.update(OKF_FFN_STALL="1", OKF_FFN_SPIN="2000")
+        os.environ.update(env)
+        try:
+            return ok.Enc(0)
+        finally:
+            for k in env:
+                del os.environ[k]
+
+    e, clean = ctx(True), ctx(False)
     try:
         H, D = 6144, 2048
         wg, wu, wd = weights(Q2_0, H, D, 81), weights(Q2_0, H, D, 82), weights(Q2_0, D, H, 83)
         qg, qu, qd = (ok.QuantTensor(dev(w), k, m, Q2_0) for w, k, m in ((wg, D, H), (wu, D, H), (wd, H, D)))
         x = dev(acts(1, D, 84)[0])
         outs, codes = [], []
-        for en in (e, e, enc):
-            say("ffn barrier time-out", len(outs))
+        for en in (e, e, clean):
+            say("ffn barrier time-out", mfma, len(outs))
             g, u = torch.zeros(H, device="cuda"), torch.zeros(H, device="cuda")
             y = torch.zeros(D, device="cuda")
             en.ffn(qg, qu, qd, x, g, u, y)
@@ -641,11 +651,7 @@ def test_ffn_barrier_timeout_is_loud_and_recovers(enc):
         assert np.isnan(outs[0]).all()
         assert np.array_equal(outs[1], outs[2])
         # a failure not yet collected by okf_sync is reported by the next okf_ffn
-        os.environ["OKF_FFN_STALL"], os.environ["OKF_FFN_SPIN"] = "1", "2000"
-        try:
-            e2 = ok.Enc(0)
-        finally:
-            del os.environ["OKF_FFN_STALL"], os.environ["OKF_FFN_SPIN"]
+        e2 = ctx(True)
         try:
             y = torch.zeros(D, device="cuda")
             g, u = torch.zeros(H, device="cuda"), torch.zeros(H, device="cuda")
@@ -661,6 +667,7 @@ def test_ffn_barrier_timeout_is_loud_and_recovers(enc):
             e2.close()
     finally:
         e.close()
+        clean.close()
 
 
 @pytest.mark.parametrize("H,D,seed", [(6144, 2048, 1002), (8192, 4096, 38), (384, 640, 39), (128, 128, 40)])
