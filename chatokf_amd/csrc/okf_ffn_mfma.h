@@ -294,4 +294,103 @@ __global__ __launch_bounds__(FM_T) void ffn_mfma_kernel(FfnArgs a) {
 #endif
 }
 
+// ------------------------------------------------------------------------
+// The same arithmetic for one Q2_0 matvec (or gate and up paired), the
+// reference's gemv (LLM/metal/Kernels.metal:1572-1617) on the Bonsai
+// shapes: y = W x, K = 1024 NB, one workgroup per CU taking rows
+// b R .. b R + R - 1 (R = ceil(M / grid)) as up to three 16-column tiles;
+// x staged per workgroup (with SILU: silu(x) * x2, okf_gemv_silu); with
+// PAIR, W0 = gate and W1 = up share x: columns 0 .. R - 1 gate rows, R ..
+// 2 R - 1 up rows, and the outputs y0 = silu(gate x) * (up x), y1 = up x
+// (okf_gemv_gate_up).  The wavefronts split K as in ffn_mfma_kernel.
+struct Q2mArgs {
+    const uint8_t *w0, *w1;
+    uint64_t rb;
+    uint32_t K, M;
+    const float *x, *x2;
+    float *y0, *y1;
+};
+
+__host__ __device__ constexpr size_t q2m_lds_bytes(uint32_t K) { return fm_lds_bytes(K); }
+
+// NT: the workgroup's 16-column tiles, ceil(R / 16) (PAIR: ceil(2 R / 16)),
+// host-checked.
+template <int NB, int NT, bool PAIR, bool SILU>
+__global__ __launch_bounds__(FM_T) void q2m_gemv_kernel(Q2mArgs a) {
+    constexpr uint32_t K = 1024 * NB, SR = (K / 8 + FM_T - 1) / FM_T;
+    extern __shared__ u32x4 lds[];
+    uint8_t *planes = (uint8_t *)lds;
+    int2 *gd = (int2 *)(planes + 3 * K + 32);
+    float *red = (float *)(gd + K / 128);  // [wavefront][48]
+    const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6, col = lane & 15, q = lane >> 4;
+    const uint32_t R = (a.M + gridDim.x - 1) / gridDim.x;
+
+    // x's loads (with SILU x2's too), then every weight load
+    float xv[SR][8], x2v[SR][8];
+#pragma unroll
+    for (uint32_t k = 0; k < SR; k++) {
+        const uint32_t s = min(k * FM_T + tid, K / 8 - 1);
+        load_slot<Q2_0>(a.x + (uint64_t)(s >> 3) * 64, s & 7, xv[k]);
+        if constexpr (SILU) load_slot<Q2_0>(a.x2 + (uint64_t)(s >> 3) * 64, s & 7, x2v[k]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    uint3 cw[NT][NB];
+    const uint32_t lo = fm_off(q);
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        // column n = 16 t + col: with PAIR gate row n, up row n - R (the
+        // clamp outside the select, as in ffn_mfma_kernel)
+        const uint32_t n = 16 * t + col;
+        const bool first = !PAIR || n < R;
+        const uint32_t kk = first ? n : n - R;
+        const uint32_t r = min(blockIdx.x * R + min(kk, R - 1), a.M - 1);
+        const uint8_t *row = (first ? a.w0 : a.w1) + (uint64_t)r * a.rb;
+#pragma unroll
+        for (int i = 0; i < NB; i++) cw[t][i] = ldu<uint3>(row + (uint64_t)(w * NB + i) * 34 + lo);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    if (tid < 8) ((uint32_t *)(planes + 3 * K))[tid] = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < SR; k++)
+        if (k * FM_T < K / 8) {  // (the whole workgroup)
+            if constexpr (SILU)
+#pragma unroll
+                for (int j = 0; j < 8; j++) xv[k][j] = silu_mul1(xv[k][j], x2v[k][j]);
+            fm_stage_slot(xv[k], k * FM_T + tid, k * FM_T + tid < K / 8, planes, K, gd);
+        }
+    __syncthreads();
+
+    const bool arow = col < 3;
+    const uint8_t *ab = arow ? planes + col * K + (w * NB) * 128 + 32 * q : planes + 3 * K;
+    const uint32_t ablk = arow ? 128 : 0;
+    float acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        acc[t] = 0.0f;
+        fm_tile<NB>(cw[t], q == 3, ab, ablk, gd + w * NB, acc[t]);
+    }
+    if (lane < 16)
+#pragma unroll
+        for (int t = 0; t < NT; t++) red[w * 48 + 16 * t + lane] = acc[t];
+    __syncthreads();
+    if (tid < R) {
+        const uint32_t r = blockIdx.x * R + tid;
+        float v0 = 0.0f, v1 = 0.0f;
+#pragma unroll
+        for (int v = 0; v < (int)FM_W; v++) {
+            v0 += red[v * 48 + tid];
+            if constexpr (PAIR) v1 += red[v * 48 + R + tid];
+        }
+        if (r < a.M) {
+            if constexpr (PAIR) {
+                a.y0[r] = silu_mul1(v0, v1);
+                a.y1[r] = v1;
+            } else {
+                a.y0[r] = v0;
+            }
+        }
+    }
+}
+
 }  // namespace okf

@@ -23,6 +23,7 @@
 #include "okf_gemv_wide.h"
 #include "okf_gemv_sb.h"
 #include "okf_ffn.h"
+#include "okf_ffn_mfma.h"
 
 // one matvec y = W x of a launch group (with X2: x = silu(X) * X2)
 struct GemvCall {
@@ -80,6 +81,7 @@ struct okf_ctx {
     int ffn_fused = 1;            // okf_ffn as one launch with a grid barrier where it fits (0: two launches)
     int ffn_wg = 1;               // its workgroups per CU, at most
     int ffn_coop = 0;             // launched with hipLaunchCooperativeKernel (1) or as a plain grid
+    int q2_mfma = 1;              // Q2_0 Bonsai matvecs on the integer matrix cores (q2m_gemv_kernel; 0: off)
     int ffn_mfma = 1;             // the Bonsai shape on the integer matrix cores (ffn_mfma_kernel; 0: off)
     int ffn_nb[4] = {0, 0, 0, 0}; // its kernels' resident workgroups per CU (0: not yet queried)
     int ffn_spin = 0;             // its barrier's poll limit (0: FF_SPIN)
@@ -437,8 +439,30 @@ void launch_gemv_nc(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint3
     else launch_gemv_s<F, NC, 1, SILU>(c, calls, n, rb, K, cunits, lds);
 }
 
+// Q2_0 matvecs of the Bonsai shapes on the integer matrix cores
+// (q2m_gemv_kernel, okf_ffn_mfma.h): K = 2048 (gate / up, alone or paired
+// with the SiLU) or 6144 (down, with or without the SiLU formed in the
+// staging), one workgroup per CU; true when launched.
+inline bool launch_q2m(okf_ctx *c, const GemvCall &g0, const GemvCall *g1, uint64_t rb, uint32_t K) {
+    if (!c->q2_mfma || !c->cus || (K != 2048 && K != 6144) || (g1 && (K != 2048 || g1->M != g0.M))) return false;
+    const uint32_t G = c->cus, R = (g0.M + G - 1) / G, nt = ((g1 ? 2 : 1) * R + 15) / 16;
+    const size_t lds = q2m_lds_bytes(K);
+    if (lds > c->max_lds || nt > 3) return false;
+    const Q2mArgs a{g0.W, g1 ? g1->W : nullptr, rb, K, g0.M, g0.X, g0.X2, g0.Y, g1 ? g1->Y : nullptr};
+    const void *fn = nullptr;
+    if (K == 2048 && g1 && !g0.X2) fn = nt == 3 ? (const void *)q2m_gemv_kernel<2, 3, true, false> : nullptr;
+    else if (K == 2048 && !g0.X2) fn = nt == 2 ? (const void *)q2m_gemv_kernel<2, 2, false, false> : nullptr;
+    else if (K == 6144 && !g1 && nt == 1)
+        fn = g0.X2 ? (const void *)q2m_gemv_kernel<6, 1, false, true> : (const void *)q2m_gemv_kernel<6, 1, false, false>;
+    if (!fn) return false;
+    void *args[] = {(void *)&a};
+    return hipLaunchKernel(fn, dim3(G), dim3(FM_T), args, lds, c->stream) == hipSuccess;
+}
+
 template <int F>
 void launch_gemv(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32_t K, uint32_t N) {
+    if constexpr (F == Q2_0)
+        if (n == 1 && N == 1 && launch_q2m(c, calls[0], nullptr, rb, K)) return;
     if (calls[0].X2) {  // SiLU-gated activations: one column
         launch_gemv_nc<F, 1, true>(c, calls, n, rb, K);
         return;
@@ -458,6 +482,8 @@ void launch_gemv(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint32_t
 // with no SiLU in its staging.
 template <int F>
 void launch_gemv_pair(okf_ctx *c, const GemvCall *calls, uint64_t rb, uint32_t K) {
+    if constexpr (F == Q2_0)
+        if (launch_q2m(c, calls[0], &calls[1], rb, K)) return;
     constexpr uint32_t UW = unit_weights<F>();
     const size_t tab = gemv_tab_rows<F>() * 16;
     const uint32_t units = K / UW;
