@@ -215,8 +215,9 @@ def main():
         # gate and up in one parallel group, as the reference's FFN encodes
         # them (LLM/Qwen/QwenMetalEngine.swift:918-923, MetalEnc.parallel),
         # then down on silu(gate) * up (siluMul + gemv, :924-928): one
-        # okf_ffn call per step (one launch: gate and up, a grid
-        # barrier, down; OKF_FFN_FUSED=0 gives the two-launch form)
+        # okf_ffn call per step (at this shape two launches on the integer
+        # matrix cores, gate and up with the SiLU, then down;
+        # OKF_FFN_FUSED=2 gives the one launch with a grid barrier)
         pbegin, pend, hctx = enc._lib.okf_parallel_begin, enc._lib.okf_parallel_end, enc.h
         ffn_c = enc._lib.okf_ffn
         refs = [(ctypes.byref(g), ctypes.byref(u), ctypes.byref(d)) for g, u, d in zip(gw, uw, dw)]
@@ -247,19 +248,21 @@ def main():
         step_gpu_t, _ = time_calls(ffn_step, args.steps, 5)
         gate_t, _ = time_calls(gate_up, args.steps, 5)
         down_t, _ = time_calls(lambda i: gemv_c(dw[i % nrot], hp, yp), args.steps, 5)
-        if os.environ.get("OKF_FFN_FUSED", "1") != "0":
-            # okf_ffn is one launch (ffn_fused_kernel): the step's bytes are the
-            # three weight matrices, x, g and u written, g read back, y
+        fused, q2m = os.environ.get("OKF_FFN_FUSED", "1"), os.environ.get("OKF_Q2_MFMA", "1") != "0"
+        if fused == "2" or (fused == "1" and not q2m):
+            # okf_ffn is one launch: the step's bytes are the three weight
+            # matrices, x, g and u written, g read back, y (ffn_mfma_kernel,
+            # or with OKF_FFN_MFMA=0 ffn_fused_kernel)
             ffn_alg = step_bytes + 4 * (K1 + 2 * M1 + M1 + K1)
-            # (at this shape okf_ffn launches ffn_mfma_kernel, the integer
-            # matrix-core form; OKF_FFN_MFMA=0 gives ffn_fused_kernel)
             kern = "okf::ffn_fused_kernel<Q2_0>" if os.environ.get("OKF_FFN_MFMA", "1") == "0" else \
                 "okf::ffn_mfma_kernel<2, 6>"
             dom = ("q2_0_ffn_step_okf_ffn", ffn_alg, step_gpu_t, kern)
         elif gate_t >= down_t:
-            dom = ("q2_0_matvec_gate_up_2x6144x2048", gate_np.nbytes + up_np.nbytes, gate_t, "okf::gemv_kernel<Q2_0>")
+            dom = ("q2_0_matvec_gate_up_2x6144x2048", gate_np.nbytes + up_np.nbytes, gate_t,
+                   "okf::q2m_gemv_kernel<2, 3, true, false>" if q2m else "okf::gemv_kernel<Q2_0>")
         else:
-            dom = ("q2_0_matvec_2048x6144", down_np.nbytes, down_t, "okf::gemv_kernel<Q2_0>")
+            dom = ("q2_0_matvec_2048x6144", down_np.nbytes, down_t,
+                   "okf::q2m_gemv_kernel<6, 1, false, false>" if q2m else "okf::gemv_kernel<Q2_0>")
         roofline = {"kernel": f"{dom[3]} ({dom[0]})", "bound": "hbm",
                     "achieved": round(dom[1] / dom[2] / 1e9, 1), "peak": HBM_PEAK / 1e9,
                     "unit": "GB/s", "frac": round(dom[1] / dom[2] / HBM_PEAK, 4),
@@ -446,9 +449,10 @@ def main():
                  "(int8 dot4, exact per group), f32 scales and accumulation",
         "data": "synthetic (reference LCG, BASELINE.json distributions); weights rotated over >= 1 GiB",
         "config": {"workload": "BASELINE configs[1]: Bonsai-1.7B ternary FFN decode step, one token "
-                               "(okf_ffn, one launch): gate+up Q2_0 W 6144x2048 with the siluMul "
-                               "(as the reference's parallel group + in-place siluMul), a grid "
-                               "barrier, then down Q2_0 W 2048x6144 on silu(gate)*up",
+                               "(one okf_ffn call): gate+up Q2_0 W 6144x2048 with the siluMul "
+                               "(as the reference's parallel group + in-place siluMul), then down "
+                               "Q2_0 W 2048x6144 on silu(gate)*up: two launches on the integer "
+                               "matrix cores",
                    "weight_bytes_per_step": step_bytes, "parallelism": "single GPU"},
         "roofline": roofline,
         "cpu_baseline": cpu,

@@ -78,7 +78,8 @@ struct okf_ctx {
     uint8_t *scratch = nullptr;  // this device's copy of the static scratch array
     uint32_t *ffn_bar = nullptr;  // the one-launch FFN's grid barrier (zeroed at creation)
     uint32_t *ffn_status = nullptr;  // pinned host word: 1 once a launch's barrier gave up (GPUGate verdict)
-    int ffn_fused = 1;            // okf_ffn as one launch with a grid barrier where it fits (0: two launches)
+    int ffn_fused = 1;            // okf_ffn as one launch with a grid barrier: 1 where it fits and is the faster
+                                  // form, 2 wherever it fits, 0 never (two launches)
     int ffn_wg = 1;               // its workgroups per CU, at most
     int ffn_coop = 0;             // launched with hipLaunchCooperativeKernel (1) or as a plain grid
     int q2_mfma = 1;              // Q2_0 Bonsai matvecs on the integer matrix cores (q2m_gemv_kernel; 0: off)
@@ -457,6 +458,15 @@ inline bool launch_q2m(okf_ctx *c, const GemvCall &g0, const GemvCall *g1, uint6
     if (!fn) return false;
     void *args[] = {(void *)&a};
     return hipLaunchKernel(fn, dim3(G), dim3(FM_T), args, lds, c->stream) == hipSuccess;
+}
+
+// okf_ffn's two launches both on q2m_gemv_kernel (gate / up K 2048, down K
+// 6144): then they are faster than the one launch with its grid barrier
+// (8.6 against 9.5 us a step), so okf_ffn takes them unless told otherwise.
+inline bool q2m_ffn_fits(const okf_ctx *c, uint32_t ka, uint32_t ma, uint32_t mb) {
+    if (!c->q2_mfma || !c->cus || ka != 2048 || ma != 6144) return false;
+    const uint32_t G = c->cus, ra = (ma + G - 1) / G, rb = (mb + G - 1) / G;
+    return (2 * ra + 15) / 16 == 3 && (rb + 15) / 16 == 1 && q2m_lds_bytes(6144) <= c->max_lds;
 }
 
 template <int F>

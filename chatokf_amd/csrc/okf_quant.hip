@@ -522,7 +522,9 @@ int okf_ffn(okf_ctx *c, const okf_weight *gate, const okf_weight *up, const okf_
         const FfnArgs a{(const uint8_t *)gate->base + gate->off, (const uint8_t *)up->base + up->off,
                         (const uint8_t *)down->base + down->off, rb0, rb1, gate->K, gate->M, down->M,
                         x, g, u, y, nullptr};
-        if (launch_ffn_fused(c, a)) return finish(c);
+        // (at the Bonsai shape the two matrix-core launches are the faster form)
+        if ((c->ffn_fused == 2 || !q2m_ffn_fits(c, gate->K, gate->M, down->M)) && launch_ffn_fused(c, a))
+            return finish(c);
     }
     if ((st = okf_gemv_gate_up(c, gate, up, x, g, u))) return st;
     const GemvCall dn{(const uint8_t *)down->base + down->off, g, y, down->M};

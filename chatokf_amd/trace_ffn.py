@@ -135,6 +135,7 @@ def main():
                 ("ffn_fused_kernel (OKF_FFN_MFMA=0, the VALU digit-plane form)", "0"))
     for title, mf in variants[:1] if args.mfma_only else variants:
         os.environ["OKF_FFN_MFMA"] = mf
+        os.environ["OKF_FFN_FUSED"] = "2"  # the one launch, also where two are okf_ffn's default
         enc = ok.Enc(0)
         print(f"## {title}\n")
         print("\n".join(trace(enc, refs, ptrs, n)) + "\n")

@@ -520,7 +520,24 @@ def enc_ffn2():
 # every replay must synchronise as a fresh launch does.  Each replay runs on
 # a new x (written into the captured buffer), with eager calls between the
 # replays, and must give the eager call's bits for that x.
-def test_ffn_graph_replay(enc):
+@pytest.mark.parametrize("fused", ["1", "2"])
+def test_ffn_graph_replay(fused):
+    # fused "1": okf_ffn's default at this shape (two matrix-core launches);
+    # "2": the one launch with its grid barrier, whose epochs live on the
+    # device, so replays of one captured launch keep agreeing
+    import os
+    os.environ["OKF_FFN_FUSED"] = fused
+    try:
+        enc = ok.Enc(0)
+    finally:
+        del os.environ["OKF_FFN_FUSED"]
+    try:
+        _ffn_graph_replay(enc)
+    finally:
+        enc.close()
+
+
+def _ffn_graph_replay(enc):
     hip = ctypes.CDLL("libamdhip64.so")
     vp = ctypes.c_void_p
     H, D = 6144, 2048
@@ -619,7 +636,7 @@ def test_ffn_barrier_timeout_is_loud_and_recovers(mfma):
     import os
 
     def ctx(stall):
-        env = {"OKF_FFN_MFMA": mfma}
+        env = {"OKF_FFN_MFMA": mfma, "OKF_FFN_FUSED": "2"}
         if stall:
             env.update(OKF_FFN_STALL="1", OKF_FFN_SPIN="2000")
         os.environ.update(env)
@@ -670,14 +687,28 @@ def test_ffn_barrier_timeout_is_loud_and_recovers(mfma):
         clean.close()
 
 
+@pytest.fixture(scope="module")
+def enc_ffn1():
+    # okf_ffn as one launch wherever it fits (at the Bonsai shape the default
+    # takes the two matrix-core launches)
+    import os
+    os.environ["OKF_FFN_FUSED"] = "2"
+    try:
+        e = ok.Enc(0)
+    finally:
+        del os.environ["OKF_FFN_FUSED"]
+    yield e
+    e.close()
+
+
 @pytest.mark.parametrize("H,D,seed", [(6144, 2048, 1002), (8192, 4096, 38), (384, 640, 39), (128, 128, 40)])
-def test_ffn_one_launch_matches_two(enc, enc_ffn2, H, D, seed):
+def test_ffn_one_launch_matches_two(enc_ffn1, enc_ffn2, H, D, seed):
     say("ffn one launch", H, D)
     wg, wu, wd = weights(Q2_0, H, D, seed), weights(Q2_0, H, D, seed + 1), weights(Q2_0, D, H, seed + 2)
     qg, qu, qd = (ok.QuantTensor(dev(w), k, m, Q2_0) for w, k, m in ((wg, D, H), (wu, D, H), (wd, H, D)))
     x = dev(acts(1, D, seed + 10)[0])
     outs = []
-    for e in (enc, enc, enc_ffn2):
+    for e in (enc_ffn1, enc_ffn1, enc_ffn2):
         g, u = (torch.full((H,), float("nan"), device="cuda") for _ in range(2))
         y = torch.full((D,), float("nan"), device="cuda")
         e.ffn(qg, qu, qd, x, g, u, y)
