@@ -147,8 +147,10 @@ int okf_gemv_gate_up(okf_ctx *ctx, const okf_weight *gate, const okf_weight *up,
  * forever; the next okf_sync then returns OKF_E_TIMEOUT once (or, with no
  * okf_sync between, the next okf_ffn returns it and launches nothing)
  * (OKF_FFN_FUSED=0 at okf_ctx_create selects the two launches).  At gate / up
- * 6144 x 2048 the launch computes on the integer matrix cores (OKF_FFN_MFMA=0:
- * the VALU form; the same outputs within 1e-5).  Otherwise two launches when gate and up
+ * 6144 x 2048 (the Bonsai FFN) two launches on the integer matrix cores are
+ * faster and are the default (OKF_FFN_FUSED=2 keeps the one launch, which then
+ * also computes on the matrix cores; OKF_FFN_MFMA=0 its VALU form; the same
+ * outputs within 1e-5).  Otherwise two launches when gate and up
  * share a format: one grid whose workgroups each compute the same rows of
  * gate and up and form silu(g) * u there, then the down projection.
  * down->K must equal gate->M; x, g, u 16-byte aligned. */
