@@ -457,7 +457,9 @@ inline bool launch_q2m(okf_ctx *c, const GemvCall &g0, const GemvCall *g1, uint6
         fn = g0.X2 ? (const void *)q2m_gemv_kernel<6, 1, false, true> : (const void *)q2m_gemv_kernel<6, 1, false, false>;
     if (!fn) return false;
     void *args[] = {(void *)&a};
-    return hipLaunchKernel(fn, dim3(G), dim3(FM_T), args, lds, c->stream) == hipSuccess;
+    if (hipLaunchKernel(fn, dim3(G), dim3(FM_T), args, lds, c->stream) == hipSuccess) return true;
+    (void)hipGetLastError();  // (the caller's fallback launch is the call's result)
+    return false;
 }
 
 // okf_ffn's two launches both on q2m_gemv_kernel (gate / up K 2048, down K
