@@ -311,13 +311,17 @@ struct Q2mArgs {
     float *y0, *y1;
 };
 
-__host__ __device__ constexpr size_t q2m_lds_bytes(uint32_t K) { return fm_lds_bytes(K); }
+// LDS of q2m_gemv_kernel with NW wavefronts: the planes, zeros, block data
+// as fm_lds_bytes, the partial sums NW x 48 floats
+__host__ __device__ constexpr size_t q2m_lds_bytes(uint32_t K, uint32_t NW) {
+    return 3 * (size_t)K + 32 + (size_t)(K / 128) * 8 + (size_t)NW * 48 * 4;
+}
 
-// NT: the workgroup's 16-column tiles, ceil(R / 16) (PAIR: ceil(2 R / 16)),
-// host-checked.
-template <int NB, int NT, bool PAIR, bool SILU>
-__global__ __launch_bounds__(FM_T) void q2m_gemv_kernel(Q2mArgs a) {
-    constexpr uint32_t K = 1024 * NB, SR = (K / 8 + FM_T - 1) / FM_T;
+// NW wavefronts, each NB K blocks (K = 128 NB NW); NT: the workgroup's
+// 16-column tiles, ceil(R / 16) (PAIR: ceil(2 R / 16)), host-checked.
+template <int NB, int NT, bool PAIR, bool SILU, int NW>
+__global__ __launch_bounds__(NW * 64) void q2m_gemv_kernel(Q2mArgs a) {
+    constexpr uint32_t T = NW * 64, K = 128 * NB * NW, SR = (K / 8 + T - 1) / T;
     extern __shared__ u32x4 lds[];
     uint8_t *planes = (uint8_t *)lds;
     int2 *gd = (int2 *)(planes + 3 * K + 32);
@@ -329,7 +333,7 @@ __global__ __launch_bounds__(FM_T) void q2m_gemv_kernel(Q2mArgs a) {
     float xv[SR][8], x2v[SR][8];
 #pragma unroll
     for (uint32_t k = 0; k < SR; k++) {
-        const uint32_t s = min(k * FM_T + tid, K / 8 - 1);
+        const uint32_t s = min(k * T + tid, K / 8 - 1);
         load_slot<Q2_0>(a.x + (uint64_t)(s >> 3) * 64, s & 7, xv[k]);
         if constexpr (SILU) load_slot<Q2_0>(a.x2 + (uint64_t)(s >> 3) * 64, s & 7, x2v[k]);
     }
@@ -353,11 +357,11 @@ __global__ __launch_bounds__(FM_T) void q2m_gemv_kernel(Q2mArgs a) {
     if (tid < 8) ((uint32_t *)(planes + 3 * K))[tid] = 0;
 #pragma unroll
     for (uint32_t k = 0; k < SR; k++)
-        if (k * FM_T < K / 8) {  // (the whole workgroup)
+        if (k * T < K / 8) {  // (the whole workgroup)
             if constexpr (SILU)
 #pragma unroll
                 for (int j = 0; j < 8; j++) xv[k][j] = silu_mul1(xv[k][j], x2v[k][j]);
-            fm_stage_slot(xv[k], k * FM_T + tid, k * FM_T + tid < K / 8, planes, K, gd);
+            fm_stage_slot(xv[k], k * T + tid, k * T + tid < K / 8, planes, K, gd);
         }
     __syncthreads();
 
@@ -378,7 +382,7 @@ __global__ __launch_bounds__(FM_T) void q2m_gemv_kernel(Q2mArgs a) {
         const uint32_t r = blockIdx.x * R + tid;
         float v0 = 0.0f, v1 = 0.0f;
 #pragma unroll
-        for (int v = 0; v < (int)FM_W; v++) {
+        for (int v = 0; v < NW; v++) {
             v0 += red[v * 48 + tid];
             if constexpr (PAIR) v1 += red[v * 48 + R + tid];
         }
