@@ -259,10 +259,11 @@ def main():
             dom = ("q2_0_ffn_step_okf_ffn", ffn_alg, step_gpu_t, kern)
         elif gate_t >= down_t:
             dom = ("q2_0_matvec_gate_up_2x6144x2048", gate_np.nbytes + up_np.nbytes, gate_t,
-                   "okf::q2m_gemv_kernel<2, 3, true, false>" if q2m else "okf::gemv_kernel<Q2_0>")
+                   "okf::q2m_gemv_kernel<2, 3, true, false, 8, false>" if q2m else "okf::gemv_kernel<Q2_0>")
         else:
             dom = ("q2_0_matvec_2048x6144", down_np.nbytes, down_t,
-                   "okf::q2m_gemv_kernel<6, 1, false, false>" if q2m else "okf::gemv_kernel<Q2_0>")
+                   ("okf::q2m_gemv_kernel<4, 1, false, false, 12, true>" if os.environ.get("OKF_Q2_KS", "1") != "0"
+                    else "okf::q2m_gemv_kernel<6, 1, false, false, 8, false>") if q2m else "okf::gemv_kernel<Q2_0>")
         roofline = {"kernel": f"{dom[3]} ({dom[0]})", "bound": "hbm",
                     "achieved": round(dom[1] / dom[2] / 1e9, 1), "peak": HBM_PEAK / 1e9,
                     "unit": "GB/s", "frac": round(dom[1] / dom[2] / HBM_PEAK, 4),

@@ -120,8 +120,10 @@ __device__ __forceinline__ uint32_t fm_off(uint32_t q) { return 8 * q - (q == 3 
 // sum over the blocks of d (sum (c - 1) x).  raw[i]: this lane's 12 bytes of
 // block i, q3: lane group 3 (fm_off); abase: this lane's A bytes of block 0
 // (its plane, or the zero bytes), ablk: bytes a block in LDS (128 for a
-// plane, 0 for the zeros).
-template <int NB>
+// plane, 0 for the zeros).  KS (the K-split tile of q2m_gemv_kernel):
+// lanes 16-31 hold sums too (A rows 4-6, the planes of the other K half),
+// and take d from lane - 16, which loaded the block's first bytes.
+template <int NB, bool KS = false>
 __device__ __forceinline__ void fm_tile(const uint3 (&raw)[NB], bool q3, const uint8_t *abase, uint32_t ablk,
                                         const int2 *gd, float &acc) {
 #pragma unroll
@@ -139,7 +141,9 @@ __device__ __forceinline__ void fm_tile(const uint3 (&raw)[NB], bool q3, const u
         }
         const int2 g = gd[i];
         const int T = (c[2] << 16) + (c[1] << 8) + c[0] - g.x;
-        acc = fmaf((float)T, h2f((uint16_t)raw[i].x) * __builtin_bit_cast(float, g.y), acc);
+        uint32_t dw = raw[i].x;
+        if constexpr (KS) dw = (uint32_t)__builtin_amdgcn_ds_bpermute((int)((threadIdx.x & 15) << 2), (int)dw);
+        acc = fmaf((float)T, h2f((uint16_t)dw) * __builtin_bit_cast(float, g.y), acc);
     }
 }
 
@@ -319,8 +323,13 @@ __host__ __device__ constexpr size_t q2m_lds_bytes(uint32_t K, uint32_t NW) {
 
 // NW wavefronts, each NB K blocks (K = 128 NB NW); NT: the workgroup's
 // 16-column tiles, ceil(R / 16) (PAIR: ceil(2 R / 16)), host-checked.
-template <int NB, int NT, bool PAIR, bool SILU, int NW>
+// KS (one tile, R <= 8, not PAIR): columns 8 + r take row r over the second
+// half of the wavefront's blocks, whose planes are A rows 4-6, so no column
+// repeats a row and a wavefront runs NB / 2 block steps.
+template <int NB, int NT, bool PAIR, bool SILU, int NW, bool KS = false>
 __global__ __launch_bounds__(NW * 64) void q2m_gemv_kernel(Q2mArgs a) {
+    static_assert(!KS || (NT == 1 && !PAIR && NB % 2 == 0), "K split: one tile of one matrix");
+    constexpr int NL = KS ? NB / 2 : NB;  // blocks a lane loads
     constexpr uint32_t T = NW * 64, K = 128 * NB * NW, SR = (K / 8 + T - 1) / T;
     extern __shared__ u32x4 lds[];
     uint8_t *planes = (uint8_t *)lds;
@@ -338,19 +347,21 @@ __global__ __launch_bounds__(NW * 64) void q2m_gemv_kernel(Q2mArgs a) {
         if constexpr (SILU) load_slot<Q2_0>(a.x2 + (uint64_t)(s >> 3) * 64, s & 7, x2v[k]);
     }
     __builtin_amdgcn_sched_barrier(0);
-    uint3 cw[NT][NB];
+    uint3 cw[NT][NL];
     const uint32_t lo = fm_off(q);
 #pragma unroll
     for (int t = 0; t < NT; t++) {
         // column n = 16 t + col: with PAIR gate row n, up row n - R (the
-        // clamp outside the select, as in ffn_mfma_kernel)
+        // clamp outside the select, as in ffn_mfma_kernel); with KS row n % 8
+        // of K half n / 8
         const uint32_t n = 16 * t + col;
         const bool first = !PAIR || n < R;
-        const uint32_t kk = first ? n : n - R;
+        const uint32_t kk = KS ? (n & 7) : first ? n : n - R;
         const uint32_t r = min(blockIdx.x * R + min(kk, R - 1), a.M - 1);
         const uint8_t *row = (first ? a.w0 : a.w1) + (uint64_t)r * a.rb;
+        const uint32_t b0 = w * NB + (KS ? (n >> 3) * NL : 0);
 #pragma unroll
-        for (int i = 0; i < NB; i++) cw[t][i] = ldu<uint3>(row + (uint64_t)(w * NB + i) * 34 + lo);
+        for (int i = 0; i < NL; i++) cw[t][i] = ldu<uint3>(row + (uint64_t)(b0 + i) * 34 + lo);
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -365,18 +376,23 @@ __global__ __launch_bounds__(NW * 64) void q2m_gemv_kernel(Q2mArgs a) {
         }
     __syncthreads();
 
-    const bool arow = col < 3;
-    const uint8_t *ab = arow ? planes + col * K + (w * NB) * 128 + 32 * q : planes + 3 * K;
+    // A row ar: plane ar of the first K half (rows 0-2), with KS plane ar - 4
+    // of the second (rows 4-6); the other rows read the zeros
+    const uint32_t ar = col, ah = KS ? ar >> 2 : 0, ap = ar - 4 * ah;
+    const bool arow = ap < 3 && ah < 2;
+    const uint8_t *ab = arow ? planes + ap * K + (w * NB + ah * NL) * 128 + 32 * q : planes + 3 * K;
     const uint32_t ablk = arow ? 128 : 0;
     float acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) {
         acc[t] = 0.0f;
-        fm_tile<NB>(cw[t], q == 3, ab, ablk, gd + w * NB, acc[t]);
+        // (KS: lanes 16-31 sum the second half, whose block data follow)
+        fm_tile<NL, KS>(cw[t], q == 3, ab, ablk, gd + w * NB + (KS && q == 1 ? NL : 0), acc[t]);
     }
-    if (lane < 16)
+    // KS: row r's halves in lanes r and 24 + r, kept at red[r], red[8 + r]
+    if (KS ? (lane < 8 || (lane >= 24 && lane < 32)) : lane < 16)
 #pragma unroll
-        for (int t = 0; t < NT; t++) red[w * 48 + 16 * t + lane] = acc[t];
+        for (int t = 0; t < NT; t++) red[w * 48 + 16 * t + (KS ? lane & 15 : lane)] = acc[t];
     __syncthreads();
     if (tid < R) {
         const uint32_t r = blockIdx.x * R + tid;
@@ -384,6 +400,7 @@ __global__ __launch_bounds__(NW * 64) void q2m_gemv_kernel(Q2mArgs a) {
 #pragma unroll
         for (int v = 0; v < NW; v++) {
             v0 += red[v * 48 + tid];
+            if constexpr (KS) v0 += red[v * 48 + 8 + tid];
             if constexpr (PAIR) v1 += red[v * 48 + R + tid];
         }
         if (r < a.M) {

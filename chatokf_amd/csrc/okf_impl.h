@@ -83,6 +83,7 @@ struct okf_ctx {
     int ffn_wg = 1;               // its workgroups per CU, at most
     int ffn_coop = 0;             // launched with hipLaunchCooperativeKernel (1) or as a plain grid
     int q2_mfma = 1;              // Q2_0 Bonsai matvecs on the integer matrix cores (q2m_gemv_kernel; 0: off)
+    int q2_ks = 1;                // ... down (R <= 8 rows a workgroup) as the K-split tile (0: rows repeated)
     int ffn_mfma = 1;             // the Bonsai shape on the integer matrix cores (ffn_mfma_kernel; 0: off)
     int ffn_nb[4] = {0, 0, 0, 0}; // its kernels' resident workgroups per CU (0: not yet queried)
     int ffn_spin = 0;             // its barrier's poll limit (0: FF_SPIN)
@@ -447,21 +448,27 @@ void launch_gemv_nc(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint3
 inline bool launch_q2m(okf_ctx *c, const GemvCall &g0, const GemvCall *g1, uint64_t rb, uint32_t K) {
     if (!c->q2_mfma || !c->cus || (K != 2048 && K != 6144) || (g1 && (K != 2048 || g1->M != g0.M))) return false;
     const uint32_t G = c->cus, R = (g0.M + G - 1) / G, nt = ((g1 ? 2 : 1) * R + 15) / 16;
-    // (eight wavefronts: with sixteen, each a half of the K blocks, gate / up
-    // took 4.89 against 4.09 us and down 4.33 against 4.25)
-    constexpr uint32_t nw = 8;
-    const size_t lds = q2m_lds_bytes(K, nw);
+    // Eight wavefronts (with sixteen, each a half of the K blocks, gate / up
+    // took 4.89 against 4.09 us and down 4.33 against 4.25; with four, gate /
+    // up 4.40 against 4.14); twelve for the K-split down, so that every
+    // thread stages one slot of its 6144 values (3.67 against 3.76 us).
+    constexpr uint32_t nw = 8, nwk = 12;
+    const bool ks = K == 6144 && !g1 && nt == 1 && R <= 8 && c->q2_ks;
+    const size_t lds = q2m_lds_bytes(K, ks ? nwk : nw);
     if (lds > c->max_lds || nt > 3) return false;
     const Q2mArgs a{g0.W, g1 ? g1->W : nullptr, rb, K, g0.M, g0.X, g0.X2, g0.Y, g1 ? g1->Y : nullptr};
     const void *fn = nullptr;
     if (K == 2048 && g1 && !g0.X2) fn = nt == 3 ? (const void *)q2m_gemv_kernel<2, 3, true, false, nw> : nullptr;
     else if (K == 2048 && !g0.X2) fn = nt == 2 ? (const void *)q2m_gemv_kernel<2, 2, false, false, nw> : nullptr;
+    else if (ks)
+        fn = g0.X2 ? (const void *)q2m_gemv_kernel<4, 1, false, true, nwk, true>
+                   : (const void *)q2m_gemv_kernel<4, 1, false, false, nwk, true>;
     else if (K == 6144 && !g1 && nt == 1)
         fn = g0.X2 ? (const void *)q2m_gemv_kernel<6, 1, false, true, nw>
                    : (const void *)q2m_gemv_kernel<6, 1, false, false, nw>;
     if (!fn) return false;
     void *args[] = {(void *)&a};
-    if (hipLaunchKernel(fn, dim3(G), dim3(nw * 64), args, lds, c->stream) == hipSuccess) return true;
+    if (hipLaunchKernel(fn, dim3(G), dim3((ks ? nwk : nw) * 64), args, lds, c->stream) == hipSuccess) return true;
     (void)hipGetLastError();  // (the caller's fallback launch is the call's result)
     return false;
 }
@@ -472,7 +479,7 @@ inline bool launch_q2m(okf_ctx *c, const GemvCall &g0, const GemvCall *g1, uint6
 inline bool q2m_ffn_fits(const okf_ctx *c, uint32_t ka, uint32_t ma, uint32_t mb) {
     if (!c->q2_mfma || !c->cus || ka != 2048 || ma != 6144) return false;
     const uint32_t G = c->cus, ra = (ma + G - 1) / G, rb = (mb + G - 1) / G;
-    return (2 * ra + 15) / 16 == 3 && (rb + 15) / 16 == 1 && q2m_lds_bytes(6144, 8) <= c->max_lds;
+    return (2 * ra + 15) / 16 == 3 && (rb + 15) / 16 == 1 && q2m_lds_bytes(6144, 12) <= c->max_lds;
 }
 
 template <int F>

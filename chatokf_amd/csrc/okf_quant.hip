@@ -398,6 +398,7 @@ int okf_ctx_create(int device, okf_ctx **out) {
         if (const char *e = getenv("OKF_FFN_FUSED")) c->ffn_fused = atoi(e);
         if (const char *e = getenv("OKF_FFN_MFMA")) c->ffn_mfma = atoi(e);
         if (const char *e = getenv("OKF_Q2_MFMA")) c->q2_mfma = atoi(e);
+        if (const char *e = getenv("OKF_Q2_KS")) c->q2_ks = atoi(e);
         if (const char *e = getenv("OKF_FFN_WG")) c->ffn_wg = atoi(e);
         if (const char *e = getenv("OKF_FFN_COOP")) c->ffn_coop = atoi(e);
         if (const char *e = getenv("OKF_FFN_T")) c->ffn_t = atoi(e);

@@ -465,6 +465,47 @@ def test_gemv_silu_matches_silu_mul_then_matvec(enc, t, M, K, seed):
     assert rel(got, host(y2).astype(np.float64)) <= 1e-5
 
 
+# The Bonsai-shape Q2_0 matvecs on the integer matrix cores (K 2048 and
+# 6144) at row counts that leave the last workgroups partial or empty, and
+# R = ceil(M / CUs) rows a workgroup from 1 to 16: with OKF_Q2_KS=1 (the
+# default) a K-6144 workgroup of at most 8 rows runs its tile as two K
+# halves side by side, with 0 it repeats rows in the tile's spare columns.
+# Both against the oracle, plain and with the SiLU-gated activations.
+@pytest.fixture(scope="module", params=["1", "0"], ids=["ks", "noks"])
+def enc_q2ks(request):
+    import os
+    os.environ["OKF_Q2_KS"] = request.param
+    try:
+        e = ok.Enc(0)
+    finally:
+        del os.environ["OKF_Q2_KS"]
+    yield e
+    e.close()
+
+
+@pytest.mark.parametrize("M,K", [(2048, 6144), (2000, 6144), (1100, 6144), (37, 6144), (3000, 6144),
+                                 (4000, 2048), (100, 2048), (6143, 2048)])
+@pytest.mark.parametrize("silu", [False, True], ids=["plain", "silu"])
+def test_q2_0_matrix_core_rows(enc_q2ks, M, K, silu):
+    say("q2_0 matrix-core rows", M, K, "silu" if silu else "plain")
+    w = weights(Q2_0, M, K, 61)
+    g, u = acts(1, K, 62)[0] * 2, acts(1, K, 63)[0]
+    x = oracle.silu_mul(g, u) if silu else g
+    ref = oracle.matvec(Q2_0, w, K, M, x).astype(np.float64)
+    y = torch.full((M,), float("nan"), device="cuda")
+    qt = ok.QuantTensor(dev(w), K, M, Q2_0)
+    if silu:
+        enc_q2ks.gemv_silu(qt, dev(g), dev(u), y)
+    else:
+        enc_q2ks.gemv(qt, dev(g), y)
+    got = host(y)
+    r = rel(got, ref)
+    say("  rel", r)
+    assert r <= TOL_MV
+    if M <= 64:
+        assert (np.abs(got - ref) <= 2e-6 * l1_rows(Q2_0, w, K, M, x) + 1e-30).all()
+
+
 # ------------------------------------------------------------ FFN block
 # okf_ffn: gate and up on x (one grid), then down on silu(gate) * up
 # (QwenMetalEngine.swift:918-929); against the oracle's three matvecs.
