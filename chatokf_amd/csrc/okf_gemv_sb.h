@@ -1,4 +1,4 @@
-// okf_gemv_sb.h -- matvec with one superblock per lane (Q4_K).
+// okf_gemv_sb.h -- matvec with one superblock per lane (Q4_K, IQ2_XXS).
 //
 // Work items are (row, superblock) pairs.  A workgroup owns RW consecutive
 // rows, i.e. RW * nsb items that lie back to back in memory (GGUF rows are
@@ -9,6 +9,7 @@
 // of a 9 KB span: each instruction moves 16 bytes per lane, and the header,
 // decoded once per lane, serves all 256 weights.  Measured on MI355X, this
 // pattern reads a 50 MB Q4_K matrix as fast as a plain contiguous stream.
+// An IQ2_XXS superblock (66 bytes) is d plus four 16-byte loads from byte 2.
 //
 // Arithmetic is the exact per-group scheme of okf_gemv.h: each 32-weight
 // group of x is staged once per workgroup as three signed byte planes of a
@@ -33,7 +34,21 @@ constexpr uint32_t SB_CHUNKS = 57;
 
 template <int F>
 __host__ __device__ constexpr bool sb_fmt() {
-    return F == Q4_K;
+    return F == Q4_K || F == IQ2_XXS;
+}
+// 16-byte loads a superblock takes, its bytes, and the LDS table rows its
+// compute reads (IQ2_XXS: the grid and sign rows of Compute<IQ2_XXS>)
+template <int F>
+__host__ __device__ constexpr int sb_loads() {
+    return F == Q4_K ? 9 : 5;
+}
+template <int F>
+__host__ __device__ constexpr uint32_t sb_bytes() {
+    return F == Q4_K ? 144 : 66;
+}
+template <int F>
+__host__ __device__ constexpr uint32_t sb_tab_rows() {
+    return F == IQ2_XXS ? 384 : 0;
 }
 
 // Stages slots [0, K/8) of the NC columns into the superblock records, in
@@ -173,13 +188,83 @@ __device__ __forceinline__ void sb_q4k(const u32x4 (&c)[R][9], const u32x4 *rec,
     }
 }
 
+// R IQ2_XXS superblocks (IQ2XXS.dot, LLM/Quantize/IQ2XXS.swift:34-54, as
+// the integer form of Compute<IQ2_XXS>): c[r][0].x low half d, c[r][1..4]
+// the 16 qs dwords (loaded from byte 2); sub-block j = qs dwords 2j (four
+// grid indices, 8 weights each) and 2j + 1 (four 7-bit sign indices, the
+// 4-bit scale on top) = staged group j.  Per 8 weights: two 8-byte table
+// reads, one add and one v_perm per 4 weights make the signed grid bytes
+// (tab layout as Compute<IQ2_XXS>), dotted with the three digit planes;
+// per sub-block db (f sum(g s X)), db = d (0.5 + scale) / 4.
+template <int NC, int R>
+__device__ __forceinline__ void sb_iq2(const u32x4 (&c)[R][5], const u32x4 *rec, uint32_t cs, const u32x4 *tab,
+                                       float (&out)[R][NC]) {
+    float acc[R][NC];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int n = 0; n < NC; n++) acc[r][n] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        int s[3][R][NC];
+#pragma unroll
+        for (int p = 0; p < 3; p++)
+#pragma unroll
+            for (int r = 0; r < R; r++)
+#pragma unroll
+                for (int n = 0; n < NC; n++) s[p][r][n] = 0;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {  // grid entries 2h, 2h + 1 = plane chunk h of the group
+            uint32_t w[R][4];
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const uint32_t a0 = c[r][1 + (j >> 1)][2 * (j & 1)], a1 = c[r][1 + (j >> 1)][2 * (j & 1) + 1];
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    const int l = 2 * h + e;
+                    const uint2 gv = *(const uint2 *)&tab[(a0 >> (8 * l)) & 0xFF];
+                    const uint2 sg = *(const uint2 *)&tab[256 + ((a1 >> (7 * l)) & 127)];
+                    w[r][2 * e] = perm(IQ2_NEG, IQ2_POS, gv.x + sg.x - 0x03020100u);
+                    w[r][2 * e + 1] = perm(IQ2_NEG, IQ2_POS, gv.y + sg.y - 0x03020100u);
+                }
+            }
+#pragma unroll
+            for (int n = 0; n < NC; n++)
+#pragma unroll
+                for (int p = 0; p < 3; p++) {
+                    const u32x4 xv = rec[n * cs + j * 6 + p * 2 + h];
+#pragma unroll
+                    for (int r = 0; r < R; r++)
+#pragma unroll
+                        for (int k = 0; k < 4; k++) s[p][r][n] = sdot4(w[r][k], xv[k], s[p][r][n]);
+                }
+        }
+#pragma unroll
+        for (int n = 0; n < NC; n++) {
+            const floatx4 gd = *(const floatx4 *)&rec[n * cs + 48 + j];
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const uint32_t a1 = c[r][1 + (j >> 1)][2 * (j & 1) + 1];
+                const float db = h2f(c[r][0][0] & 0xFFFF) * (0.5f + (float)(a1 >> 28)) * 0.25f;
+                acc[r][n] += db * (comb(s, r, n) * gd[1]);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int n = 0; n < NC; n++) out[r][n] = acc[r][n];
+}
+
 // Grid: one workgroup per RW rows of a matrix of the group (GemvGroup as
 // gemv_kernel).  Items are (row pair-set, superblock): item i covers
 // superblock i % nsb of rows i / nsb + k RW / R, k < R (RW a multiple of R).
-// Dynamic LDS: NC columns of nsb records (column stride cs = nsb * SB_CHUNKS
-// chunks), then the partials [row][superblock][NC].
+// Dynamic LDS: the format's table rows (copied from tab_g), NC columns of
+// nsb records (column stride cs = nsb * SB_CHUNKS chunks), then the
+// partials [row][superblock][NC].
 template <int F, int NC, int R, int T, int SR, bool SILU>
-__global__ __launch_bounds__(T) void gemv_sb_kernel(GemvGroup g, uint64_t row_bytes, uint32_t K, uint32_t RW) {
+__global__ __launch_bounds__(T) void gemv_sb_kernel(GemvGroup g, uint64_t row_bytes, uint32_t K, uint32_t RW,
+                                                    const u32x4 *__restrict__ tab_g) {
     static_assert(sb_fmt<F>(), "no superblock-per-lane matvec for this format");
     uint32_t mi = 0;
 #pragma unroll
@@ -192,22 +277,32 @@ __global__ __launch_bounds__(T) void gemv_sb_kernel(GemvGroup g, uint64_t row_by
     float *__restrict__ Y = g.Y[mi];
     extern __shared__ u32x4 lds[];
     const uint32_t tid = threadIdx.x, nsb = K / 256, cs = nsb * SB_CHUNKS;
-    u32x4 *xs = lds;
-    float *part = (float *)(lds + NC * cs);
+    constexpr uint32_t TABR = sb_tab_rows<F>(), NL = sb_loads<F>();
+    u32x4 *tab = lds;
+    if constexpr (TABR > 0)
+        for (uint32_t e = tid; e < TABR; e += T) tab[e] = tab_g[e];
+    u32x4 *xs = lds + TABR;
+    float *part = (float *)(xs + NC * cs);
     const uint32_t r0 = blk * RW, rows = min(RW, M - r0), rs = RW / R;
     const uint32_t items = rs * nsb;
     const uint8_t *base = g.W[mi] + (uint64_t)r0 * row_bytes;
 
-    u32x4 c[R][9];
+    u32x4 c[R][NL];
     auto load = [&](uint32_t it) {
         const uint32_t i = min(it, items - 1), row = i / nsb, sb = i - row * nsb;
 #pragma unroll
         for (int r = 0; r < R; r++) {
             // rows past the matrix re-read the last row (their results are dropped)
             const uint32_t rr = min(row + r * rs, rows - 1);
-            const u32x4 *p = (const u32x4 *)(base + (uint64_t)rr * row_bytes + (uint64_t)sb * 144);
+            const uint8_t *p = base + (uint64_t)rr * row_bytes + (uint64_t)sb * sb_bytes<F>();
+            if constexpr (F == IQ2_XXS) {
+                c[r][0] = u32x4{ldu<uint16_t>(p), 0u, 0u, 0u};
 #pragma unroll
-            for (int k = 0; k < 9; k++) c[r][k] = p[k];
+                for (int k = 0; k < 4; k++) c[r][1 + k] = ldu<u32x4>(p + 2 + 16 * k);
+            } else {
+#pragma unroll
+                for (int k = 0; k < 9; k++) c[r][k] = ((const u32x4 *)p)[k];
+            }
         }
     };
     // the first item's loads go right behind the staging's activation loads
@@ -218,7 +313,8 @@ __global__ __launch_bounds__(T) void gemv_sb_kernel(GemvGroup g, uint64_t row_by
     for (uint32_t it = tid; it < items; it += T) {
         float o[R][NC];
         const uint32_t row = it / nsb, sb = it - row * nsb;
-        sb_q4k<NC, R>(c, xs + sb * SB_CHUNKS, cs, o);
+        if constexpr (F == IQ2_XXS) sb_iq2<NC, R>(c, xs + sb * SB_CHUNKS, cs, tab, o);
+        else sb_q4k<NC, R>(c, xs + sb * SB_CHUNKS, cs, o);
         if (it + T < items) load(it + T);
 #pragma unroll
         for (int r = 0; r < R; r++)

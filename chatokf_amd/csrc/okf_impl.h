@@ -49,6 +49,7 @@ struct okf_ctx {
     int gemv_sb = -1;    // superblock-per-lane matvec: -1 auto, 0 never, 1 where it fits
     int gemv_sb_rw = 0;  // its rows per workgroup (0 = auto)
     int gemv_sb_t = 0;   // its threads per workgroup (0 = auto)
+    int gemv_sb_r = 2;   // its rows per lane for IQ2_XXS (2: each x record read serves two rows; or 1)
     int gemm_ks = 0;     // wide-tile GEMM: K ranges per remainder tile (0 = auto)
     int q4k_mm = 0xFFF;  // 2..4 columns on the matrix cores, bits mm_bit(F) (0: the dot4 kernels)
     int gemm_split = 1;  // tile GEMM of the other formats: K split when the grid is small (0 never, > 1 ways)
@@ -344,16 +345,16 @@ bool launch_gemv_wide(okf_ctx *c, const GemvCall &call, uint64_t rb, uint32_t K)
     return true;
 }
 
-template <int F, int NC, int T, bool SILU>
+template <int F, int NC, int T, bool SILU, int R = 1>
 void launch_sb_t(okf_ctx *c, const GemvGroup &g, uint32_t total, uint64_t rb, uint32_t K, uint32_t RW, size_t lds,
                  uint32_t sr) {
     auto go = [&](auto src) {
         constexpr int SR = decltype(src)::value;
-        const void *fn = (const void *)gemv_sb_kernel<F, NC, 1, T, SR, SILU>;
+        const void *fn = (const void *)gemv_sb_kernel<F, NC, R, T, SR, SILU>;
         static std::atomic<uint64_t> attr{0};  // devices that have the attribute set
         set_lds_attr(c, fn, attr);
-        hipLaunchKernelGGL((gemv_sb_kernel<F, NC, 1, T, SR, SILU>), dim3(total), dim3(T), lds, c->stream, g, rb, K,
-                           RW);
+        hipLaunchKernelGGL((gemv_sb_kernel<F, NC, R, T, SR, SILU>), dim3(total), dim3(T), lds, c->stream, g, rb, K,
+                           RW, (const u32x4 *)c->tab8);
     };
     // (one register buffer: a two-deep ring measured slower at every
     // workgroup size tried, 15.5 against 13.6 us at 17408 x 5120)
@@ -369,7 +370,8 @@ void launch_sb_t(okf_ctx *c, const GemvGroup &g, uint32_t total, uint64_t rb, ui
 
 // Superblock-per-lane matvec (gemv_sb_kernel): true when launched.  Short
 // rows (<= 32 superblocks): T = 256 lanes and RW = T / nsb rows, one
-// superblock per lane.  Long rows: T = 512 and RW = M / CUs (one workgroup
+// superblock per lane (IQ2_XXS: two rows per lane, RW = 2 T / nsb; 17408 x
+// 5120 in 15.5 us against 16.1 for one row per lane and for gemv_kernel).  Long rows: T = 512 and RW = M / CUs (one workgroup
 // per CU, each lane a few superblocks), so that the per-workgroup staging of
 // x is shared by more rows.  Measured on MI355X (A/B in one process):
 // Q4_K 17408 x 5120 from 15.7 us (gemv_kernel) to 13.6 us; 5120 x 17408
@@ -382,6 +384,7 @@ bool launch_gemv_sb(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint3
         const uint32_t nsb = K / 256;
         if (c->gemv_sb == 0) return false;
         const bool lng = nsb > 32;
+        if (F == IQ2_XXS && lng) return false;  // (long rows: gemv_kernel, not measured here)
         uint32_t T = c->gemv_sb_t ? (uint32_t)c->gemv_sb_t : lng ? 512 : 256;
         if (T != 256 && T != 512) T = 256;
         const uint32_t sr = (K / 8 + T - 1) / T;  // staging rounds
@@ -390,8 +393,9 @@ bool launch_gemv_sb(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint3
         for (int i = 0; i < n; i++) M += calls[i].M;
         const uint32_t RW = c->gemv_sb_rw ? (uint32_t)c->gemv_sb_rw
                             : lng       ? std::min(32u, std::max(4u, (M + c->cus - 1) / c->cus))
-                                        : std::max(1u, T / nsb);
-        const size_t lds = ((size_t)NC * nsb * SB_CHUNKS * 16) + (size_t)RW * nsb * NC * sizeof(float);
+                                        : std::max(1u, T / nsb) * (F == IQ2_XXS && c->gemv_sb_r == 2 ? 2 : 1);
+        const size_t lds = (size_t)sb_tab_rows<F>() * 16 + ((size_t)NC * nsb * SB_CHUNKS * 16) +
+                           (size_t)RW * nsb * NC * sizeof(float);
         if (lds > c->max_lds) return false;
         GemvGroup g{};
         uint32_t total = 0;
@@ -405,7 +409,9 @@ bool launch_gemv_sb(okf_ctx *c, const GemvCall *calls, int n, uint64_t rb, uint3
             g.end[i] = total;
         }
         g.n = (uint32_t)n;
-        if (T == 256) launch_sb_t<F, NC, 256, SILU>(c, g, total, rb, K, RW, lds, sr);
+        if (F == IQ2_XXS && c->gemv_sb_r == 2 && T == 256 && RW % 2 == 0)
+            launch_sb_t<F, NC, 256, SILU, 2>(c, g, total, rb, K, RW, lds, sr);
+        else if (T == 256) launch_sb_t<F, NC, 256, SILU>(c, g, total, rb, K, RW, lds, sr);
         else launch_sb_t<F, NC, 512, SILU>(c, g, total, rb, K, RW, lds, sr);
         return true;
     }

@@ -389,6 +389,7 @@ int okf_ctx_create(int device, okf_ctx **out) {
         if (const char *e = getenv("OKF_GEMV_SB")) c->gemv_sb = atoi(e);
         if (const char *e = getenv("OKF_GEMV_SB_RW")) c->gemv_sb_rw = atoi(e);
         if (const char *e = getenv("OKF_GEMV_SB_T")) c->gemv_sb_t = atoi(e);
+        if (const char *e = getenv("OKF_GEMV_SB_R")) c->gemv_sb_r = atoi(e);
         if (const char *e = getenv("OKF_GEMM_KS")) c->gemm_ks = atoi(e);
         if (const char *e = getenv("OKF_GEMM_NG")) c->gemm_ng = atoi(e);
         if (const char *e = getenv("OKF_GEMM_THIN")) c->gemm_thin = atoi(e);
