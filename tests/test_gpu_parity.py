@@ -134,7 +134,7 @@ def test_gemv_full_config(enc, name, t, M, K, seed):
 # Shapes that exercise tails: M not a multiple of the rows per workgroup, a
 # single block per row, K not a multiple of 64 units.
 EDGE = [(Q8_0, 1, 32), (Q8_0, 3, 96), (Q8_0, 4099, 2080), (Q2_0, 5, 128), (Q2_0, 4097, 384),
-        (Q4_K, 1, 256), (Q4_K, 7, 768), (Q4_K, 4101, 2304), (Q4_K, 1000, 8192), (Q4_K, 13, 8448), (IQ2_XXS, 2, 256), (IQ2_XXS, 4103, 1280),
+        (Q4_K, 1, 256), (Q4_K, 7, 768), (Q4_K, 4101, 2304), (Q4_K, 1000, 8192), (Q4_K, 13, 8448), (IQ2_XXS, 2, 256), (IQ2_XXS, 4103, 1280), (IQ2_XXS, 301, 8192),
         (Q4_0, 1, 32), (Q4_0, 4099, 2080), (Q4_0, 2048, 4096), (IQ4_NL, 3, 96), (IQ4_NL, 4099, 2080),
         (IQ4_NL, 2048, 4096), (Q5_K, 1, 256), (Q5_K, 4101, 2304), (Q6_K, 3, 256), (Q6_K, 4099, 1280),
         (IQ4_XS, 2, 512), (IQ4_XS, 4103, 2304)] + \
