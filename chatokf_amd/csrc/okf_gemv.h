@@ -514,10 +514,10 @@ __device__ __forceinline__ void zero3(int (&s)[3][R][NC]) {
 
 // sum(q X) of a group from its digit sums: s2 2^16 + s1 2^8 + s0.  (s2 << 8)
 // + s1 is exact in int32 (|s2| <= 32 * 128 * 64 = 2^18, so it stays below
-// 2^27); its conversion to float is exact below 2^24 (every format whose
-// weight bytes stay within +-63, Q2_0 and the grid formats' small values
-// among them) and otherwise rounds once, and the fma rounds once: at most
-// two roundings of 2^-24 relative to the group's sum.
+// 2^27); its conversion to float is exact below 2^24 (weight bytes within
+// +-31: |s2| < 2^16; Q2_0, the 4-bit codes and IQ1's values among them) and
+// otherwise rounds once, and the fma rounds once: at most two roundings of
+// 2^-24 relative to the group's sum.
 template <int NC, int R>
 __device__ __forceinline__ float comb(const int (&s)[3][R][NC], int r, int n) {
     return fmaf((float)((s[2][r][n] << 8) + s[1][r][n]), 256.0f, (float)s[0][r][n]);
