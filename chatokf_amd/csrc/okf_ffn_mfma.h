@@ -125,7 +125,7 @@ __device__ __forceinline__ uint32_t fm_off(uint32_t q) { return 8 * q - (q == 3 
 // and take d from lane - 16, which loaded the block's first bytes.
 template <int NB, bool KS = false>
 __device__ __forceinline__ void fm_tile(const uint3 (&raw)[NB], bool q3, const uint8_t *abase, uint32_t ablk,
-                                        const int2 *gd, float &acc) {
+                                        const int2 *gd, float &acc, bool arow = true) {
 #pragma unroll
     for (int i = 0; i < NB; i++) {
         int32x4 c = {0, 0, 0, 0};
@@ -136,7 +136,8 @@ __device__ __forceinline__ void fm_tile(const uint3 (&raw)[NB], bool q3, const u
                                  : (q3 ? raw[i].y : __builtin_amdgcn_alignbyte(raw[i].y, raw[i].x, 2));
             const int32x4 b = {(int)(v & 0x03030303u), (int)((v >> 2) & 0x03030303u), (int)((v >> 4) & 0x03030303u),
                                (int)((v >> 6) & 0x03030303u)};
-            const int32x4 a = *(const int32x4 *)(abase + i * ablk + 16 * t);
+            // (arow false: an A row of zeros, from registers)
+            const int32x4 a = arow ? *(const int32x4 *)(abase + i * ablk + 16 * t) : int32x4{0, 0, 0, 0};
             c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
         }
         const int2 g = gd[i];
@@ -330,7 +331,16 @@ template <int NB, int NT, bool PAIR, bool SILU, int NW, bool KS = false>
 __global__ __launch_bounds__(NW * 64) void q2m_gemv_kernel(Q2mArgs a) {
     static_assert(!KS || (NT == 1 && !PAIR && NB % 2 == 0), "K split: one tile of one matrix");
     constexpr int NL = KS ? NB / 2 : NB;  // blocks a lane loads
-    constexpr uint32_t T = NW * 64, K = 128 * NB * NW, SR = (K / 8 + T - 1) / T;
+    // WL (with KS): each wavefront stages the x slots of its own K blocks (WS
+    // = 16 a block, in rounds of 64) and reads no other wavefront's planes,
+    // so no workgroup barrier sits between staging and compute (down 3.67
+    // -> 3.64 us, the SiLU down 4.45 -> 4.17; gate / up measured 4.14
+    // against 4.10 with it and gate alone 3.62 against 3.58, so they stage as
+    // one workgroup, rounds of T)
+    constexpr bool WL = KS;
+    constexpr uint32_t T = NW * 64, K = 128 * NB * NW, WS = 16 * NB, SN = WL ? 64 : T, SS = WL ? WS : K / 8,
+                       SR = (SS + SN - 1) / SN;
+    const uint32_t s0 = WL ? (threadIdx.x >> 6) * WS : 0, sl = WL ? (threadIdx.x & 63) : threadIdx.x;
     extern __shared__ u32x4 lds[];
     uint8_t *planes = (uint8_t *)lds;
     int2 *gd = (int2 *)(planes + 3 * K + 32);
@@ -342,7 +352,7 @@ __global__ __launch_bounds__(NW * 64) void q2m_gemv_kernel(Q2mArgs a) {
     float xv[SR][8], x2v[SR][8];
 #pragma unroll
     for (uint32_t k = 0; k < SR; k++) {
-        const uint32_t s = min(k * T + tid, K / 8 - 1);
+        const uint32_t s = s0 + min(k * SN + sl, SS - 1);
         load_slot<Q2_0>(a.x + (uint64_t)(s >> 3) * 64, s & 7, xv[k]);
         if constexpr (SILU) load_slot<Q2_0>(a.x2 + (uint64_t)(s >> 3) * 64, s & 7, x2v[k]);
     }
@@ -365,20 +375,31 @@ __global__ __launch_bounds__(NW * 64) void q2m_gemv_kernel(Q2mArgs a) {
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    if (tid < 8) ((uint32_t *)(planes + 3 * K))[tid] = 0;
+    // the 32 zero bytes of the A rows past the planes (with WL every
+    // wavefront writes them, the same values)
+    if ((WL ? lane : tid) < 8) ((uint32_t *)(planes + 3 * K))[WL ? lane : tid] = 0;
 #pragma unroll
     for (uint32_t k = 0; k < SR; k++)
-        if (k * T < K / 8) {  // (the whole workgroup)
+        if (k * SN < SS) {  // (the whole wavefront / workgroup: a block's 16 lanes reduce together)
             if constexpr (SILU)
 #pragma unroll
                 for (int j = 0; j < 8; j++) xv[k][j] = silu_mul1(xv[k][j], x2v[k][j]);
-            fm_stage_slot(xv[k], k * T + tid, k * T + tid < K / 8, planes, K, gd);
+            fm_stage_slot(xv[k], s0 + k * SN + sl, k * SN + sl < SS, planes, K, gd);
         }
-    __syncthreads();
+    if constexpr (WL) {
+        // the planes are this wavefront's own, and its LDS accesses
+        // complete in order
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+    } else {
+        __syncthreads();
+    }
 
     // A row ar: plane ar of the first K half (rows 0-2), with KS plane ar - 4
     // of the second (rows 4-6); the other rows read the zeros
     const uint32_t ar = col, ah = KS ? ar >> 2 : 0, ap = ar - 4 * ah;
+    // (zero rows as an LDS read like the planes': from registers, a
+    // divergent select, they measured 0.04-0.08 us slower)
     const bool arow = ap < 3 && ah < 2;
     const uint8_t *ab = arow ? planes + ap * K + (w * NB + ah * NL) * 128 + 32 * q : planes + 3 * K;
     const uint32_t ablk = arow ? 128 : 0;
