@@ -125,7 +125,7 @@ __device__ __forceinline__ uint32_t fm_off(uint32_t q) { return 8 * q - (q == 3 
 // and take d from lane - 16, which loaded the block's first bytes.
 template <int NB, bool KS = false>
 __device__ __forceinline__ void fm_tile(const uint3 (&raw)[NB], bool q3, const uint8_t *abase, uint32_t ablk,
-                                        const int2 *gd, float &acc, bool arow = true) {
+                                        const int2 *gd, float &acc) {
 #pragma unroll
     for (int i = 0; i < NB; i++) {
         int32x4 c = {0, 0, 0, 0};
@@ -136,8 +136,7 @@ __device__ __forceinline__ void fm_tile(const uint3 (&raw)[NB], bool q3, const u
                                  : (q3 ? raw[i].y : __builtin_amdgcn_alignbyte(raw[i].y, raw[i].x, 2));
             const int32x4 b = {(int)(v & 0x03030303u), (int)((v >> 2) & 0x03030303u), (int)((v >> 4) & 0x03030303u),
                                (int)((v >> 6) & 0x03030303u)};
-            // (arow false: an A row of zeros, from registers)
-            const int32x4 a = arow ? *(const int32x4 *)(abase + i * ablk + 16 * t) : int32x4{0, 0, 0, 0};
+            const int32x4 a = *(const int32x4 *)(abase + i * ablk + 16 * t);
             c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
         }
         const int2 g = gd[i];
