@@ -324,14 +324,29 @@ __global__ __launch_bounds__(T) void gemv_sb_kernel(GemvGroup g, uint64_t row_by
     __syncthreads();
     // row sums: four lanes per (row, column) add every fourth partial in
     // order, then the quad adds its four sums (fixed order: deterministic);
-    // the four lanes of a quad share q, so a quad is active as a whole
-    const uint32_t lane4 = tid & 3, pairs = rows * NC;
-    for (uint32_t q = tid >> 2; q < pairs; q += T >> 2) {
-        const uint32_t r = q / NC, n = q % NC;
-        float v = 0.0f;
-        for (uint32_t sb = lane4; sb < nsb; sb += 4) v += part[(r * nsb + sb) * NC + n];
-        v = quad_sum(v);
-        if (lane4 == 0) Y[(uint64_t)n * M + r0 + r] = v;
+    // the four lanes of a quad share q, so a quad is active as a whole.
+    // Long rows: sixteen lanes per row, every sixteenth partial, then a
+    // fixed butterfly over the sixteen (a shorter chain of dependent reads)
+    const uint32_t pairs = rows * NC;
+    if (nsb > 32 && pairs <= T / 16) {
+        const uint32_t l16 = tid & 15, q = tid >> 4;
+        if (q < pairs) {  // (whole groups of sixteen)
+            const uint32_t r = q / NC, n = q % NC;
+            float v = 0.0f;
+            for (uint32_t sb = l16; sb < nsb; sb += 16) v += part[(r * nsb + sb) * NC + n];
+#pragma unroll
+            for (int m = 1; m < 16; m <<= 1) v += __shfl_xor(v, m, 16);
+            if (l16 == 0) Y[(uint64_t)n * M + r0 + r] = v;
+        }
+    } else {
+        const uint32_t lane4 = tid & 3;
+        for (uint32_t q = tid >> 2; q < pairs; q += T >> 2) {
+            const uint32_t r = q / NC, n = q % NC;
+            float v = 0.0f;
+            for (uint32_t sb = lane4; sb < nsb; sb += 4) v += part[(r * nsb + sb) * NC + n];
+            v = quad_sum(v);
+            if (lane4 == 0) Y[(uint64_t)n * M + r0 + r] = v;
+        }
     }
 }
 
